@@ -1,0 +1,173 @@
+/*
+ * popkv_hip.h -- C ABI of the MI355X (gfx950) PopKV decode-time retrieval path.
+ *
+ * Plain C: device pointers, sizes and a stream handle (a hipStream_t passed as
+ * void*, NULL = the default stream).  No entry point allocates device memory
+ * or synchronizes with the host; every launch is asynchronous on `stream`.
+ * Callers that need scratch memory pass a workspace sized by the matching
+ * *_workspace_bytes() query.
+ *
+ * Every entry point returns POPKV_OK (0) or a negative status; the detail of
+ * the last failure on the calling thread is available from popkv_last_error().
+ *
+ * Layouts (row-major, element counts):
+ *   keys       [KVH, tokens, D]; rows of one head are contiguous (token stride
+ *              D), heads are key_head_stride elements apart.
+ *   k_sign/mag int32 [KVH, capacity, W], W = ceil(D/32); dim 32w+j is bit j.
+ *   k_low/delta fp16 bit patterns [KVH, capacity, R], R = ceil(D/G).
+ *   q_sign/mag int32 [B*QH, W];  q_low/delta float32 [B*QH, R].
+ *   scores     fp16 [B, QH, tokens] (D == 128) or float32 (other D).
+ *   indices    [QH, S] int64 or int32; an index equal to prefix_tokens names
+ *              the current (not yet cached) token.
+ *   partials   float32 [QH, ceil(S/split), D+2] = (m, l, acc[D]).
+ */
+#ifndef POPKV_HIP_H
+#define POPKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define POPKV_OK                0
+#define POPKV_ERR_INVALID      -1  /* bad argument: shape, dtype, group size, null pointer */
+#define POPKV_ERR_CAPACITY     -2  /* "Pop-KV cache capacity exceeded" */
+#define POPKV_ERR_TOKENS       -3  /* "invalid score token count" */
+#define POPKV_ERR_UNSUPPORTED  -4  /* valid, but outside what the kernels implement */
+#define POPKV_ERR_LAUNCH       -5  /* the HIP runtime rejected a launch */
+#define POPKV_ERR_WORKSPACE    -6  /* workspace pointer null or too small */
+
+/* ---- element types ----------------------------------------------------- */
+#define POPKV_DTYPE_F32   0
+#define POPKV_DTYPE_F16   1
+#define POPKV_DTYPE_BF16  2
+#define POPKV_INDEX_I64   0
+#define POPKV_INDEX_I32   1
+
+/* ---- query-encode summation order -------------------------------------- */
+#define POPKV_ENCODE_FOLD 0  /* left fold over ascending dims: decode path */
+#define POPKV_ENCODE_TREE 1  /* reduction-tree order: score() path, D == 128 */
+
+const char* popkv_status_string(int status);
+const char* popkv_last_error(void);
+const char* popkv_version(void);
+
+/* Key prepack and in-place append.  Encodes tokens [0, tokens) of `keys`
+ * into rows [token_offset, token_offset + tokens) of the packed cache, token
+ * groups of token_group_size (1..4096) counted from the first key, dimension
+ * groups of dim_group_size (16, 32, 64).  D <= 256.
+ * Replaces popkv_pack_cuda / popkv_pack_into_cuda / popkv_pack_dim_cuda /
+ * popkv_pack_into_dim_cuda (reference csrc/popkv_ext.cu:1058-1206, bound at
+ * csrc/popkv_ext.cpp:44-45, :48-49) and their kernels (popkv_ext.cu:79-143,
+ * :283-500). */
+int popkv_pack(const void* keys, int32_t dtype, int64_t kv_heads, int64_t tokens,
+               int64_t head_dim, int64_t key_head_stride,
+               int32_t* k_sign, int32_t* k_mag, void* k_low, void* k_delta,
+               int64_t capacity, int64_t token_offset,
+               int32_t token_group_size, int32_t dim_group_size, void* stream);
+
+/* Query encode: rows = B*QH rows of D values.  order POPKV_ENCODE_FOLD
+ * replaces popkv_query_encode_out_cuda (popkv_ext.cu:1315-1358, kernels
+ * :232-281, :911-957, bound at popkv_ext.cpp:47); POPKV_ENCODE_TREE is the
+ * warp encode the reference runs inside score() (popkv_ext.cu:677-755). */
+int popkv_query_encode(const void* queries, int32_t dtype, int64_t rows, int64_t head_dim,
+                       int32_t dim_group_size, int32_t order,
+                       int32_t* q_sign, int32_t* q_mag, float* q_low, float* q_delta,
+                       void* stream);
+
+/* Popcount scorer on a pre-encoded query, head_dim 128 only (W = 4).
+ * Query head qh of KV group j reads KV head head_to_kv[j * QH/KVH]; output is
+ * fp16 [B, QH, tokens], 0 < tokens <= capacity.
+ * Replaces popkv_score_encoded_cuda (popkv_ext.cu:1533-1593, kernel :757-876,
+ * bound at popkv_ext.cpp:51). */
+int popkv_score_encoded(const int32_t* q_sign, const int32_t* q_mag,
+                        const float* q_low, const float* q_delta,
+                        const int32_t* k_sign, const int32_t* k_mag,
+                        const void* k_low, const void* k_delta,
+                        const int64_t* head_to_kv, int64_t batch, int64_t q_heads,
+                        int64_t kv_heads, int64_t capacity, int64_t tokens,
+                        int32_t dim_group_size, void* scores, void* stream);
+
+/* Score from raw queries [B, QH, D]: D == 128 encodes in tree order and runs
+ * the GQA scorer (fp16 out); other D encode in fold order and run the generic
+ * per-head scorer (float32 out).  Needs popkv_score_workspace_bytes() bytes.
+ * Replaces popkv_score_cuda / popkv_score_dim_cuda (popkv_ext.cu:1208-1313,
+ * bound at popkv_ext.cpp:46, :50). */
+size_t popkv_score_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
+                                   int32_t dim_group_size);
+int popkv_score(const void* queries, int32_t dtype, int64_t batch, int64_t q_heads,
+                int64_t head_dim, const int32_t* k_sign, const int32_t* k_mag,
+                const void* k_low, const void* k_delta, const int64_t* head_to_kv,
+                int64_t kv_heads, int64_t capacity, int64_t tokens, int32_t dim_group_size,
+                void* scores, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Per-row top-k over fp16 scores: the k largest (PyTorch's fp16 radix order,
+ * -0 < +0, NaN largest), ties at the k-th value taken in ascending token
+ * order, written in ascending token order to indices[r, 0..k), and `current`
+ * written to indices[r, k].  0 <= k <= tokens.  tokens <= 131072 per row.
+ * Replaces torch.topk(scores, k, dim=-1, sorted=False).indices followed by
+ * _append_current (reference popkv.py:1094-1098, :287-291). */
+int popkv_topk_select(const void* scores, int64_t rows, int64_t row_stride, int64_t tokens,
+                      int64_t k, int64_t current, void* indices, int32_t index_dtype,
+                      int64_t index_row_stride, void* stream);
+
+/* Split sparse attention, partial pass: for query head h and split s, the
+ * online-softmax state of rows indices[h, s*split .. s*split+split) of
+ * prefix K/V head head_to_kv[h] (the current k/v where the index equals
+ * prefix_tokens; rows with valid_mask == 0 skipped).  D % 8 == 0, D <= 256,
+ * split_tokens a positive multiple of 16.  A head_to_kv entry outside
+ * [0, kv_heads) is clamped into range, and a row index outside
+ * [0, prefix_tokens] is clamped to the nearest cached row (the reference
+ * clamps with min(token, prefix_tokens - 1)), so no input can read out of
+ * bounds.
+ * Replaces indexed_attention_split_partial (reference sparse_kernels.py:
+ * 321-364, Triton kernel :237-294). */
+int popkv_sparse_attention_partial(const void* queries, int32_t dtype,
+                                   const void* prefix_k, const void* prefix_v,
+                                   int64_t k_head_stride, int64_t k_token_stride,
+                                   int64_t v_head_stride, int64_t v_token_stride,
+                                   int64_t prefix_tokens,
+                                   const void* current_k, const void* current_v,
+                                   const void* indices, int32_t index_dtype,
+                                   const uint8_t* valid_mask, const int64_t* head_to_kv,
+                                   int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t selected,
+                                   int32_t split_tokens, float* partials, void* stream);
+
+/* Log-sum-exp merge of split states into output [QH, D] of out_dtype.
+ * Replaces indexed_attention_split_merge (sparse_kernels.py:367-387,
+ * Triton kernel :297-318). */
+int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t splits,
+                                 int64_t head_dim, void* output, int32_t out_dtype,
+                                 void* stream);
+
+/* One decode step of one sparse layer (batch 1, head_dim 128): query encode,
+ * popcount score over `tokens` cached tokens, per-head top-k with
+ * k = min(budget-1, tokens) plus the current token (index `tokens`), and
+ * 256-token split sparse attention with an in-kernel log-sum-exp merge.
+ * queries/prefix/current K/V share `dtype`; output [QH, 128] has `dtype`.
+ * indices_out (int64 [QH, k+1]) may be NULL; when given, the selection is
+ * also written there.  Needs popkv_layer_step_workspace_bytes() bytes.
+ * Replaces the PopKV branch of LlamaSparseDecoder.decode (reference
+ * popkv.py:1076-1115): query_encode, score_encoded, torch.topk +
+ * _append_current, indexed_attention_split_partial and _merge. */
+size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t budget,
+                                        int32_t dim_group_size);
+int popkv_layer_step(const void* queries, int32_t dtype,
+                     const int32_t* k_sign, const int32_t* k_mag,
+                     const void* k_low, const void* k_delta, int64_t capacity,
+                     const void* prefix_k, const void* prefix_v,
+                     int64_t k_head_stride, int64_t v_head_stride,
+                     const void* current_k, const void* current_v,
+                     const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
+                     int64_t tokens, int64_t budget, int32_t dim_group_size,
+                     void* output, int64_t* indices_out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POPKV_HIP_H */

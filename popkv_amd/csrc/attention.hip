@@ -1,0 +1,389 @@
+// Split sparse attention over gathered K/V rows (gfx950).
+//
+// Replaces indexed_attention_split_partial / _merge (reference
+// sparse_kernels.py:237-387).  The step is a per-head GEMV in which every
+// query head picks its own rows, so it is bound by HBM bandwidth and uses no
+// MFMA.
+//
+// Partial kernel: one workgroup of 4 wave64s per (query head, split).  A row
+// of D bf16 values is read by LPR = D/8 lanes with one 16-byte load each, so
+// a wave covers 64/LPR rows per instruction.  Each lane first loads the
+// indices of its rows, then issues the K and V loads of a whole batch of rows
+// before using any of them (deep memory-level parallelism for the random
+// 256-byte gathers).  Logits are reduced across the LPR lanes of a row with
+// xor shuffles; every row slot keeps an online-softmax state (m, l, acc[8]),
+// slots are merged within the wave and then across waves through LDS, and
+// the split's (m, l, acc[D]) is written as float32.
+//
+// An index equal to prefix_tokens is the current token: its key/value come
+// from current_k/current_v (sparse_kernels.py:267-286).  Rows past `selected`
+// or with valid_mask == 0 are skipped.
+//
+// Merge: out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}, M = max_s m_s,
+// cast to the output dtype.  The layer-step variant fuses it into the partial
+// kernel: the last workgroup of a head to finish (device-scope counter)
+// merges that head's splits and re-arms the counter.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace popkv {
+namespace {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / kWave;
+
+template <typename T>
+__device__ __forceinline__ void load_row8(const T* p, int dim0, int d, float v[8]) {
+    if (dim0 + 8 <= d) {
+        load8<T>(p + dim0, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+}
+
+struct SoftmaxState {
+    float m, l, acc[8];
+};
+
+__device__ __forceinline__ void merge_state(SoftmaxState& a, float m2, float l2, const float* acc2) {
+    const float mm = fmaxf(a.m, m2);
+    if (mm == -INFINITY) return;
+    const float wa = a.m == -INFINITY ? 0.0f : __expf(a.m - mm);
+    const float wb = m2 == -INFINITY ? 0.0f : __expf(m2 - mm);
+    a.l = a.l * wa + l2 * wb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a.acc[i] = a.acc[i] * wa + acc2[i] * wb;
+    a.m = mm;
+}
+
+// Merge `nsplit` states [(m, l, acc[D])] into out[d] for d = threadIdx.x < D.
+template <typename T>
+__device__ __forceinline__ void merge_splits(const float* st, int nsplit, int d, T* out) {
+    const int dim = threadIdx.x;
+    if (dim >= d) return;
+    float mx = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, st[s * (d + 2)]);
+    float den = 0.0f, num = 0.0f;
+    for (int s = 0; s < nsplit; ++s) {
+        const float m = st[s * (d + 2)];
+        if (m == -INFINITY) continue;
+        const float w = __expf(m - mx);
+        den += st[s * (d + 2) + 1] * w;
+        num += st[s * (d + 2) + 2 + dim] * w;
+    }
+    Elem<T>::store(out, dim, num / den);
+}
+
+// Raw storage of 8 consecutive elements: one 16-byte packet for 16-bit types,
+// two for float32.  Rows stay packed in registers until they are consumed.
+template <typename T> struct Raw8 {
+    uint4 u;
+    __device__ __forceinline__ void load(const T* p) { u = *reinterpret_cast<const uint4*>(p); }
+    __device__ __forceinline__ void zero() { u = make_uint4(0u, 0u, 0u, 0u); }
+    __device__ __forceinline__ float get(int i) const {
+        const uint32_t w = i < 2 ? u.x : i < 4 ? u.y : i < 6 ? u.z : u.w;
+        const uint32_t h = (i & 1) ? (w >> 16) : (w & 0xffffu);
+        return Elem<T>::kDtype == POPKV_DTYPE_BF16 ? bits_bf16(h) : bits_f16(h);
+    }
+};
+template <> struct Raw8<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = reinterpret_cast<const float4*>(p)[0];
+        b = reinterpret_cast<const float4*>(p)[1];
+    }
+    __device__ __forceinline__ void zero() { a = make_float4(0.f, 0.f, 0.f, 0.f); b = a; }
+    __device__ __forceinline__ float get(int i) const {
+        const float4& x = i < 4 ? a : b;
+        const int j = i & 3;
+        return j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
+    }
+};
+
+template <typename T, typename IdxT, int LPR, int NB, bool FUSED>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
+    int64_t k_hs, int64_t k_ts, int64_t v_hs, int64_t v_ts, int64_t prefix_tokens,
+    const T* __restrict__ cur_k, const T* __restrict__ cur_v,
+    const IdxT* __restrict__ idx, int64_t idx_stride, const uint8_t* __restrict__ valid,
+    const int64_t* __restrict__ head_to_kv, int kv_heads, int d, int64_t selected, int split, float scale,
+    float* __restrict__ partials, int nsplit, unsigned int* __restrict__ counters, T* __restrict__ out) {
+    constexpr int SLOTS = kWave / LPR;               // row slots per wave
+    constexpr int ROWS_PER_PASS = SLOTS * kAttnWaves;
+    const int h = blockIdx.y;
+    const int s = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int sub = lane % LPR;                       // dim slice [8*sub, 8*sub+8)
+    const int slot = wave * SLOTS + lane / LPR;
+    const int dim0 = sub * 8;
+    const bool dim_ok = dim0 + 8 <= d;
+    // A mapping outside [0, kv_heads) is clamped, never dereferenced.
+    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+
+    float qv[8];
+    load_row8<T>(q + static_cast<int64_t>(h) * d, dim0, d, qv);
+    const T* kbase = kc + kvh * k_hs;
+    const T* vbase = vc + kvh * v_hs;
+    const T* ck = cur_k + kvh * d;
+    const T* cv = cur_v + kvh * d;
+
+    const int64_t row0 = static_cast<int64_t>(s) * split;
+    const int64_t rows_here = min(static_cast<int64_t>(split), selected - row0);
+    const IdxT* irow = idx + static_cast<int64_t>(h) * idx_stride + row0;
+    const uint8_t* vrow = valid ? valid + static_cast<int64_t>(h) * idx_stride + row0 : nullptr;
+
+    SoftmaxState st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = 0.0f;
+
+    for (int64_t base = 0; base < rows_here; base += static_cast<int64_t>(ROWS_PER_PASS) * NB) {
+        int64_t tok[NB];
+        bool live[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int64_t r = base + static_cast<int64_t>(b) * ROWS_PER_PASS + slot;
+            live[b] = r < rows_here && (vrow == nullptr || vrow[r] != 0);
+            const int64_t t = live[b] ? static_cast<int64_t>(irow[r]) : 0;
+            // Out-of-range indices are clamped into the cache (as the
+            // reference's min(token, prefix_tokens - 1)), never dereferenced.
+            tok[b] = t == prefix_tokens ? t : min(max(t, static_cast<int64_t>(0)), prefix_tokens - 1);
+        }
+        Raw8<T> kr[NB], vr[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const bool is_cur = tok[b] == prefix_tokens;
+            if (live[b] && dim_ok) {
+                kr[b].load((is_cur ? ck : kbase + tok[b] * k_ts) + dim0);
+                vr[b].load((is_cur ? cv : vbase + tok[b] * v_ts) + dim0);
+            } else {
+                kr[b].zero();
+                vr[b].zero();
+            }
+        }
+        float logit[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dot = fmaf(qv[i], kr[b].get(i), dot);
+#pragma unroll
+            for (int m = 1; m < LPR; m <<= 1) dot += __shfl_xor(dot, m);
+            logit[b] = live[b] ? dot * scale : -INFINITY;
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) bm = fmaxf(bm, logit[b]);
+        const float mnew = fmaxf(st.m, bm);
+        if (mnew != -INFINITY) {
+            const float alpha = st.m == -INFINITY ? 0.0f : __expf(st.m - mnew);
+            st.l *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float p = live[b] ? __expf(logit[b] - mnew) : 0.0f;
+                st.l += p;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) st.acc[i] = fmaf(p, vr[b].get(i), st.acc[i]);
+            }
+            st.m = mnew;
+        }
+    }
+
+    // Merge the row slots of this wave (lanes with equal `sub`).
+#pragma unroll
+    for (int m = LPR; m < kWave; m <<= 1) {
+        const float m2 = __shfl_xor(st.m, m);
+        const float l2 = __shfl_xor(st.l, m);
+        float a2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a2[i] = __shfl_xor(st.acc[i], m);
+        merge_state(st, m2, l2, a2);
+    }
+
+    // Merge across waves through LDS.
+    __shared__ float s_m[kAttnWaves], s_l[kAttnWaves];
+    __shared__ float s_acc[kAttnWaves][256];
+    if (lane < LPR) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_acc[wave][dim0 + i] = st.acc[i];
+        if (lane == 0) { s_m[wave] = st.m; s_l[wave] = st.l; }
+    }
+    __syncthreads();
+    float* dst = partials + (static_cast<int64_t>(h) * nsplit + s) * (d + 2);
+    {
+        const int dim = threadIdx.x;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, s_m[w]);
+        float l = 0.0f, a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            if (s_m[w] == -INFINITY) continue;
+            const float wt = __expf(s_m[w] - mx);
+            l += s_l[w] * wt;
+            if (dim < d) a += s_acc[w][dim] * wt;
+        }
+        if (dim < d) dst[2 + dim] = a;
+        if (dim == 0) { dst[0] = mx; dst[1] = l; }
+    }
+
+    if constexpr (FUSED) {
+        __shared__ unsigned int s_last;
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const unsigned int prev = atomicAdd(&counters[h], 1u);
+            s_last = prev == static_cast<unsigned int>(nsplit - 1) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (s_last) {
+            __threadfence();
+            merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (d + 2), nsplit, d,
+                            out + static_cast<int64_t>(h) * d);
+            if (threadIdx.x == 0) counters[h] = 0u;
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ partials, int nsplit, int d,
+                                                         T* __restrict__ out) {
+    const int h = blockIdx.x;
+    merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (d + 2), nsplit, d,
+                    out + static_cast<int64_t>(h) * d);
+}
+
+__global__ void zero_u32_kernel(unsigned int* p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+template <typename T, typename IdxT, int LPR, bool FUSED>
+hipError_t launch_partial_t(const T* q, const T* kc, const T* vc, int64_t k_hs, int64_t k_ts, int64_t v_hs,
+                            int64_t v_ts, int64_t prefix_tokens, const T* ck, const T* cv, const IdxT* idx,
+                            int64_t idx_stride, const uint8_t* valid, const int64_t* h2k, int qh, int kvh, int d,
+                            int64_t selected, int split, float* partials, unsigned int* counters, T* out,
+                            hipStream_t stream) {
+    const int nsplit = static_cast<int>((selected + split - 1) / split);
+    const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(d)));
+    constexpr int NB = (sizeof(T) == 4 || LPR == 32) ? 8 : 16;
+    dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(qh));
+    hipLaunchKernelGGL((attn_partial_kernel<T, IdxT, LPR, NB, FUSED>), grid, dim3(kAttnThreads), 0, stream, q, kc,
+                       vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx, idx_stride, valid, h2k, kvh, d, selected,
+                       split, scale, partials, nsplit, counters, out);
+    return hipGetLastError();
+}
+
+template <typename T, typename IdxT, bool FUSED>
+hipError_t launch_partial_lpr(const T* q, const T* kc, const T* vc, int64_t k_hs, int64_t k_ts, int64_t v_hs,
+                              int64_t v_ts, int64_t prefix_tokens, const T* ck, const T* cv, const IdxT* idx,
+                              int64_t idx_stride, const uint8_t* valid, const int64_t* h2k, int qh, int kvh, int d,
+                              int64_t selected, int split, float* partials, unsigned int* counters, T* out,
+                              hipStream_t stream) {
+    if (d <= 64)
+        return launch_partial_t<T, IdxT, 8, FUSED>(q, kc, vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx,
+                                                   idx_stride, valid, h2k, qh, kvh, d, selected, split, partials, counters,
+                                                   out, stream);
+    if (d <= 128)
+        return launch_partial_t<T, IdxT, 16, FUSED>(q, kc, vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx,
+                                                    idx_stride, valid, h2k, qh, kvh, d, selected, split, partials,
+                                                    counters, out, stream);
+    return launch_partial_t<T, IdxT, 32, FUSED>(q, kc, vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx,
+                                                idx_stride, valid, h2k, qh, kvh, d, selected, split, partials, counters,
+                                                out, stream);
+}
+
+template <typename T>
+hipError_t launch_partial_dt(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t k_ts, int64_t v_hs,
+                             int64_t v_ts, int64_t prefix_tokens, const void* ck, const void* cv, const void* idx,
+                             int index_dtype, int64_t idx_stride, const uint8_t* valid, const int64_t* h2k, int qh,
+                             int kvh, int d, int64_t selected, int split, float* partials, unsigned int* counters, void* out,
+                             hipStream_t stream) {
+    const T* q_ = static_cast<const T*>(q);
+    const T* k_ = static_cast<const T*>(kc);
+    const T* v_ = static_cast<const T*>(vc);
+    const T* ck_ = static_cast<const T*>(ck);
+    const T* cv_ = static_cast<const T*>(cv);
+    T* o_ = static_cast<T*>(out);
+    if (counters != nullptr) {
+        if (index_dtype == POPKV_INDEX_I32)
+            return launch_partial_lpr<T, int32_t, true>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
+                                                         static_cast<const int32_t*>(idx), idx_stride, valid, h2k, qh, kvh,
+                                                         d, selected, split, partials, counters, o_, stream);
+        return launch_partial_lpr<T, int64_t, true>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
+                                                     static_cast<const int64_t*>(idx), idx_stride, valid, h2k, qh, kvh, d,
+                                                     selected, split, partials, counters, o_, stream);
+    }
+    if (index_dtype == POPKV_INDEX_I32)
+        return launch_partial_lpr<T, int32_t, false>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
+                                                      static_cast<const int32_t*>(idx), idx_stride, valid, h2k, qh, kvh, d,
+                                                      selected, split, partials, nullptr, o_, stream);
+    return launch_partial_lpr<T, int64_t, false>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
+                                                  static_cast<const int64_t*>(idx), idx_stride, valid, h2k, qh, kvh, d,
+                                                  selected, split, partials, nullptr, o_, stream);
+}
+
+}  // namespace
+
+hipError_t launch_attention_partial(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                    int64_t k_head_stride, int64_t k_token_stride, int64_t v_head_stride,
+                                    int64_t v_token_stride, int64_t prefix_tokens, const void* current_k,
+                                    const void* current_v, const void* indices, int index_dtype,
+                                    int64_t index_row_stride, const uint8_t* valid_mask, const int64_t* head_to_kv,
+                                    int q_heads, int kv_heads, int head_dim, int64_t selected, int split_tokens,
+                                    float* partials,
+                                    unsigned int* merge_counters, void* merge_output, hipStream_t stream) {
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_partial_dt<float>(queries, prefix_k, prefix_v, k_head_stride, k_token_stride, v_head_stride,
+                                            v_token_stride, prefix_tokens, current_k, current_v, indices, index_dtype,
+                                            index_row_stride, valid_mask, head_to_kv, q_heads, kv_heads, head_dim, selected,
+                                            split_tokens, partials, merge_counters, merge_output, stream);
+        case POPKV_DTYPE_F16:
+            return launch_partial_dt<f16_t>(queries, prefix_k, prefix_v, k_head_stride, k_token_stride, v_head_stride,
+                                            v_token_stride, prefix_tokens, current_k, current_v, indices, index_dtype,
+                                            index_row_stride, valid_mask, head_to_kv, q_heads, kv_heads, head_dim, selected,
+                                            split_tokens, partials, merge_counters, merge_output, stream);
+        default:
+            return launch_partial_dt<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, k_token_stride,
+                                             v_head_stride, v_token_stride, prefix_tokens, current_k, current_v,
+                                             indices, index_dtype, index_row_stride, valid_mask, head_to_kv, q_heads,
+                                             kv_heads, head_dim, selected, split_tokens, partials, merge_counters,
+                                             merge_output,
+                                             stream);
+    }
+}
+
+hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t splits, int head_dim, void* output,
+                                  int out_dtype, hipStream_t stream) {
+    dim3 grid(static_cast<unsigned>(q_heads)), block(256);
+    const int ns = static_cast<int>(splits);
+    switch (out_dtype) {
+        case POPKV_DTYPE_F32:
+            hipLaunchKernelGGL((attn_merge_kernel<float>), grid, block, 0, stream, partials, ns, head_dim,
+                               static_cast<float*>(output));
+            break;
+        case POPKV_DTYPE_F16:
+            hipLaunchKernelGGL((attn_merge_kernel<f16_t>), grid, block, 0, stream, partials, ns, head_dim,
+                               static_cast<f16_t*>(output));
+            break;
+        default:
+            hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), grid, block, 0, stream, partials, ns, head_dim,
+                               static_cast<bf16_t*>(output));
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_u32(unsigned int* p, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, p, n);
+    return hipGetLastError();
+}
+
+}  // namespace popkv

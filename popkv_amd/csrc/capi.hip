@@ -1,0 +1,341 @@
+// extern "C" entry points of libpopkv_hip.so (declared in include/popkv_hip.h).
+//
+// Each entry point validates its arguments on the host, records a readable
+// message for popkv_last_error() on failure, and launches asynchronously on
+// the caller's stream.  Nothing here allocates device memory or synchronizes.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "kernels.h"
+#include "popkv_hip.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int launched(hipError_t err, const char* what) {
+    if (err != hipSuccess) return fail(POPKV_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err));
+    return POPKV_OK;
+}
+
+bool valid_dtype(int32_t dt) {
+    return dt == POPKV_DTYPE_F32 || dt == POPKV_DTYPE_F16 || dt == POPKV_DTYPE_BF16;
+}
+bool valid_group(int32_t g) { return g == 16 || g == 32 || g == 64; }
+size_t elem_size(int32_t dt) { return dt == POPKV_DTYPE_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+constexpr int64_t kMaxSelectTokens = 1024 * 128;
+constexpr int kLayerSplit = 256;
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Workspace layout of popkv_layer_step (batch 1, head_dim 128).
+struct StepLayout {
+    size_t q_sign, q_mag, q_low, q_delta, scores, indices, partials, counters, total;
+    int64_t score_stride, k, nsplit;
+};
+
+StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget, int32_t g) {
+    StepLayout L{};
+    const int64_t reps = 128 / g;
+    L.k = budget - 1 < tokens ? budget - 1 : tokens;
+    L.nsplit = ceil_div(L.k + 1, kLayerSplit);
+    L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 64) * 64;
+    size_t off = 0;
+    L.q_sign = off; off = align_up(off + qh * 4 * 4);
+    L.q_mag = off; off = align_up(off + qh * 4 * 4);
+    L.q_low = off; off = align_up(off + qh * reps * 4);
+    L.q_delta = off; off = align_up(off + qh * reps * 4);
+    L.scores = off; off = align_up(off + static_cast<size_t>(qh * L.score_stride) * 2);
+    L.indices = off; off = align_up(off + static_cast<size_t>(qh * (L.k + 1)) * 4);
+    L.partials = off; off = align_up(off + static_cast<size_t>(qh * L.nsplit * (128 + 2)) * 4);
+    L.counters = off; off = align_up(off + qh * 4);
+    L.total = off;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* popkv_status_string(int status) {
+    switch (status) {
+        case POPKV_OK: return "ok";
+        case POPKV_ERR_INVALID: return "invalid argument";
+        case POPKV_ERR_CAPACITY: return "Pop-KV cache capacity exceeded";
+        case POPKV_ERR_TOKENS: return "invalid score token count";
+        case POPKV_ERR_UNSUPPORTED: return "unsupported shape";
+        case POPKV_ERR_LAUNCH: return "kernel launch failed";
+        case POPKV_ERR_WORKSPACE: return "workspace too small";
+        default: return "unknown status";
+    }
+}
+
+const char* popkv_last_error(void) { return g_last_error; }
+
+const char* popkv_version(void) { return "popkv-hip 0.1 gfx950"; }
+
+int popkv_pack(const void* keys, int32_t dtype, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+               int64_t key_head_stride, int32_t* k_sign, int32_t* k_mag, void* k_low, void* k_delta,
+               int64_t capacity, int64_t token_offset, int32_t token_group_size, int32_t dim_group_size,
+               void* stream) {
+    if (!keys || !k_sign || !k_mag || !k_low || !k_delta) return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "keys must be fp32/fp16/bf16");
+    if (kv_heads <= 0 || kv_heads > 65535 || tokens < 0 || head_dim <= 0)
+        return fail(POPKV_ERR_INVALID, "keys must be [KVH, tokens, head dim]");
+    if (head_dim > 256) return fail(POPKV_ERR_UNSUPPORTED, "head_dim must be <= 256");
+    if (key_head_stride < tokens * head_dim) return fail(POPKV_ERR_INVALID, "key head stride too small");
+    if (token_group_size < 1 || token_group_size > 4096)
+        return fail(POPKV_ERR_INVALID, "token_group_size must be between 1 and 4096");
+    if (!valid_group(dim_group_size)) return fail(POPKV_ERR_INVALID, "dim_group_size must be 16, 32, or 64");
+    if (token_offset < 0 || token_offset + tokens > capacity)
+        return fail(POPKV_ERR_CAPACITY, "Pop-KV cache capacity exceeded");
+    return launched(popkv::launch_pack(keys, dtype, kv_heads, tokens, static_cast<int>(head_dim), key_head_stride,
+                                       k_sign, k_mag, static_cast<uint16_t*>(k_low), static_cast<uint16_t*>(k_delta),
+                                       capacity, token_offset, token_group_size, dim_group_size, as_stream(stream)),
+                    "popkv_pack");
+}
+
+int popkv_query_encode(const void* queries, int32_t dtype, int64_t rows, int64_t head_dim, int32_t dim_group_size,
+                       int32_t order, int32_t* q_sign, int32_t* q_mag, float* q_low, float* q_delta, void* stream) {
+    if (!queries || !q_sign || !q_mag || !q_low || !q_delta) return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "queries must be fp32/fp16/bf16");
+    if (rows < 0 || head_dim <= 0) return fail(POPKV_ERR_INVALID, "queries must be [rows, non-empty head dim]");
+    if (head_dim > 256) return fail(POPKV_ERR_UNSUPPORTED, "head_dim must be <= 256");
+    if (rows > 0x7fffffff) return fail(POPKV_ERR_UNSUPPORTED, "too many query rows");
+    if (!valid_group(dim_group_size)) return fail(POPKV_ERR_INVALID, "dim_group_size must be 16, 32, or 64");
+    if (order != POPKV_ENCODE_FOLD && order != POPKV_ENCODE_TREE)
+        return fail(POPKV_ERR_INVALID, "order must be POPKV_ENCODE_FOLD or POPKV_ENCODE_TREE");
+    return launched(popkv::launch_query_encode(queries, dtype, rows, static_cast<int>(head_dim), dim_group_size,
+                                               order, q_sign, q_mag, q_low, q_delta, as_stream(stream)),
+                    "popkv_query_encode");
+}
+
+static int check_score_common(const int64_t* head_to_kv, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                              int64_t capacity, int64_t tokens, int32_t g) {
+    if (!head_to_kv) return fail(POPKV_ERR_INVALID, "null head mapping");
+    if (!valid_group(g)) return fail(POPKV_ERR_INVALID, "dim_group_size must be 16, 32, or 64");
+    if (batch <= 0 || q_heads <= 0 || kv_heads <= 0) return fail(POPKV_ERR_INVALID, "empty batch or heads");
+    if (tokens <= 0 || tokens > capacity) return fail(POPKV_ERR_TOKENS, "invalid score token count");
+    if (q_heads % kv_heads != 0) return fail(POPKV_ERR_INVALID, "GQA query heads must be divisible by KV heads");
+    if (batch * q_heads > 65535 || batch * kv_heads > 65535) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
+    return POPKV_OK;
+}
+
+int popkv_score_encoded(const int32_t* q_sign, const int32_t* q_mag, const float* q_low, const float* q_delta,
+                        const int32_t* k_sign, const int32_t* k_mag, const void* k_low, const void* k_delta,
+                        const int64_t* head_to_kv, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                        int64_t tokens, int32_t dim_group_size, void* scores, void* stream) {
+    if (!q_sign || !q_mag || !q_low || !q_delta || !k_sign || !k_mag || !k_low || !k_delta || !scores)
+        return fail(POPKV_ERR_INVALID, "null pointer");
+    int st = check_score_common(head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size);
+    if (st) return st;
+    if (!aligned16(k_sign) || !aligned16(k_mag) || !aligned16(k_low) || !aligned16(k_delta))
+        return fail(POPKV_ERR_INVALID, "packed cache tensors must be 16-byte aligned");
+    return launched(popkv::launch_score_d128(q_sign, q_mag, q_low, q_delta, k_sign, k_mag,
+                                             static_cast<const uint16_t*>(k_low),
+                                             static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
+                                             static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity, tokens,
+                                             dim_group_size, static_cast<uint16_t*>(scores), tokens, as_stream(stream)),
+                    "popkv_score_encoded");
+}
+
+size_t popkv_score_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int32_t dim_group_size) {
+    if (batch <= 0 || q_heads <= 0 || head_dim <= 0 || !valid_group(dim_group_size)) return 0;
+    const int64_t rows = batch * q_heads;
+    const int64_t w = ceil_div(head_dim, 32), r = ceil_div(head_dim, dim_group_size);
+    return align_up(rows * w * 4) * 2 + align_up(rows * r * 4) * 2;
+}
+
+int popkv_score(const void* queries, int32_t dtype, int64_t batch, int64_t q_heads, int64_t head_dim,
+                const int32_t* k_sign, const int32_t* k_mag, const void* k_low, const void* k_delta,
+                const int64_t* head_to_kv, int64_t kv_heads, int64_t capacity, int64_t tokens, int32_t dim_group_size,
+                void* scores, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!queries || !k_sign || !k_mag || !k_low || !k_delta || !scores) return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "queries must be fp32/fp16/bf16");
+    if (head_dim <= 0) return fail(POPKV_ERR_INVALID, "empty head dim");
+    if (head_dim > 256) return fail(POPKV_ERR_UNSUPPORTED, "head_dim must be <= 256");
+    int st = check_score_common(head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size);
+    if (st) return st;
+    const size_t need = popkv_score_workspace_bytes(batch, q_heads, head_dim, dim_group_size);
+    if (!workspace || workspace_bytes < need) return fail(POPKV_ERR_WORKSPACE, "score needs %zu workspace bytes", need);
+    const int64_t rows = batch * q_heads;
+    const int64_t w = ceil_div(head_dim, 32), r = ceil_div(head_dim, dim_group_size);
+    char* ws = static_cast<char*>(workspace);
+    int32_t* qs = reinterpret_cast<int32_t*>(ws);
+    int32_t* qm = reinterpret_cast<int32_t*>(ws + align_up(rows * w * 4));
+    float* ql = reinterpret_cast<float*>(ws + 2 * align_up(rows * w * 4));
+    float* qd = reinterpret_cast<float*>(ws + 2 * align_up(rows * w * 4) + align_up(rows * r * 4));
+    const bool d128 = head_dim == 128;
+    st = launched(popkv::launch_query_encode(queries, dtype, rows, static_cast<int>(head_dim), dim_group_size,
+                                             d128 ? POPKV_ENCODE_TREE : POPKV_ENCODE_FOLD, qs, qm, ql, qd,
+                                             as_stream(stream)),
+                  "popkv_score(encode)");
+    if (st) return st;
+    if (d128) {
+        if (!aligned16(k_sign) || !aligned16(k_mag) || !aligned16(k_low) || !aligned16(k_delta))
+            return fail(POPKV_ERR_INVALID, "packed cache tensors must be 16-byte aligned");
+        return launched(popkv::launch_score_d128(qs, qm, ql, qd, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
+                                                 static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
+                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
+                                                 tokens, dim_group_size, static_cast<uint16_t*>(scores), tokens,
+                                                 as_stream(stream)),
+                        "popkv_score");
+    }
+    return launched(popkv::launch_score_generic(qs, qm, ql, qd, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
+                                                static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
+                                                static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                                                static_cast<int>(head_dim), capacity,
+                                                tokens, dim_group_size, static_cast<float*>(scores), as_stream(stream)),
+                    "popkv_score");
+}
+
+int popkv_topk_select(const void* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
+                      int64_t current, void* indices, int32_t index_dtype, int64_t index_row_stride, void* stream) {
+    if (!scores || !indices) return fail(POPKV_ERR_INVALID, "null pointer");
+    if (rows < 0 || tokens < 0 || row_stride < tokens) return fail(POPKV_ERR_INVALID, "bad score shape");
+    if (k < 0 || k > tokens) return fail(POPKV_ERR_INVALID, "k must satisfy 0 <= k <= tokens");
+    if (index_row_stride < k + 1) return fail(POPKV_ERR_INVALID, "index row stride too small");
+    if (index_dtype != POPKV_INDEX_I64 && index_dtype != POPKV_INDEX_I32)
+        return fail(POPKV_ERR_INVALID, "index dtype must be int64 or int32");
+    if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens per row");
+    if (rows > 0x7fffffff) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
+    return launched(popkv::launch_topk_select(static_cast<const uint16_t*>(scores), rows, row_stride, tokens, k,
+                                              current, indices, index_dtype, index_row_stride, nullptr,
+                                              as_stream(stream)),
+                    "popkv_topk_select");
+}
+
+static int check_attention_common(int32_t dtype, int64_t q_heads, int64_t head_dim) {
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "attention tensors must be fp32/fp16/bf16");
+    if (q_heads <= 0 || q_heads > 65535) return fail(POPKV_ERR_INVALID, "bad query head count");
+    if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256)
+        return fail(POPKV_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 and <= 256");
+    return POPKV_OK;
+}
+
+int popkv_sparse_attention_partial(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
+                                   int64_t k_head_stride, int64_t k_token_stride, int64_t v_head_stride,
+                                   int64_t v_token_stride, int64_t prefix_tokens, const void* current_k,
+                                   const void* current_v, const void* indices, int32_t index_dtype,
+                                   const uint8_t* valid_mask, const int64_t* head_to_kv, int64_t q_heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t selected, int32_t split_tokens,
+                                   float* partials, void* stream) {
+    if (!queries || !prefix_k || !prefix_v || !current_k || !current_v || !indices || !head_to_kv || !partials)
+        return fail(POPKV_ERR_INVALID, "null pointer");
+    int st = check_attention_common(dtype, q_heads, head_dim);
+    if (st) return st;
+    if (kv_heads <= 0) return fail(POPKV_ERR_INVALID, "bad KV head count");
+    if (prefix_tokens <= 0 || selected <= 0)
+        return fail(POPKV_ERR_INVALID, "indexed attention requires non-empty prefix and selection");
+    if (split_tokens <= 0 || split_tokens % 16) return fail(POPKV_ERR_INVALID, "split_tokens must be a positive multiple of 16");
+    if (index_dtype != POPKV_INDEX_I64 && index_dtype != POPKV_INDEX_I32)
+        return fail(POPKV_ERR_INVALID, "index dtype must be int64 or int32");
+    if (ceil_div(selected, split_tokens) > 65535) return fail(POPKV_ERR_UNSUPPORTED, "too many splits");
+    const size_t es = elem_size(dtype);
+    if (!aligned16(queries) || !aligned16(prefix_k) || !aligned16(prefix_v) || !aligned16(current_k) ||
+        !aligned16(current_v) || (k_head_stride * es) % 16 || (k_token_stride * es) % 16 ||
+        (v_head_stride * es) % 16 || (v_token_stride * es) % 16)
+        return fail(POPKV_ERR_UNSUPPORTED, "attention tensors need 16-byte aligned rows");
+    if (k_token_stride < head_dim || v_token_stride < head_dim) return fail(POPKV_ERR_INVALID, "token stride < head_dim");
+    return launched(popkv::launch_attention_partial(queries, dtype, prefix_k, prefix_v, k_head_stride, k_token_stride,
+                                                    v_head_stride, v_token_stride, prefix_tokens, current_k, current_v,
+                                                    indices, index_dtype, selected, valid_mask, head_to_kv,
+                                                    static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                                                    static_cast<int>(head_dim), selected,
+                                                    split_tokens, partials, nullptr, nullptr, as_stream(stream)),
+                    "popkv_sparse_attention_partial");
+}
+
+int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t splits, int64_t head_dim,
+                                 void* output, int32_t out_dtype, void* stream) {
+    if (!partials || !output) return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(out_dtype)) return fail(POPKV_ERR_INVALID, "output must be fp32/fp16/bf16");
+    if (q_heads <= 0 || q_heads > 65535 || splits <= 0 || head_dim <= 0)
+        return fail(POPKV_ERR_INVALID, "partials must be [QH, splits, D+2]");
+    if (head_dim > 256) return fail(POPKV_ERR_UNSUPPORTED, "head_dim must be <= 256");
+    return launched(popkv::launch_attention_merge(partials, static_cast<int>(q_heads), splits,
+                                                  static_cast<int>(head_dim), output, out_dtype, as_stream(stream)),
+                    "popkv_sparse_attention_merge");
+}
+
+size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t budget, int32_t dim_group_size) {
+    if (q_heads <= 0 || tokens < 0 || budget <= 1 || !valid_group(dim_group_size)) return 0;
+    return step_layout(q_heads, tokens, budget, dim_group_size).total;
+}
+
+int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                     const void* k_low, const void* k_delta, int64_t capacity, const void* prefix_k,
+                     const void* prefix_v, int64_t k_head_stride, int64_t v_head_stride, const void* current_k,
+                     const void* current_v, const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
+                     int64_t tokens, int64_t budget, int32_t dim_group_size, void* output, int64_t* indices_out,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+    if (!queries || !k_sign || !k_mag || !k_low || !k_delta || !prefix_k || !prefix_v || !current_k || !current_v ||
+        !head_to_kv || !output)
+        return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "tensors must be fp32/fp16/bf16");
+    if (budget <= 1) return fail(POPKV_ERR_INVALID, "budget must reserve at least one retrieved and one current token");
+    int st = check_score_common(head_to_kv, 1, q_heads, kv_heads, capacity, tokens, dim_group_size);
+    if (st) return st;
+    if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens");
+    const StepLayout L = step_layout(q_heads, tokens, budget, dim_group_size);
+    if (!workspace || workspace_bytes < L.total)
+        return fail(POPKV_ERR_WORKSPACE, "layer step needs %zu workspace bytes", L.total);
+    if (!aligned16(workspace)) return fail(POPKV_ERR_INVALID, "workspace must be 16-byte aligned");
+    const size_t es = elem_size(dtype);
+    if (!aligned16(k_sign) || !aligned16(k_mag) || !aligned16(k_low) || !aligned16(k_delta) || !aligned16(queries) ||
+        !aligned16(prefix_k) || !aligned16(prefix_v) || !aligned16(current_k) || !aligned16(current_v) ||
+        (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
+        return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
+    char* ws = static_cast<char*>(workspace);
+    int32_t* qs = reinterpret_cast<int32_t*>(ws + L.q_sign);
+    int32_t* qm = reinterpret_cast<int32_t*>(ws + L.q_mag);
+    float* ql = reinterpret_cast<float*>(ws + L.q_low);
+    float* qd = reinterpret_cast<float*>(ws + L.q_delta);
+    uint16_t* scores = reinterpret_cast<uint16_t*>(ws + L.scores);
+    float* partials = reinterpret_cast<float*>(ws + L.partials);
+    unsigned int* counters = reinterpret_cast<unsigned int*>(ws + L.counters);
+    void* idx = indices_out ? static_cast<void*>(indices_out) : static_cast<void*>(ws + L.indices);
+    const int idx_dtype = indices_out ? POPKV_INDEX_I64 : POPKV_INDEX_I32;
+    hipStream_t s = as_stream(stream);
+
+    st = launched(popkv::launch_query_encode(queries, dtype, q_heads, 128, dim_group_size, POPKV_ENCODE_FOLD, qs, qm,
+                                             ql, qd, s),
+                  "popkv_layer_step(encode)");
+    if (st) return st;
+    // Score rows use a padded stride (a multiple of 64 tokens) so every row
+    // starts 128-byte aligned for the select kernel's loads.
+    st = launched(popkv::launch_score_d128(qs, qm, ql, qd, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
+                                           static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
+                                           static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity, tokens,
+                                           dim_group_size, scores, L.score_stride, s),
+                  "popkv_layer_step(score)");
+    if (st) return st;
+    st = launched(popkv::launch_topk_select(scores, q_heads, L.score_stride, tokens, L.k, tokens, idx, idx_dtype,
+                                            L.k + 1, counters, s),
+                  "popkv_layer_step(select)");
+    if (st) return st;
+    return launched(popkv::launch_attention_partial(queries, dtype, prefix_k, prefix_v, k_head_stride, 128,
+                                                    v_head_stride, 128, tokens, current_k, current_v, idx, idx_dtype,
+                                                    L.k + 1, nullptr, head_to_kv, static_cast<int>(q_heads),
+                                                    static_cast<int>(kv_heads), 128,
+                                                    L.k + 1, kLayerSplit, partials, counters, output, s),
+                    "popkv_layer_step(attention)");
+}
+
+}  // extern "C"

@@ -1,0 +1,174 @@
+// Shared device helpers for the gfx950 PopKV kernels (wave64, CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "popkv_hip.h"
+
+namespace popkv {
+
+constexpr int kWave = 64;
+
+// ---- element loads -------------------------------------------------------
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__device__ __forceinline__ float bits_bf16(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float bits_f16(uint32_t b) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(b)));
+}
+// fp16 round-to-nearest-even of an already-rounded float32 value
+// (v_cvt_f16_f32 under the default round mode).  The empty asm pins `x` as a
+// materialized float32: without it the backend fuses a producing multiply
+// and this conversion into one v_fma_mixlo_f16, which rounds the exact
+// product once to fp16 instead of rounding to fp32 first, and differs in the
+// last fp16 bit whenever the fp32 product lands on an fp16 tie.
+__device__ __forceinline__ uint16_t f16_rne(float x) {
+    asm volatile("" : "+v"(x));
+    return __half_as_ushort(__float2half_rn(x));
+}
+// bf16 round-to-nearest-even; NaN kept quiet.
+__device__ __forceinline__ uint16_t bf16_rne(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static constexpr int kDtype = POPKV_DTYPE_F32;
+    __device__ static __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+    __device__ static __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Elem<bf16_t> {
+    static constexpr int kDtype = POPKV_DTYPE_BF16;
+    __device__ static __forceinline__ float load(const bf16_t* p, int64_t i) { return bits_bf16(p[i].bits); }
+    __device__ static __forceinline__ void store(bf16_t* p, int64_t i, float v) { p[i].bits = bf16_rne(v); }
+};
+template <> struct Elem<f16_t> {
+    static constexpr int kDtype = POPKV_DTYPE_F16;
+    __device__ static __forceinline__ float load(const f16_t* p, int64_t i) { return bits_f16(p[i].bits); }
+    __device__ static __forceinline__ void store(f16_t* p, int64_t i, float v) { p[i].bits = f16_rne(v); }
+};
+
+// Eight consecutive elements starting at a 16-byte aligned address -> float.
+template <typename T> __device__ __forceinline__ void load8(const T* p, float v[8]);
+template <> __device__ __forceinline__ void load8<bf16_t>(const bf16_t* p, float v[8]) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xffff0000u);
+    v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xffff0000u);
+    v[4] = __uint_as_float(u.z << 16); v[5] = __uint_as_float(u.z & 0xffff0000u);
+    v[6] = __uint_as_float(u.w << 16); v[7] = __uint_as_float(u.w & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void load8<f16_t>(const f16_t* p, float v[8]) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    v[0] = bits_f16(u.x & 0xffffu); v[1] = bits_f16(u.x >> 16);
+    v[2] = bits_f16(u.y & 0xffffu); v[3] = bits_f16(u.y >> 16);
+    v[4] = bits_f16(u.z & 0xffffu); v[5] = bits_f16(u.z >> 16);
+    v[6] = bits_f16(u.w & 0xffffu); v[7] = bits_f16(u.w >> 16);
+}
+template <> __device__ __forceinline__ void load8<float>(const float* p, float v[8]) {
+    float4 a = reinterpret_cast<const float4*>(p)[0];
+    float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// ---- representative reduction trees ---------------------------------------
+// The production packers reduce one representative group's 32 (or 16) lane
+// contributions with a halving tree: a_i = z_i + z_{i+16}, then +8, +4, +2, +1.
+// G64 first pairs dims j and j+32.  All terms are >= +0, so adding +0 from an
+// absent lane is exact and the same trees cover partial groups.
+
+__device__ __forceinline__ float tree_halving(float* z, int n) {
+#pragma unroll
+    for (int h = n / 2; h >= 1; h /= 2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (i < h) z[i] = z[i] + z[i + h];
+    }
+    return z[0];
+}
+
+// Sum of G contributions x[0..G) in the production tree order (destroys x).
+template <int G>
+__device__ __forceinline__ float rep_tree_sum(float* x) {
+    if constexpr (G == 64) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) x[j] = x[j] + x[j + 32];
+        return tree_halving(x, 32);
+    } else {
+        return tree_halving(x, G);
+    }
+}
+
+// low/delta with the empty-bucket rules of the reference packers.
+__device__ __forceinline__ void finish_rep(float ls, int ln, float hs, int hn, float& low, float& delta) {
+    float lo, hi;
+    if (ln == 0) {
+        lo = hn ? hs / static_cast<float>(hn) : 0.0f;
+        hi = lo;
+    } else {
+        lo = ls / static_cast<float>(ln);
+        hi = hn ? hs / static_cast<float>(hn) : lo;
+    }
+    low = lo;
+    delta = hi - lo;
+}
+
+// ---- wave / block reductions --------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// Inclusive prefix sum across the wave.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        uint32_t o = __shfl_up(v, off);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// Exclusive prefix sum across a block of `waves` wave64s.  `sh` holds at
+// least `waves` + 1 words of LDS.  Returns the exclusive prefix; *total gets
+// the block sum.  Contains three __syncthreads() (the first protects `sh`
+// from a previous call's readers), so every thread of the block must call it.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, int waves, uint32_t* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    uint32_t incl = wave_incl_scan(v, lane);
+    __syncthreads();
+    if (lane == kWave - 1) sh[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t w = lane < waves ? sh[lane] : 0u;
+        uint32_t wi = wave_incl_scan(w, lane);
+        if (lane < waves) sh[lane] = wi - w;
+        if (lane == waves - 1) sh[waves] = wi;
+    }
+    __syncthreads();
+    uint32_t base = sh[wave];
+    *total = sh[waves];
+    return base + incl - v;
+}
+
+}  // namespace popkv

@@ -1,0 +1,53 @@
+// Host-side launchers shared between the kernel translation units and the
+// C ABI (capi.hip).  Every launcher validates nothing: the C ABI checks the
+// arguments before calling.  All take a hipStream_t and return the launch
+// status from hipGetLastError().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace popkv {
+
+hipError_t launch_pack(const void* keys, int dtype, int64_t kv_heads, int64_t tokens, int head_dim,
+                       int64_t key_head_stride, int32_t* k_sign, int32_t* k_mag, uint16_t* k_low,
+                       uint16_t* k_delta, int64_t capacity, int64_t token_offset, int token_group_size,
+                       int dim_group_size, hipStream_t stream);
+
+hipError_t launch_query_encode(const void* queries, int dtype, int64_t rows, int head_dim,
+                               int dim_group_size, int order, int32_t* q_sign, int32_t* q_mag,
+                               float* q_low, float* q_delta, hipStream_t stream);
+
+hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const float* q_low,
+                             const float* q_delta, const int32_t* k_sign, const int32_t* k_mag,
+                             const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
+                             int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
+                             int dim_group_size, uint16_t* scores, int64_t score_row_stride,
+                             hipStream_t stream);
+
+hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, const float* q_low,
+                                const float* q_delta, const int32_t* k_sign, const int32_t* k_mag,
+                                const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
+                                int64_t batch, int q_heads, int kv_heads, int head_dim, int64_t capacity,
+                                int64_t tokens, int dim_group_size, float* scores, hipStream_t stream);
+
+hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens,
+                              int64_t k, int64_t current, void* indices, int index_dtype,
+                              int64_t index_row_stride, unsigned int* rearm_counters, hipStream_t stream);
+
+hipError_t launch_attention_partial(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                    int64_t k_head_stride, int64_t k_token_stride, int64_t v_head_stride,
+                                    int64_t v_token_stride, int64_t prefix_tokens, const void* current_k,
+                                    const void* current_v, const void* indices, int index_dtype,
+                                    int64_t index_row_stride, const uint8_t* valid_mask,
+                                    const int64_t* head_to_kv, int q_heads, int kv_heads, int head_dim,
+                                    int64_t selected,
+                                    int split_tokens, float* partials, unsigned int* merge_counters,
+                                    void* merge_output, hipStream_t stream);
+
+hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t splits, int head_dim,
+                                  void* output, int out_dtype, hipStream_t stream);
+
+hipError_t launch_zero_u32(unsigned int* p, int64_t n, hipStream_t stream);
+
+}  // namespace popkv

@@ -1,0 +1,369 @@
+// Query encode and the popcount Q.K scorer (gfx950).
+//
+// Query encode: one wave64 per query row.  The row is staged in LDS; the
+// whole-head extrema come from a butterfly (exact for min/max); sign and
+// magnitude words come from 64-bit ballots (two 32-bit words per ballot);
+// lane r < R then reduces representative group r from LDS in the requested
+// order -- a left fold over ascending dims (the decode-path encode,
+// popkv_ext.cu:232-281, :911-957) or the production reduction tree (the
+// warp encode inside score(), popkv_ext.cu:677-755).
+//
+// Scorer (head_dim 128): one thread per (KV head, token).  Each thread loads
+// its token's 16-byte sign and magnitude words and its fp16 representatives
+// once with coalesced vector loads, then scores every query head of the GQA
+// group.  The query state of the group is wave-uniform: the kernel reads it
+// with scalar loads, so it lives in SGPRs and the per-head popcount of the
+// query magnitude word is a scalar op.  Per head and representative the
+// kernel needs four signed agreement counts 2*popc(x & sel) - popc(sel)
+// (v_bcnt_u32_b32) and the fp32 fma chain of popkv_ext.cu:502-515 / :867-870,
+// summed from +0 over representatives, times fp32(1/sqrt(128)), rounded once
+// to fp16 (popkv_ext.cu:757-876).
+#include "device_common.h"
+#include "kernels.h"
+
+namespace popkv {
+namespace {
+
+// ---------------------------------------------------------------- encode
+
+template <typename T, int G, int ORDER>
+__global__ __launch_bounds__(kWave) void query_encode_kernel(
+    const T* __restrict__ q, int64_t rows, int d, int32_t* __restrict__ q_sign,
+    int32_t* __restrict__ q_mag, float* __restrict__ q_low, float* __restrict__ q_delta) {
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int W = (d + 31) / 32;
+    const int R = (d + G - 1) / G;
+    __shared__ float s_q[256];
+    const T* src = q + row * d;
+
+    float mn = INFINITY, mx = -INFINITY;
+    float v[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int dim = s * kWave + lane;
+        v[s] = dim < d ? Elem<T>::load(src, dim) : 0.0f;
+        if (dim < d) {
+            s_q[dim] = v[s];
+            mn = fminf(mn, v[s]);
+            mx = fmaxf(mx, v[s]);
+        }
+    }
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    const float neg = mn * 0.5f, pos = mx * 0.5f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int dim = s * kWave + lane;
+        const bool valid = dim < d;
+        const bool sg = valid && v[s] >= 0.0f;
+        const bool mg = valid && (sg ? v[s] > pos : v[s] < neg);
+        const uint64_t bs = __ballot(sg);
+        const uint64_t bm = __ballot(mg);
+        if (lane == 0) {
+            if (2 * s < W) {
+                q_sign[row * W + 2 * s] = static_cast<int32_t>(static_cast<uint32_t>(bs));
+                q_mag[row * W + 2 * s] = static_cast<int32_t>(static_cast<uint32_t>(bm));
+            }
+            if (2 * s + 1 < W) {
+                q_sign[row * W + 2 * s + 1] = static_cast<int32_t>(static_cast<uint32_t>(bs >> 32));
+                q_mag[row * W + 2 * s + 1] = static_cast<int32_t>(static_cast<uint32_t>(bm >> 32));
+            }
+        }
+    }
+    __syncthreads();
+    if (lane < R) {
+        const int start = lane * G;
+        const int end = min(start + G, d);
+        float ls = 0.0f, hs = 0.0f;
+        int ln = 0, hn = 0;
+        if constexpr (ORDER == POPKV_ENCODE_FOLD) {
+            for (int i = start; i < end; ++i) {
+                const float x = s_q[i];
+                const bool sg = x >= 0.0f;
+                const bool mg = sg ? x > pos : x < neg;
+                if (mg) { hs += fabsf(x); ++hn; } else { ls += fabsf(x); ++ln; }
+            }
+        } else {
+            float xl[G], xh[G];
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const int i = start + j;
+                const float x = i < end ? s_q[min(i, 255)] : 0.0f;
+                const bool sg = x >= 0.0f;
+                const bool mg = i < end && (sg ? x > pos : x < neg);
+                xl[j] = (i < end && !mg) ? fabsf(x) : 0.0f;
+                xh[j] = mg ? fabsf(x) : 0.0f;
+                ln += (i < end && !mg) ? 1 : 0;
+                hn += mg ? 1 : 0;
+            }
+            ls = rep_tree_sum<G>(xl);
+            hs = rep_tree_sum<G>(xh);
+        }
+        float lo, de;
+        finish_rep(ls, ln, hs, hn, lo, de);
+        q_low[row * R + lane] = lo;
+        q_delta[row * R + lane] = de;
+    }
+}
+
+// ---------------------------------------------------------------- score, D = 128
+
+// Four signed agreement counts of one representative over the masked bits of
+// word pair (w0, w1) (w1 unused when ONE_WORD), combined with the fp32 chain.
+template <int G>
+__device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm, const uint32_t* ks,
+                                          const uint32_t* km, int r, float ql, float dq, float kl, float dk) {
+    int cs, cq, ck, cqk;
+    if constexpr (G == 64) {
+        const uint32_t m0 = ~(qs[2 * r] ^ ks[2 * r]), m1 = ~(qs[2 * r + 1] ^ ks[2 * r + 1]);
+        const uint32_t b0 = qm[2 * r] & km[2 * r], b1 = qm[2 * r + 1] & km[2 * r + 1];
+        cs = 2 * (__popc(m0) + __popc(m1)) - 64;
+        cq = 2 * (__popc(m0 & qm[2 * r]) + __popc(m1 & qm[2 * r + 1])) - (__popc(qm[2 * r]) + __popc(qm[2 * r + 1]));
+        ck = 2 * (__popc(m0 & km[2 * r]) + __popc(m1 & km[2 * r + 1])) - (__popc(km[2 * r]) + __popc(km[2 * r + 1]));
+        cqk = 2 * (__popc(m0 & b0) + __popc(m1 & b1)) - (__popc(b0) + __popc(b1));
+    } else {
+        const int w = G == 32 ? r : r / 2;
+        const uint32_t mask = G == 32 ? 0xffffffffu : ((r & 1) ? 0xffff0000u : 0x0000ffffu);
+        const uint32_t qmm = qm[w] & mask, kmm = km[w] & mask;
+        const uint32_t match = ~(qs[w] ^ ks[w]) & mask, both = qmm & kmm;
+        cs = 2 * __popc(match) - (G == 32 ? 32 : 16);
+        cq = 2 * __popc(match & qmm) - __popc(qmm);
+        ck = 2 * __popc(match & kmm) - __popc(kmm);
+        cqk = 2 * __popc(match & both) - __popc(both);
+    }
+    return fmaf(ql * kl, static_cast<float>(cs),
+                fmaf(dq * kl, static_cast<float>(cq),
+                     fmaf(ql * dk, static_cast<float>(ck), dq * dk * static_cast<float>(cqk))));
+}
+
+constexpr int kScoreThreads = 256;
+constexpr int kScoreTokensPerThread = 2;
+
+// grid.x: token tiles of kScoreThreads*kScoreTokensPerThread; grid.y: batch*kv_heads.
+template <int G, int QPK>
+__global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
+    const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
+    const float* __restrict__ q_low, const float* __restrict__ q_delta,
+    const uint4* __restrict__ k_sign, const uint4* __restrict__ k_mag,
+    const uint16_t* __restrict__ k_low, const uint16_t* __restrict__ k_delta,
+    const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, int qpk_rt,
+    int64_t cap, int64_t tokens, uint16_t* __restrict__ scores, int64_t out_stride) {
+    constexpr int R = 128 / G;
+    const int qpk = QPK > 0 ? QPK : qpk_rt;
+    const int64_t grow = blockIdx.y;
+    const int64_t b = grow / kv_heads;
+    const int64_t slot = grow % kv_heads;
+    const int64_t qh0 = slot * qpk;
+    // A mapping outside [0, kv_heads) is clamped, never dereferenced.
+    const int64_t kvh = min(max(head_to_kv[qh0], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    const int64_t qrow0 = b * q_heads + qh0;
+
+#pragma unroll
+    for (int it = 0; it < kScoreTokensPerThread; ++it) {
+        const int64_t t = (static_cast<int64_t>(blockIdx.x) * kScoreTokensPerThread + it) * kScoreThreads + threadIdx.x;
+        if (t >= tokens) break;
+        const int64_t krow = kvh * cap + t;
+        const uint4 s4 = k_sign[krow];
+        const uint4 m4 = k_mag[krow];
+        const uint32_t ks[4] = {s4.x, s4.y, s4.z, s4.w};
+        const uint32_t km[4] = {m4.x, m4.y, m4.z, m4.w};
+        float kl[R], dk[R];
+        if constexpr (R == 2) {
+            const uint32_t l2 = reinterpret_cast<const uint32_t*>(k_low)[krow];
+            const uint32_t d2 = reinterpret_cast<const uint32_t*>(k_delta)[krow];
+            kl[0] = bits_f16(l2 & 0xffffu); kl[1] = bits_f16(l2 >> 16);
+            dk[0] = bits_f16(d2 & 0xffffu); dk[1] = bits_f16(d2 >> 16);
+        } else if constexpr (R == 4) {
+            const uint2 l4 = reinterpret_cast<const uint2*>(k_low)[krow];
+            const uint2 d4 = reinterpret_cast<const uint2*>(k_delta)[krow];
+            const uint32_t lw[2] = {l4.x, l4.y}, dw[2] = {d4.x, d4.y};
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                kl[2 * i] = bits_f16(lw[i] & 0xffffu); kl[2 * i + 1] = bits_f16(lw[i] >> 16);
+                dk[2 * i] = bits_f16(dw[i] & 0xffffu); dk[2 * i + 1] = bits_f16(dw[i] >> 16);
+            }
+        } else {
+            const uint4 l8 = reinterpret_cast<const uint4*>(k_low)[krow];
+            const uint4 d8 = reinterpret_cast<const uint4*>(k_delta)[krow];
+            const uint32_t lw[4] = {l8.x, l8.y, l8.z, l8.w}, dw[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kl[2 * i] = bits_f16(lw[i] & 0xffffu); kl[2 * i + 1] = bits_f16(lw[i] >> 16);
+                dk[2 * i] = bits_f16(dw[i] & 0xffffu); dk[2 * i + 1] = bits_f16(dw[i] >> 16);
+            }
+        }
+        for (int h = 0; h < qpk; ++h) {
+            const int64_t qrow = qrow0 + h;
+            uint32_t qs[4], qm[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                qs[w] = static_cast<uint32_t>(q_sign[qrow * 4 + w]);
+                qm[w] = static_cast<uint32_t>(q_mag[qrow * 4 + w]);
+            }
+            float total = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                total = total + rep_term<G>(qs, qm, ks, km, r, q_low[qrow * R + r], q_delta[qrow * R + r], kl[r], dk[r]);
+            scores[qrow * out_stride + t] = f16_rne(total * 0x1.6a09e6p-4f);  // fp32(1/sqrt(128)) = 0x3DB504F3
+        }
+    }
+}
+
+// ---------------------------------------------------------------- score, generic D
+
+// One thread per (query row, token), float32 output (popkv_ext.cu:145-230,
+// :517-675): per-head KV mapping, partial words masked, scale 1/sqrt(D).
+template <int G>
+__global__ __launch_bounds__(256) void score_generic_kernel(
+    const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
+    const float* __restrict__ q_low, const float* __restrict__ q_delta,
+    const int32_t* __restrict__ k_sign, const int32_t* __restrict__ k_mag,
+    const uint16_t* __restrict__ k_low, const uint16_t* __restrict__ k_delta,
+    const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, int d, int64_t cap, int64_t tokens,
+    float scale, float* __restrict__ scores) {
+    const int64_t row = blockIdx.y;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= tokens) return;
+    const int W = (d + 31) / 32, R = (d + G - 1) / G;
+    const int64_t kvh = min(max(head_to_kv[row % q_heads], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    const int64_t krow = kvh * cap + t;
+    float score = 0.0f;
+    for (int r = 0; r < R; ++r) {
+        const float ql = q_low[row * R + r], dq = q_delta[row * R + r];
+        const float kl = bits_f16(k_low[krow * R + r]), dk = bits_f16(k_delta[krow * R + r]);
+        int cs = 0, cq = 0, ck = 0, cqk = 0;
+        const int rs = r * G, re = min(rs + G, d);
+        for (int w = rs / 32; w <= (re - 1) / 32; ++w) {
+            const int ws = w * 32;
+            const int begin = max(rs, ws) - ws, end = min(re, ws + 32) - ws;
+            const int count = end - begin;
+            const uint32_t mask = count == 32 ? 0xffffffffu : ((1u << count) - 1u) << begin;
+            const uint32_t qs = static_cast<uint32_t>(q_sign[row * W + w]);
+            const uint32_t qm = static_cast<uint32_t>(q_mag[row * W + w]) & mask;
+            const uint32_t ks = static_cast<uint32_t>(k_sign[krow * W + w]);
+            const uint32_t km = static_cast<uint32_t>(k_mag[krow * W + w]) & mask;
+            const uint32_t match = ~(qs ^ ks) & mask, both = qm & km;
+            cs += 2 * __popc(match) - __popc(mask);
+            cq += 2 * __popc(match & qm) - __popc(qm);
+            ck += 2 * __popc(match & km) - __popc(km);
+            cqk += 2 * __popc(match & both) - __popc(both);
+        }
+        score = score + fmaf(ql * kl, static_cast<float>(cs),
+                             fmaf(dq * kl, static_cast<float>(cq),
+                                  fmaf(ql * dk, static_cast<float>(ck), dq * dk * static_cast<float>(cqk))));
+    }
+    scores[row * tokens + t] = score * scale;
+}
+
+template <typename T, int G>
+hipError_t launch_encode_t(const T* q, int64_t rows, int d, int order, int32_t* qs, int32_t* qm, float* ql,
+                           float* qd, hipStream_t stream) {
+    if (order == POPKV_ENCODE_TREE)
+        hipLaunchKernelGGL((query_encode_kernel<T, G, POPKV_ENCODE_TREE>), dim3(static_cast<unsigned>(rows)),
+                           dim3(kWave), 0, stream, q, rows, d, qs, qm, ql, qd);
+    else
+        hipLaunchKernelGGL((query_encode_kernel<T, G, POPKV_ENCODE_FOLD>), dim3(static_cast<unsigned>(rows)),
+                           dim3(kWave), 0, stream, q, rows, d, qs, qm, ql, qd);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_encode_g(const T* q, int64_t rows, int d, int g, int order, int32_t* qs, int32_t* qm,
+                           float* ql, float* qd, hipStream_t stream) {
+    switch (g) {
+        case 16: return launch_encode_t<T, 16>(q, rows, d, order, qs, qm, ql, qd, stream);
+        case 32: return launch_encode_t<T, 32>(q, rows, d, order, qs, qm, ql, qd, stream);
+        default: return launch_encode_t<T, 64>(q, rows, d, order, qs, qm, ql, qd, stream);
+    }
+}
+
+template <int G>
+hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float* ql, const float* qd,
+                               const int32_t* ks, const int32_t* km, const uint16_t* kl, const uint16_t* kd,
+                               const int64_t* h2k, int64_t batch, int qh, int kvh, int64_t cap, int64_t tokens,
+                               uint16_t* out, int64_t out_stride, hipStream_t stream) {
+    const int qpk = qh / kvh;
+    const int64_t per_block = static_cast<int64_t>(kScoreThreads) * kScoreTokensPerThread;
+    dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block), static_cast<unsigned>(batch * kvh));
+    const uint4* ks4 = reinterpret_cast<const uint4*>(ks);
+    const uint4* km4 = reinterpret_cast<const uint4*>(km);
+#define POPKV_SCORE_LAUNCH(Q)                                                                              \
+    hipLaunchKernelGGL((score_d128_kernel<G, Q>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd, ks4, \
+                       km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride)
+    switch (qpk) {
+        case 1: POPKV_SCORE_LAUNCH(1); break;
+        case 2: POPKV_SCORE_LAUNCH(2); break;
+        case 4: POPKV_SCORE_LAUNCH(4); break;
+        case 8: POPKV_SCORE_LAUNCH(8); break;
+        default: POPKV_SCORE_LAUNCH(0); break;
+    }
+#undef POPKV_SCORE_LAUNCH
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_query_encode(const void* queries, int dtype, int64_t rows, int head_dim, int dim_group_size,
+                               int order, int32_t* q_sign, int32_t* q_mag, float* q_low, float* q_delta,
+                               hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_encode_g(static_cast<const float*>(queries), rows, head_dim, dim_group_size, order, q_sign,
+                                   q_mag, q_low, q_delta, stream);
+        case POPKV_DTYPE_F16:
+            return launch_encode_g(static_cast<const f16_t*>(queries), rows, head_dim, dim_group_size, order, q_sign,
+                                   q_mag, q_low, q_delta, stream);
+        default:
+            return launch_encode_g(static_cast<const bf16_t*>(queries), rows, head_dim, dim_group_size, order,
+                                   q_sign, q_mag, q_low, q_delta, stream);
+    }
+}
+
+hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const float* q_low, const float* q_delta,
+                             const int32_t* k_sign, const int32_t* k_mag, const uint16_t* k_low,
+                             const uint16_t* k_delta, const int64_t* head_to_kv, int64_t batch, int q_heads,
+                             int kv_heads, int64_t capacity, int64_t tokens, int dim_group_size, uint16_t* scores,
+                             int64_t score_row_stride, hipStream_t stream) {
+    switch (dim_group_size) {
+        case 16:
+            return launch_score_d128_g<16>(q_sign, q_mag, q_low, q_delta, k_sign, k_mag, k_low, k_delta, head_to_kv,
+                                           batch, q_heads, kv_heads, capacity, tokens, scores, score_row_stride, stream);
+        case 32:
+            return launch_score_d128_g<32>(q_sign, q_mag, q_low, q_delta, k_sign, k_mag, k_low, k_delta, head_to_kv,
+                                           batch, q_heads, kv_heads, capacity, tokens, scores, score_row_stride, stream);
+        default:
+            return launch_score_d128_g<64>(q_sign, q_mag, q_low, q_delta, k_sign, k_mag, k_low, k_delta, head_to_kv,
+                                           batch, q_heads, kv_heads, capacity, tokens, scores, score_row_stride, stream);
+    }
+}
+
+hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, const float* q_low,
+                                const float* q_delta, const int32_t* k_sign, const int32_t* k_mag,
+                                const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
+                                int64_t batch, int q_heads, int kv_heads, int head_dim, int64_t capacity,
+                                int64_t tokens, int dim_group_size, float* scores, hipStream_t stream) {
+    const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(head_dim)));
+    dim3 grid(static_cast<unsigned>((tokens + 255) / 256), static_cast<unsigned>(batch * q_heads));
+    switch (dim_group_size) {
+        case 16:
+            hipLaunchKernelGGL((score_generic_kernel<16>), grid, dim3(256), 0, stream, q_sign, q_mag, q_low, q_delta,
+                               k_sign, k_mag, k_low, k_delta, head_to_kv, q_heads, kv_heads, head_dim, capacity, tokens, scale,
+                               scores);
+            break;
+        case 32:
+            hipLaunchKernelGGL((score_generic_kernel<32>), grid, dim3(256), 0, stream, q_sign, q_mag, q_low, q_delta,
+                               k_sign, k_mag, k_low, k_delta, head_to_kv, q_heads, kv_heads, head_dim, capacity, tokens, scale,
+                               scores);
+            break;
+        default:
+            hipLaunchKernelGGL((score_generic_kernel<64>), grid, dim3(256), 0, stream, q_sign, q_mag, q_low, q_delta,
+                               k_sign, k_mag, k_low, k_delta, head_to_kv, q_heads, kv_heads, head_dim, capacity, tokens, scale,
+                               scores);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace popkv

@@ -1,0 +1,388 @@
+"""GPU parity of the HIP path against the CPU oracle (bit-exact for planes,
+representatives, popcount scores and selected indices; attention within
+2e-2 max-abs / 1e-2 relative of a float64 materialized reference).
+
+Mirrors the reference's GPU tests (tests/test_popkv.py:199-372,
+tests/test_sparse_kernels.py:118-140) and extends them to the benchmark
+configuration C1 at full size.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from popkv_amd import _native, popkv, popkv_cuda, sparse_kernels, topk, workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DIMS = (32, 64, 96, 127, 128)
+GROUPS = (16, 32, 64)
+DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+ATTN_ATOL, ATTN_RTOL = 2e-2, 1e-2
+
+
+def f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float32:
+        return t.view(torch.int32).numpy().view(np.uint32)
+    return t.numpy()
+
+
+def randn(*shape, dtype=torch.bfloat16, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype).to(DEV)
+
+
+# ------------------------------------------------------------------ query encode
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("d", DIMS)
+def test_query_encode_bit_exact(d, g, dtype):
+    q = randn(2, 8, d, dtype=dtype, seed=17 + d + g)
+    got = popkv_cuda.query_encode(q.contiguous(), dim_group_size=g)
+    want = core.query_encode(f32(q), g, order="fold")
+    assert np.array_equal(bits(got[0]), want[0]) and np.array_equal(bits(got[1]), want[1])
+    assert np.array_equal(bits(got[2]), want[2].view(np.uint32))
+    assert np.array_equal(bits(got[3]), want[3].view(np.uint32))
+
+
+@pytest.mark.parametrize("g", GROUPS)
+def test_query_encode_tree_order_bit_exact(g):
+    q = randn(4, 8, 128, seed=3 + g, scale=7.0)
+    outs = popkv_cuda.allocate_query_encode_outputs(q, dim_group_size=g)
+    with torch.cuda.device(q.device):
+        _native.call("popkv_query_encode", q.data_ptr(), _native.DTYPE_BF16, 32, 128, g, _native.ENCODE_TREE,
+                     *(t.data_ptr() for t in outs), _native.stream_of(q.device))
+    want = core.query_encode(f32(q), g, order="tree")
+    for a, b in zip(outs, want):
+        assert np.array_equal(bits(a), b.view(np.uint32) if b.dtype == np.float32 else b)
+
+
+# ------------------------------------------------------------------ pack
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("d", DIMS)
+def test_pack_bit_exact(d, g, dtype):
+    keys = randn(2, 37, d, dtype=dtype, seed=31 + d + g)
+    packed = popkv_cuda.pack_keys(keys.contiguous(), dim_group_size=g)
+    want = core.pack_keys(f32(keys), token_group_size=32, dim_group_size=g)
+    for a, b in zip(packed, want):
+        assert a.shape == b.shape
+        assert np.array_equal(bits(a), b)
+
+
+@pytest.mark.parametrize("tg", (1, 5, 8, 10, 16, 32, 64, 125, 128, 500, 4096))
+def test_pack_token_groups_bit_exact(tg):
+    tokens = tg + 3
+    keys = randn(2, tokens, 128, seed=37 + tg)
+    for g in (GROUPS if tg in popkv_cuda.SPECIALIZED_TOKEN_GROUP_SIZES else (32,)):
+        packed = popkv_cuda.pack_keys(keys.contiguous(), token_group_size=tg, dim_group_size=g)
+        want = core.pack_keys(f32(keys), token_group_size=tg, dim_group_size=g)
+        for a, b in zip(packed, want):
+            assert np.array_equal(bits(a), b)
+
+
+def test_pack_outlier_keys_and_capacity_tail():
+    w = workloads.scaled(workloads.C1, context=1000)
+    layer = workloads.make_layer(w).to(DEV)
+    keys = layer.prefix_k().contiguous()
+    packed = popkv_cuda.pack_keys(keys, token_capacity=1100, token_group_size=64, dim_group_size=64)
+    want = core.pack_keys(f32(keys), token_group_size=64, dim_group_size=64)
+    for a, b in zip(packed, want):
+        assert a.shape[1] == 1100
+        assert np.array_equal(bits(a)[:, :999], b)
+
+
+@pytest.mark.parametrize("tg", (8, 16, 32, 64, 128))
+def test_incremental_cache_crosses_every_token_group_boundary(tg):
+    """tests/test_popkv.py:354-372 on the HIP path, bit-exact."""
+    for g in GROUPS:
+        keys = randn(2, tg - 1, 128, seed=41 + tg + g)
+        cache = popkv.build_popkv_cache(keys, group_size=tg, dim_group_size=g, reserve_tokens=3)
+        for step in range(2):
+            current = randn(2, 1, 128, seed=1000 + step + tg + g)
+            popkv.append_popkv(cache, current)
+            keys = torch.cat((keys, current), dim=1)
+            want = core.pack_keys(f32(keys), token_group_size=tg, dim_group_size=g)
+            n = keys.shape[1]
+            for a, b in zip(cache.packed, want):
+                assert np.array_equal(bits(a)[:, :n], b)
+            assert cache.token_count == n
+
+
+def test_pack_into_capacity_exceeded():
+    keys = randn(2, 10, 128)
+    packed = popkv_cuda.pack_keys(keys.contiguous(), token_capacity=12)
+    with pytest.raises(RuntimeError, match="capacity exceeded"):
+        popkv_cuda.pack_keys_into(keys.contiguous(), packed, token_offset=3)
+
+
+# ------------------------------------------------------------------ score
+
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("d", DIMS)
+def test_score_bit_exact(d, g):
+    keys = randn(2, 37, d, seed=31 + d)
+    q = randn(1, 8, d, seed=131 + d)
+    mapping = torch.arange(8, device=DEV) // 4
+    packed = popkv_cuda.pack_keys(keys.contiguous(), dim_group_size=g)
+    got = popkv_cuda.score(q.contiguous(), packed, head_to_kv=mapping, tokens=37, dim_group_size=g)
+    assert got.dtype == (torch.float16 if d == 128 else torch.float32)
+    want = core.score(f32(q), tuple(bits(t) if t.dtype != torch.int32 else t.cpu().numpy() for t in packed),
+                      head_to_kv=mapping.cpu().numpy(), tokens=37, dim_group_size=g)
+    assert np.array_equal(bits(got), want.view(np.uint32) if want.dtype == np.float32 else want)
+    if d == 128:
+        enc = popkv_cuda.query_encode(q.contiguous(), dim_group_size=g)
+        sep = popkv_cuda.score_encoded(enc, packed, head_to_kv=mapping, tokens=37, dim_group_size=g)
+        want_sep = core.score_encoded(tuple(t.cpu().numpy() for t in enc),
+                                      tuple(bits(t) if t.dtype != torch.int32 else t.cpu().numpy() for t in packed),
+                                      head_to_kv=mapping.cpu().numpy(), tokens=37, dim_group_size=g)
+        assert np.array_equal(bits(sep), want_sep)
+
+
+@pytest.mark.parametrize("g", GROUPS)
+def test_score_multiple_batches_and_tokens(g):
+    """tests/test_popkv.py:302-317 shape (batch 2, 257 tokens) plus a long row."""
+    for tokens in (257, 5000):
+        keys = randn(2, tokens, 128, seed=32 + tokens)
+        q = randn(2, 8, 128, seed=33 + tokens)
+        mapping = torch.arange(8, device=DEV) // 4
+        packed = popkv_cuda.pack_keys(keys.contiguous(), dim_group_size=g)
+        got = popkv_cuda.score(q.contiguous(), packed, head_to_kv=mapping, tokens=tokens, dim_group_size=g)
+        pk = tuple(bits(t) if t.dtype != torch.int32 else t.cpu().numpy() for t in packed)
+        want = core.score(f32(q), pk, head_to_kv=mapping.cpu().numpy(), tokens=tokens, dim_group_size=g)
+        assert np.array_equal(bits(got), want)
+
+
+def test_score_rejects_bad_token_count():
+    keys = randn(2, 8, 128)
+    packed = popkv_cuda.pack_keys(keys.contiguous())
+    mapping = torch.arange(8, device=DEV) // 4
+    with pytest.raises(RuntimeError, match="invalid score token count"):
+        popkv_cuda.score(randn(1, 8, 128).contiguous(), packed, head_to_kv=mapping, tokens=9)
+
+
+# ------------------------------------------------------------------ select
+
+def _scores(kind: str, rows: int, tokens: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    if kind == "random":
+        x = torch.randn(rows, tokens, generator=g)
+    elif kind == "ties":
+        x = torch.randint(-3, 4, (rows, tokens), generator=g).float()
+    elif kind == "two_values":
+        x = torch.where(torch.rand(rows, tokens, generator=g) < 0.5, 1.0, 2.0)
+    elif kind == "signed_zero":
+        x = torch.where(torch.rand(rows, tokens, generator=g) < 0.5, -0.0, 0.0)
+    elif kind == "nan":
+        x = torch.randn(rows, tokens, generator=g)
+        x[:, ::37] = float("nan")
+    else:  # peaked fp16 scores, as the scorer produces
+        x = torch.randn(rows, tokens, generator=g) * 0.5
+        x[:, ::97] += 4.0
+    return x.to(torch.float16).to(DEV)
+
+
+@pytest.mark.parametrize("kind", ["random", "ties", "two_values", "signed_zero", "nan", "peaked"])
+@pytest.mark.parametrize("tokens", [1, 7, 1000, 4095, 32767])
+def test_select_matches_oracle(kind, tokens):
+    s = _scores(kind, 4, tokens, seed=tokens + len(kind))
+    for k in sorted({0, 1, min(511, tokens), min(4095, tokens), max(tokens - 1, 0), tokens}):
+        got = topk.select_with_current(s, k, tokens + 1)
+        want = core.select(bits(s), k, tokens)
+        assert np.array_equal(got.cpu().numpy(), want), (kind, tokens, k)
+
+
+@pytest.mark.parametrize("tokens", [65535, 131071])
+def test_select_long_rows(tokens):
+    s = _scores("peaked", 3, tokens, seed=5)
+    got = topk.select_with_current(s, 4095, tokens + 1)
+    assert np.array_equal(got.cpu().numpy(), core.select(bits(s), 4095, tokens))
+
+
+@pytest.mark.parametrize("kind", ["ties", "two_values", "signed_zero", "random"])
+def test_select_agrees_with_torch_topk_on_rocm(kind):
+    """The tie rule (lowest indices among scores equal to the k-th) is the one
+    PyTorch's radix top-k applies; checked against torch.topk on this GPU."""
+    s = _scores(kind, 8, 4096, seed=11)
+    for k in (1, 100, 511, 2048, 4095):
+        ours = topk.topk_indices(s, k).cpu().numpy()
+        ref = torch.topk(s, k, dim=-1, sorted=False).indices.cpu().numpy()
+        for r in range(s.shape[0]):
+            assert set(ours[r].tolist()) == set(ref[r].tolist()), (kind, k, r)
+
+
+def test_topk_indices_shape_matches_torch():
+    s = _scores("random", 8, 1000, seed=3).view(1, 8, 1000)
+    idx = topk.topk_indices(s, 31)
+    assert idx.shape == (1, 8, 31) and idx.dtype == torch.int64
+    ref = torch.topk(s, 31, dim=-1, sorted=False).indices
+    assert torch.equal(idx.sort(-1).values, ref.sort(-1).values)
+
+
+# ------------------------------------------------------------------ attention
+
+def _attn_case(q_heads=8, kv_heads=2, tokens=32768, dim=128, selected=4096, dtype=torch.bfloat16, seed=104,
+               capacity=None):
+    g = torch.Generator().manual_seed(seed)
+    cap = tokens if capacity is None else capacity
+    queries = torch.randn(q_heads, dim, generator=g).to(dtype).to(DEV)
+    kstore = torch.randn(kv_heads, cap, dim, generator=g).to(dtype).to(DEV)
+    vstore = torch.randn(kv_heads, cap, dim, generator=g).to(dtype).to(DEV)
+    ck = torch.randn(kv_heads, dim, generator=g).to(dtype).to(DEV)
+    cv = torch.randn(kv_heads, dim, generator=g).to(dtype).to(DEV)
+    mapping = (torch.arange(q_heads) // (q_heads // kv_heads)).to(DEV)
+    indices = torch.randint(tokens, (q_heads, selected), generator=g).to(DEV)
+    indices[:, -1] = tokens
+    return queries, kstore[:, :tokens], vstore[:, :tokens], ck, cv, indices, mapping
+
+
+def _oracle_attention(q, k, v, ck, cv, idx, mapping, valid=None):
+    return core.attention(f32(q), f32(k), f32(v), f32(ck), f32(cv), idx.cpu().numpy(), mapping.cpu().numpy(),
+                          None if valid is None else valid.cpu().numpy())
+
+
+def test_split_attention_matches_reference_shape():
+    """tests/test_sparse_kernels.py:118-140: 32K tokens, 4096 selected, split 256, valid mask."""
+    q, k, v, ck, cv, idx, mapping = _attn_case()
+    valid = torch.ones_like(idx, dtype=torch.bool)
+    valid[:, -7:-1] = False
+    for vm in (None, valid):
+        got = sparse_kernels.indexed_attention_split(q, k, v, ck, cv, idx, mapping, vm, split_tokens=256)
+        assert got.dtype == q.dtype and got.shape == q.shape
+        want = _oracle_attention(q, k, v, ck, cv, idx, mapping, vm)
+        np.testing.assert_allclose(f32(got), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dim", (64, 128, 256))
+def test_split_attention_dtypes_dims_and_strided_cache(dtype, dim):
+    q, k, v, ck, cv, idx, mapping = _attn_case(q_heads=8, kv_heads=4, tokens=3000, dim=dim, selected=700,
+                                               dtype=dtype, seed=dim, capacity=3500)
+    assert not k.is_contiguous()  # static-cache view: head stride = capacity * D
+    for split in (16, 256, 512):
+        got = sparse_kernels.indexed_attention_split(q, k, v, ck, cv, idx, mapping, split_tokens=split)
+        want = _oracle_attention(q, k, v, ck, cv, idx, mapping)
+        np.testing.assert_allclose(f32(got), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
+def test_split_attention_partials_merge_like_oracle():
+    q, k, v, ck, cv, idx, mapping = _attn_case(tokens=5000, selected=1000, seed=9)
+    parts = sparse_kernels.indexed_attention_split_partial(q, k, v, ck, cv, idx, mapping, split_tokens=256)
+    assert parts.shape == (8, 4, 130) and parts.dtype == torch.float32
+    merged = sparse_kernels.indexed_attention_split_merge(parts, q.float())
+    np.testing.assert_allclose(f32(merged), core.attention_merge(f32(parts)), atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(f32(merged), _oracle_attention(q, k, v, ck, cv, idx, mapping), atol=ATTN_ATOL,
+                               rtol=ATTN_RTOL)
+
+
+def test_split_attention_int32_indices_and_all_masked_split():
+    q, k, v, ck, cv, idx, mapping = _attn_case(tokens=4000, selected=600, seed=12)
+    valid = torch.ones_like(idx, dtype=torch.bool)
+    valid[:, 256:512] = False  # an entire split masked out
+    got = sparse_kernels.indexed_attention_split(q, k, v, ck, cv, idx.int(), mapping, valid)
+    want = _oracle_attention(q, k, v, ck, cv, idx, mapping, valid)
+    np.testing.assert_allclose(f32(got), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
+# ------------------------------------------------------------------ decode step
+
+def _layer_setup(w: workloads.Workload, seed=None):
+    layer = workloads.make_layer(w, seed=seed).to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    cache = popkv.build_popkv_cache(layer.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                    reserve_tokens=64)
+    return layer, mapping, cache
+
+
+def _oracle_step(w, layer, mapping, cache):
+    """Oracle for one layer: fold encode -> GQA popcount scores -> select ->
+    float64 attention.  Returns (fp16 score bits, indices, output)."""
+    L = layer.prefix_tokens
+    enc = core.query_encode(f32(layer.queries)[None], w.dim_group, order="fold")
+    pk = tuple(bits(t) if t.dtype != torch.int32 else t.cpu().numpy() for t in cache.packed)
+    h2k = mapping.cpu().numpy()
+    sc = core.score_encoded(enc, pk, head_to_kv=h2k, tokens=L, dim_group_size=w.dim_group)[0]
+    idx = core.select(sc, w.k, L)
+    out = core.attention(f32(layer.queries), f32(layer.prefix_k()), f32(layer.prefix_v()), f32(layer.current_k()),
+                         f32(layer.current_v()), idx, h2k)
+    return sc, idx, out
+
+
+@pytest.mark.parametrize("method", ["popkv-s", "popkv-q", "popkv-normal"])
+def test_retrieval_step_and_layer_step_match_oracle(method):
+    tg, g = popkv.POPKV_PRESETS[method]
+    base = workloads.scaled(workloads.C1, context=6000, budget=1024)
+    w = workloads.Workload(base.name, method, base.q_heads, base.kv_heads, 128, 6000, 1024, tg, g,
+                           torch.bfloat16, 42, True)
+    layer, mapping, cache = _layer_setup(w)
+    sc, idx, out = _oracle_step(w, layer, mapping, cache)
+    enc = popkv_cuda.query_encode(layer.queries.unsqueeze(0).contiguous(), dim_group_size=g)
+    scores = popkv_cuda.score_encoded(enc, cache.packed, head_to_kv=mapping, tokens=cache.token_count,
+                                      dim_group_size=g)
+    assert np.array_equal(bits(scores[0]), sc)
+    sel = topk.select_with_current(scores, w.k, layer.prefix_tokens + 1)
+    assert np.array_equal(sel.cpu().numpy(), idx)
+    o1 = popkv.popkv_retrieval_step(layer.queries, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), cache, mapping, budget=w.budget)
+    np.testing.assert_allclose(f32(o1), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+    o2, idx2 = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                      layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(idx2.cpu().numpy(), idx)
+    np.testing.assert_allclose(f32(o2), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+    o3 = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                layer.current_v(), mapping, budget=w.budget)
+    assert torch.equal(o3, o2)
+
+
+def test_retrieval_step_with_torch_topk_hook():
+    w = workloads.scaled(workloads.C1, context=3000, budget=512)
+    layer, mapping, cache = _layer_setup(w)
+    ours = popkv.popkv_retrieval_step(layer.queries, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                      layer.current_v(), cache, mapping, budget=w.budget)
+    hooked = popkv.popkv_retrieval_step(
+        layer.queries, layer.prefix_k(), layer.prefix_v(), layer.current_k(), layer.current_v(), cache, mapping,
+        budget=w.budget, topk=lambda s, k: torch.topk(s, k=k, dim=-1, sorted=False).indices)
+    np.testing.assert_allclose(f32(hooked), f32(ours), atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
+def test_c1_full_size_parity():
+    """The headline configuration: PopKV-S, QH 32 / KVH 8, 32K context,
+    budget 4096, bf16.  Prepack bit-exact, scores bit-exact, indices exact,
+    attention within tolerance; then a decode append keeps all of it."""
+    w = workloads.C1
+    layer, mapping, cache = _layer_setup(w)
+    L = layer.prefix_tokens
+    want_pack = core.pack_keys(f32(layer.prefix_k()), token_group_size=64, dim_group_size=64)
+    for a, b in zip(cache.packed, want_pack):
+        assert np.array_equal(bits(a)[:, :L], b)
+    sc, idx, out = _oracle_step(w, layer, mapping, cache)
+    o, got_idx = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(),
+                                        layer.current_k(), layer.current_v(), mapping, budget=w.budget,
+                                        return_indices=True)
+    assert np.array_equal(got_idx.cpu().numpy(), idx)
+    err = np.abs(f32(o) - out)
+    assert (err <= ATTN_ATOL + ATTN_RTOL * np.abs(out)).all(), err.max()
+    # size-independent properties of the selection
+    assert (got_idx[:, -1] == L).all()
+    assert (got_idx[:, :-1].diff(dim=-1) > 0).all()
+    # append the current token to the retrieval cache, as the decode loop does
+    popkv.append_popkv(cache, layer.current_k()[:, None])
+    keys_all = layer.keys
+    want_tail = core.pack_keys(f32(keys_all[:, L - (L % 64):]), token_group_size=64, dim_group_size=64)
+    start = L - (L % 64)
+    for a, b in zip(cache.packed, want_tail):
+        assert np.array_equal(bits(a)[:, start:L + 1], b)

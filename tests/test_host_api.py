@@ -1,0 +1,275 @@
+"""Host-side logic of the drop-in API, runnable without a GPU: argument
+validation and exception types (the reference raises ValueError from Python
+and RuntimeError from its native checks), cache bookkeeping that fails
+before any device call, the reference's CPU tests for the PopKV subset
+(tests/test_popkv.py:38-64), the event pool with a fake clock
+(tests/test_mlp_fairness.py:31-58 style), the workload generator and the
+C ABI's exports."""
+from __future__ import annotations
+
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from popkv_amd import _native, decode_runtime, popkv, popkv_cuda, sparse_kernels, topk, workloads
+
+ROOT = Path(__file__).resolve().parent.parent
+GOLDEN = json.loads((ROOT / "tests" / "golden" / "reference_kats.json").read_text())
+
+
+# ---------------------------------------------------------------- reference CPU tests
+
+def test_public_methods_include_normal_ablation():
+    assert popkv.METHODS == tuple(GOLDEN["methods"]["value"])
+
+
+def test_sparse_methods_skip_configured_full_layers():
+    c = GOLDEN["sparse_layer_indices"]
+    assert popkv._sparse_layer_indices(c["num_layers"], tuple(c["full_layers"])) == tuple(c["expected"])
+
+
+def test_current_token_is_always_reserved():
+    c = GOLDEN["append_current"]
+    actual = popkv._append_current(torch.tensor(c["selected"]), c["num_tokens"])
+    assert torch.equal(actual[:, -1], torch.tensor(c["expected_last_column"]))
+    assert actual.dtype == torch.long and actual.shape == (2, 3)
+
+
+def test_release_configuration_is_explicit():
+    c = GOLDEN["retrieval_config"]
+    popkv.RetrievalConfig().validate()
+    popkv.RetrievalConfig(fier_kernel="fier").validate()
+    for size in c["valid_group_sizes"]:
+        popkv.RetrievalConfig(group_size=size).validate()
+    for size in c["invalid_group_sizes"]:
+        with pytest.raises(ValueError):
+            popkv.RetrievalConfig(group_size=size).validate()
+    for size in c["valid_dim_group_sizes"]:
+        popkv.RetrievalConfig(dim_group_size=size).validate()
+    for size in c["invalid_dim_group_sizes"]:
+        with pytest.raises(ValueError):
+            popkv.RetrievalConfig(dim_group_size=size).validate()
+
+
+def test_config_rules():
+    with pytest.raises(ValueError, match="budget"):
+        popkv.RetrievalConfig(budget=1).validate()
+    with pytest.raises(ValueError, match="non-specialized"):
+        popkv.RetrievalConfig(group_size=5, dim_group_size=64).validate()
+    with pytest.raises(ValueError, match="requires dim_group_size"):
+        popkv.RetrievalConfig(dim_kernel="g64-u32", dim_group_size=32).validate()
+    for method, (tg, g) in popkv.POPKV_PRESETS.items():
+        cfg = popkv.RetrievalConfig.preset(method)
+        cfg.validate()
+        assert (cfg.group_size, cfg.dim_group_size) == (tg, g)
+    with pytest.raises(ValueError):
+        popkv.RetrievalConfig.preset("popkv")
+
+
+# ---------------------------------------------------------------- validation before the device
+
+def test_pack_keys_rejects_non_cuda_and_bad_groups():
+    keys = torch.zeros(2, 8, 128)
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        popkv_cuda.pack_keys(keys)
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        popkv_cuda.pack_keys_into(keys, (None,) * 4, token_offset=0)
+    with pytest.raises(ValueError, match="token_group_size"):
+        popkv_cuda._validate_token_group_size(0)
+    with pytest.raises(ValueError, match="token_group_size"):
+        popkv_cuda._validate_token_group_size(4097)
+    with pytest.raises(ValueError, match="dim_group_size"):
+        popkv_cuda._validate_dim_group_size(8)
+    assert popkv_cuda._validate_dim_kernel(64, None) == "g64-u32"
+    assert popkv_cuda._validate_dim_kernel(64, "g64-u64") == "g64-u64"
+    with pytest.raises(ValueError, match="dim_kernel"):
+        popkv_cuda._validate_dim_kernel(16, "g99")
+    with pytest.raises(ValueError, match="requires dim_group_size"):
+        popkv_cuda._validate_dim_kernel(16, "g32")
+
+
+def test_query_and_score_reject_non_cuda():
+    q = torch.zeros(1, 8, 128)
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        popkv_cuda.query_encode(q)
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        popkv_cuda.allocate_query_encode_outputs(q)
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        popkv_cuda.score(q, (None,) * 4, head_to_kv=torch.zeros(8, dtype=torch.long), tokens=1)
+    with pytest.raises(ValueError, match="encoded_query"):
+        popkv_cuda.score_encoded((q,), (None,) * 4, head_to_kv=torch.zeros(8, dtype=torch.long), tokens=1)
+    with pytest.raises(ValueError, match="packed must contain"):
+        popkv_cuda.score_encoded((q,) * 4, (None,) * 3, head_to_kv=torch.zeros(8, dtype=torch.long), tokens=1)
+    with pytest.raises(ValueError, match="contiguous CUDA tensors"):
+        popkv_cuda.score_encoded((q,) * 4, (None,) * 4, head_to_kv=torch.zeros(8, dtype=torch.long), tokens=1)
+
+
+def test_attention_validation():
+    q = torch.zeros(8, 128)
+    k = torch.zeros(2, 16, 128)
+    idx = torch.zeros(8, 4, dtype=torch.long)
+    h2k = torch.zeros(8, dtype=torch.long)
+    with pytest.raises(ValueError, match="ranks"):
+        sparse_kernels.indexed_attention_split_partial(q[0], k, k, k[:, 0], k[:, 0], idx, h2k)
+    with pytest.raises(ValueError, match="indices"):
+        sparse_kernels.indexed_attention_split_partial(q, k, k, k[:, 0], k[:, 0], idx[:4], h2k)
+    with pytest.raises(ValueError, match="valid mask"):
+        sparse_kernels.indexed_attention_split_partial(q, k, k, k[:, 0], k[:, 0], idx, h2k,
+                                                       torch.ones(8, 3, dtype=torch.bool))
+    with pytest.raises(ValueError, match="multiple of 16"):
+        sparse_kernels.indexed_attention_split_partial(q, k, k, k[:, 0], k[:, 0], idx, h2k, split_tokens=20)
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        sparse_kernels.indexed_attention_split_partial(q, k, k, k[:, 0], k[:, 0], idx, h2k)
+    with pytest.raises(ValueError, match="CUDA float32"):
+        sparse_kernels.indexed_attention_split_merge(torch.zeros(8, 1, 130), q)
+
+
+def test_topk_validation():
+    with pytest.raises(ValueError, match="CUDA"):
+        topk.topk_indices(torch.zeros(2, 10, dtype=torch.float16), 3)
+
+
+def test_append_reserve_exhausted_before_device_call():
+    """popkv.py:445-446: raises before any kernel runs."""
+    packed = tuple(torch.zeros(2, 8, 4, dtype=torch.int32) for _ in range(2)) + \
+        tuple(torch.zeros(2, 8, 2, dtype=torch.float16) for _ in range(2))
+    cache = popkv.PopKVCache(group_size=8, dim_group_size=64, token_count=8, sealed_tokens=8,
+                             packed=packed, active_keys=torch.zeros(2, 0, 128))
+    with pytest.raises(RuntimeError, match="reserve exhausted"):
+        popkv.append_popkv(cache, torch.zeros(2, 1, 128))
+    caches = popkv.RetrievalCaches("popkv-s", {0: popkv.PopKVCache(8, 64, 8, 8, packed, torch.zeros(2, 0, 128))})
+    with pytest.raises(RuntimeError, match="reserve exhausted"):
+        popkv.append_retrieval_caches(caches, [torch.zeros(1, 2, 1, 128)])
+
+
+def test_build_cache_validation():
+    keys = torch.zeros(2, 8, 128)
+    with pytest.raises(ValueError, match="group_size"):
+        popkv.build_popkv_cache(keys, group_size=0, reserve_tokens=1)
+    with pytest.raises(ValueError, match="non-specialized"):
+        popkv.build_popkv_cache(keys, group_size=5, dim_group_size=64, reserve_tokens=1)
+    with pytest.raises(ValueError, match="dim_group_size"):
+        popkv.build_popkv_cache(keys, group_size=8, dim_group_size=8, reserve_tokens=1)
+
+
+def test_static_cache_append_and_exhaustion():
+    cache = popkv.StaticKVCache([torch.zeros(1, 2, 4, 8)], [torch.zeros(1, 2, 4, 8)], length=3, capacity=4)
+    popkv.append_kv(cache, [torch.ones(1, 2, 1, 8)], [torch.full((1, 2, 1, 8), 2.0)])
+    assert cache.length == 4
+    assert torch.equal(cache.key_storage[0][:, :, 3], torch.ones(1, 2, 8))
+    with pytest.raises(RuntimeError, match="capacity exhausted"):
+        popkv.append_kv(cache, [torch.ones(1, 2, 1, 8)], [torch.ones(1, 2, 1, 8)])
+
+
+# ---------------------------------------------------------------- event pool (fake clock)
+
+class _FakeEvent:
+    clock = 0.0
+
+    def __init__(self, enable_timing=True):
+        self.t = None
+
+    def record(self, stream=None):
+        _FakeEvent.clock += 1.5
+        self.t = _FakeEvent.clock
+
+    def synchronize(self):
+        pass
+
+    def elapsed_time(self, other):
+        return other.t - self.t
+
+
+class _FakeStream:
+    def synchronize(self):
+        pass
+
+
+class _FakeDevice:
+    def __init__(self, device):
+        pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False
+
+
+def test_event_pool_and_stage_timer(monkeypatch):
+    monkeypatch.setattr(torch.cuda, "Event", _FakeEvent)
+    monkeypatch.setattr(torch.cuda, "device", _FakeDevice)
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: _FakeStream())
+    pool = decode_runtime.DecodeEventPool(torch.device("cpu"), 1 + len(decode_runtime.RETRIEVAL_STAGES))
+    timer = decode_runtime.StageTimer(pool)
+    for name in decode_runtime.RETRIEVAL_STAGES:
+        timer.mark(name)
+    totals = timer.finish()
+    assert totals["total"] == pytest.approx(sum(totals[n] for n in decode_runtime.RETRIEVAL_STAGES))
+    with pytest.raises(ValueError, match="unknown decode stage"):
+        timer.mark("mlp")
+    with pytest.raises(RuntimeError, match="exhausted"):
+        pool.record()
+
+
+# ---------------------------------------------------------------- workloads
+
+def test_algorithmic_bytes_match_baseline_table():
+    b = workloads.algorithmic_bytes(workloads.C1)
+    assert (b["score"], b["select"], b["attention"], b["encode"]) == (12582528, 2621376, 67649536, 9728)
+    assert b["step"] == 82863168
+    sweep = [round(workloads.algorithmic_bytes(workloads.c3(c))["step"] / 1e6, 2) for c in workloads.C3_CONTEXTS]
+    assert sweep == [70.02, 71.85, 75.52, 82.86, 97.54, 126.90]
+
+
+def test_workload_generator_is_deterministic():
+    w = workloads.scaled(workloads.C1, context=512, budget=64)
+    a, b = workloads.make_layer(w), workloads.make_layer(w)
+    assert torch.equal(a.keys.view(torch.int16), b.keys.view(torch.int16))
+    assert torch.equal(a.queries.view(torch.int16), b.queries.view(torch.int16))
+    assert a.keys.dtype == torch.bfloat16 and a.keys.shape == (8, 512, 128) and a.queries.shape == (32, 128)
+    # outlier channels: 4 per KV head with ~10x the spread of the rest
+    std = a.keys.float().std(dim=1)
+    assert ((std > 5).sum(dim=1) == 4).all()
+    c0 = workloads.make_layer(workloads.C0)
+    assert c0.keys.dtype == torch.float32 and c0.keys.shape == (2, 4096, 128)
+
+
+# ---------------------------------------------------------------- C ABI
+
+def _header_functions() -> set[str]:
+    text = _native.HEADER_PATH.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(popkv_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _native.lib()
+    declared = _header_functions()
+    assert declared == set(_native.exported_symbols())
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_library_host_only_entry_points():
+    lib = _native.lib()
+    assert lib.popkv_version().decode().startswith("popkv-hip")
+    assert lib.popkv_status_string(-2).decode() == "Pop-KV cache capacity exceeded"
+    assert lib.popkv_layer_step_workspace_bytes(32, 32767, 4096, 64) > 32 * 32767 * 2
+    assert lib.popkv_layer_step_workspace_bytes(32, 32767, 1, 64) == 0
+    assert lib.popkv_score_workspace_bytes(1, 32, 128, 64) > 0
+    # argument errors are reported before anything touches a device
+    st = lib.popkv_pack(None, 2, 8, 10, 128, 1280, None, None, None, None, 10, 0, 64, 64, None)
+    assert st == -1 and "null" in lib.popkv_last_error().decode()
+    fake = 0x1000
+    st = lib.popkv_pack(fake, 2, 8, 10, 128, 1280, fake, fake, fake, fake, 12, 3, 64, 64, None)
+    assert st == -2 and "capacity exceeded" in lib.popkv_last_error().decode()
+    st = lib.popkv_topk_select(fake, 4, 10, 10, 11, 10, fake, 0, 12, None)
+    assert st == -1
+    st = lib.popkv_topk_select(fake, 4, 200000, 200000, 11, 10, fake, 0, 12, None)
+    assert st == -4
+    with pytest.raises(RuntimeError, match="capacity exceeded"):
+        _native.check(lib.popkv_pack(fake, 2, 8, 10, 128, 1280, fake, fake, fake, fake, 12, 3, 64, 64, None))
