@@ -104,45 +104,50 @@ def main() -> int:
         step(i)
     eager_ms = timed(step, args.steps)
 
-    # ---- HIP-graph replay of N_BUFFERS consecutive layer steps
-    graph_ms = None
-    if not args.no_graph:
+    def graph_timed(fn, reps: int):
+        """Average ms per call of fn(i), captured N_BUFFERS calls to a HIP
+        graph (after a warm-up on a side stream) and replayed `reps` times."""
         g = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(dev)
         side.wait_stream(stream)
         with torch.cuda.stream(side):
             for i in range(N_BUFFERS):
-                step(i)
+                fn(i)
         stream.wait_stream(side)
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
             for i in range(N_BUFFERS):
-                step(i)
-        ref_out = [o.clone() for o in outs]
-        reps = max(1, args.steps // N_BUFFERS)
-        for _ in range(max(1, args.warmup // N_BUFFERS)):
+                fn(i)
+        for _ in range(2):
             g.replay()
-        graph_ms = timed(lambda i: g.replay(), reps) / N_BUFFERS
+        return timed(lambda i: g.replay(), reps) / N_BUFFERS
+
+    # ---- HIP-graph replay of N_BUFFERS consecutive layer steps
+    graph_ms = None
+    reps = max(1, args.steps // N_BUFFERS)
+    if not args.no_graph:
+        eager_out = [o.clone() for o in outs]
+        graph_ms = graph_timed(step, reps)
         torch.cuda.synchronize()
-        if not all(torch.equal(a, b) for a, b in zip(outs, ref_out)):
+        if not all(torch.equal(a, b) for a, b in zip(outs, eager_out)):
             print("graph replay changed the layer outputs", file=sys.stderr)
             return 1
     ms_per_step = graph_ms if graph_ms is not None else eager_ms
 
     # ---- per-stage kernels (same inputs, stand-alone entry points)
+    stage_timer = timed if args.no_graph else graph_timed
     enc = popkv_cuda.query_encode(q.unsqueeze(0).contiguous(), dim_group_size=w.dim_group)
-    score_ms = timed(lambda i: popkv_cuda.score_encoded(enc, sets[i % N_BUFFERS][2].packed, head_to_kv=mapping,
-                                                        tokens=L, dim_group_size=w.dim_group), args.steps)
+    score_ms = stage_timer(lambda i: popkv_cuda.score_encoded(enc, sets[i % N_BUFFERS][2].packed, head_to_kv=mapping,
+                                                              tokens=L, dim_group_size=w.dim_group), reps)
     scores = popkv_cuda.score_encoded(enc, sets[0][2].packed, head_to_kv=mapping, tokens=L,
                                       dim_group_size=w.dim_group)
     score_bufs = [scores.clone() for _ in range(N_BUFFERS)]
-    select_ms = timed(lambda i: topk.select_with_current(score_bufs[i % N_BUFFERS], kk, L + 1), args.steps)
+    select_ms = stage_timer(lambda i: topk.select_with_current(score_bufs[i % N_BUFFERS], kk, L + 1), reps)
     indices = topk.select_with_current(scores, kk, L + 1)
-    attn_ms = timed(lambda i: sparse_kernels.indexed_attention_split_partial(
-        q, sets[i % N_BUFFERS][0], sets[i % N_BUFFERS][1], cur_k, cur_v, indices, mapping, split_tokens=256),
-        args.steps)
-    encode_ms = timed(lambda i: popkv_cuda.query_encode(q.unsqueeze(0).contiguous(), dim_group_size=w.dim_group),
-                      args.steps)
+    attn_ms = stage_timer(lambda i: sparse_kernels.indexed_attention_split_partial(
+        q, sets[i % N_BUFFERS][0], sets[i % N_BUFFERS][1], cur_k, cur_v, indices, mapping, split_tokens=256), reps)
+    encode_ms = stage_timer(lambda i: popkv_cuda.query_encode(q.unsqueeze(0).contiguous(),
+                                                              dim_group_size=w.dim_group), reps)
     unique_rows = int(sum(torch.unique(indices[h * 4:(h + 1) * 4].flatten()).numel() for h in range(w.kv_heads)))
 
     step_gbps = alg["step"] / (ms_per_step * 1e-3) / 1e9

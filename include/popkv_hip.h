@@ -136,7 +136,8 @@ int popkv_sparse_attention_partial(const void* queries, int32_t dtype,
                                    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t selected,
                                    int32_t split_tokens, float* partials, void* stream);
 
-/* Log-sum-exp merge of split states into output [QH, D] of out_dtype.
+/* Log-sum-exp merge of split states into output [QH, D] of out_dtype
+ * (at most 1024 splits per head).
  * Replaces indexed_attention_split_merge (sparse_kernels.py:367-387,
  * Triton kernel :297-318). */
 int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t splits,
@@ -146,10 +147,13 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
 /* One decode step of one sparse layer (batch 1, head_dim 128): query encode,
  * popcount score over `tokens` cached tokens, per-head top-k with
  * k = min(budget-1, tokens) plus the current token (index `tokens`), and
- * 256-token split sparse attention with an in-kernel log-sum-exp merge.
+ * 256-token split sparse attention with the log-sum-exp merge.
  * queries/prefix/current K/V share `dtype`; output [QH, 128] has `dtype`.
  * indices_out (int64 [QH, k+1]) may be NULL; when given, the selection is
- * also written there.  Needs popkv_layer_step_workspace_bytes() bytes.
+ * also written there.  Needs popkv_layer_step_workspace_bytes() bytes of
+ * workspace, 16-byte aligned and zero-filled before its first use; every call
+ * leaves the workspace's histogram region zeroed again, so it can be reused
+ * by later calls (calls sharing one workspace must be stream-ordered).
  * Replaces the PopKV branch of LlamaSparseDecoder.decode (reference
  * popkv.py:1076-1115): query_encode, score_encoded, torch.topk +
  * _append_current, indexed_attention_split_partial and _merge. */

@@ -7,11 +7,12 @@
 //
 // Partial kernel: one workgroup of 4 wave64s per (query head, split).  A row
 // of D bf16 values is read by LPR = D/8 lanes with one 16-byte load each, so
-// a wave covers 64/LPR rows per instruction.  Each lane first loads the
-// indices of its rows, then issues the K and V loads of a whole batch of rows
-// before using any of them (deep memory-level parallelism for the random
-// 256-byte gathers).  Logits are reduced across the LPR lanes of a row with
-// xor shuffles; every row slot keeps an online-softmax state (m, l, acc[8]),
+// a wave covers 64/LPR rows per instruction.  The split's indices are staged
+// in LDS with one coalesced load; each lane then issues the K and V loads of
+// a whole batch of rows before using any of them (deep memory-level
+// parallelism for the random 256-byte gathers).  Logits are reduced across
+// the LPR lanes of a row with DPP row permutations (VALU only); every row
+// slot keeps an online-softmax state (m, l, acc[8]),
 // slots are merged within the wave and then across waves through LDS, and
 // the split's (m, l, acc[D]) is written as float32.
 //
@@ -20,9 +21,10 @@
 // or with valid_mask == 0 are skipped.
 //
 // Merge: out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}, M = max_s m_s,
-// cast to the output dtype.  The layer-step variant fuses it into the partial
-// kernel: the last workgroup of a head to finish (device-scope counter)
-// merges that head's splits and re-arms the counter.
+// cast to the output dtype, one workgroup per query head.  (A last-block
+// merge inside the partial kernel would need an agent-scope release per
+// workgroup, which on gfx950 writes back the XCD's L2 each time; a separate
+// launch is far cheaper.)
 #include "device_common.h"
 #include "kernels.h"
 
@@ -31,6 +33,7 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
+constexpr int kAttnStage = 1024;  // indices of one split staged in LDS
 
 template <typename T>
 __device__ __forceinline__ void load_row8(const T* p, int dim0, int d, float v[8]) {
@@ -57,22 +60,49 @@ __device__ __forceinline__ void merge_state(SoftmaxState& a, float m2, float l2,
     a.m = mm;
 }
 
-// Merge `nsplit` states [(m, l, acc[D])] into out[d] for d = threadIdx.x < D.
+// Merge `nsplit` states [(m, l, acc[D])] of one head into out[0..D).  The
+// states are first staged into LDS with one coalesced burst, so the whole
+// merge pays a single memory latency.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeMaxFloats = 16384;  // 64 KB of staged state
+constexpr int kMergeMaxSplits = 1024;
+
 template <typename T>
-__device__ __forceinline__ void merge_splits(const float* st, int nsplit, int d, T* out) {
-    const int dim = threadIdx.x;
-    if (dim >= d) return;
-    float mx = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, st[s * (d + 2)]);
-    float den = 0.0f, num = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-        const float m = st[s * (d + 2)];
-        if (m == -INFINITY) continue;
-        const float w = __expf(m - mx);
-        den += st[s * (d + 2) + 1] * w;
-        num += st[s * (d + 2) + 2 + dim] * w;
+__device__ __forceinline__ void merge_splits(const float* __restrict__ st, int nsplit, int d, T* out) {
+    __shared__ float s_state[kMergeMaxFloats];
+    __shared__ float s_w[kMergeMaxSplits];
+    __shared__ float s_den;
+    const int n = nsplit * (d + 2);
+    const bool staged = n <= kMergeMaxFloats;
+    if (staged) {
+        for (int i = threadIdx.x; i < n; i += kMergeThreads) s_state[i] = st[i];
+        __syncthreads();
     }
-    Elem<T>::store(out, dim, num / den);
+    const float* src = staged ? s_state : st;
+    // split weights e^{m_s - M} (0 for fully masked splits) and the denominator
+    if (threadIdx.x < kWave) {
+        float mx = -INFINITY;
+        for (int s = threadIdx.x; s < nsplit; s += kWave) mx = fmaxf(mx, src[s * (d + 2)]);
+        mx = wave_max(mx);
+        float den = 0.0f;
+        for (int s = threadIdx.x; s < nsplit; s += kWave) {
+            const float m = src[s * (d + 2)];
+            const float w = m == -INFINITY ? 0.0f : __expf(m - mx);
+            s_w[s] = w;
+            den += src[s * (d + 2) + 1] * w;
+        }
+        den = wave_sum(den);
+        if (threadIdx.x == 0) s_den = den;
+    }
+    __syncthreads();
+    for (int dim = threadIdx.x; dim < d; dim += kMergeThreads) {
+        float num = 0.0f;
+        for (int s = 0; s < nsplit; ++s) {
+            const float w = s_w[s];
+            if (w != 0.0f) num += src[s * (d + 2) + 2 + dim] * w;
+        }
+        Elem<T>::store(out, dim, num / s_den);
+    }
 }
 
 // Raw storage of 8 consecutive elements: one 16-byte packet for 16-bit types,
@@ -101,14 +131,14 @@ template <> struct Raw8<float> {
     }
 };
 
-template <typename T, typename IdxT, int LPR, int NB, bool FUSED>
+template <typename T, typename IdxT, int LPR, int NB>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
     int64_t k_hs, int64_t k_ts, int64_t v_hs, int64_t v_ts, int64_t prefix_tokens,
     const T* __restrict__ cur_k, const T* __restrict__ cur_v,
     const IdxT* __restrict__ idx, int64_t idx_stride, const uint8_t* __restrict__ valid,
     const int64_t* __restrict__ head_to_kv, int kv_heads, int d, int64_t selected, int split, float scale,
-    float* __restrict__ partials, int nsplit, unsigned int* __restrict__ counters, T* __restrict__ out) {
+    float* __restrict__ partials, int nsplit) {
     constexpr int SLOTS = kWave / LPR;               // row slots per wave
     constexpr int ROWS_PER_PASS = SLOTS * kAttnWaves;
     const int h = blockIdx.y;
@@ -134,6 +164,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const IdxT* irow = idx + static_cast<int64_t>(h) * idx_stride + row0;
     const uint8_t* vrow = valid ? valid + static_cast<int64_t>(h) * idx_stride + row0 : nullptr;
 
+    // Stage this split's indices (and validity) in LDS with coalesced loads;
+    // -1 marks a skipped row.  Out-of-range indices are clamped into the
+    // cache (as the reference's min(token, prefix_tokens - 1)), never
+    // dereferenced.
+    __shared__ int64_t s_tok[kAttnStage];
+    const bool staged = rows_here <= kAttnStage;
+    if (staged) {
+        for (int r = threadIdx.x; r < rows_here; r += kAttnThreads) {
+            const int64_t t = static_cast<int64_t>(irow[r]);
+            const bool live = vrow == nullptr || vrow[r] != 0;
+            s_tok[r] = !live ? -1 : (t == prefix_tokens ? t : min(max(t, static_cast<int64_t>(0)), prefix_tokens - 1));
+        }
+        __syncthreads();
+    }
+
     SoftmaxState st;
     st.m = -INFINITY;
     st.l = 0.0f;
@@ -146,11 +191,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int64_t r = base + static_cast<int64_t>(b) * ROWS_PER_PASS + slot;
-            live[b] = r < rows_here && (vrow == nullptr || vrow[r] != 0);
-            const int64_t t = live[b] ? static_cast<int64_t>(irow[r]) : 0;
-            // Out-of-range indices are clamped into the cache (as the
-            // reference's min(token, prefix_tokens - 1)), never dereferenced.
-            tok[b] = t == prefix_tokens ? t : min(max(t, static_cast<int64_t>(0)), prefix_tokens - 1);
+            int64_t t = -1;
+            if (r < rows_here) {
+                if (staged) {
+                    t = s_tok[r];
+                } else {
+                    const int64_t raw = static_cast<int64_t>(irow[r]);
+                    const bool ok = vrow == nullptr || vrow[r] != 0;
+                    t = !ok ? -1 : (raw == prefix_tokens ? raw : min(max(raw, static_cast<int64_t>(0)), prefix_tokens - 1));
+                }
+            }
+            live[b] = t >= 0;
+            tok[b] = live[b] ? t : 0;
         }
         Raw8<T> kr[NB], vr[NB];
 #pragma unroll
@@ -170,8 +222,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
             float dot = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) dot = fmaf(qv[i], kr[b].get(i), dot);
+            if constexpr (LPR <= 16) {
+                dot = row_sum<LPR>(dot);
+            } else {
 #pragma unroll
-            for (int m = 1; m < LPR; m <<= 1) dot += __shfl_xor(dot, m);
+                for (int m = 1; m < LPR; m <<= 1) dot += __shfl_xor(dot, m);
+            }
             logit[b] = live[b] ? dot * scale : -INFINITY;
         }
         float bm = -INFINITY;
@@ -232,100 +288,71 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         if (dim == 0) { dst[0] = mx; dst[1] = l; }
     }
 
-    if constexpr (FUSED) {
-        __shared__ unsigned int s_last;
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const unsigned int prev = atomicAdd(&counters[h], 1u);
-            s_last = prev == static_cast<unsigned int>(nsplit - 1) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (s_last) {
-            __threadfence();
-            merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (d + 2), nsplit, d,
-                            out + static_cast<int64_t>(h) * d);
-            if (threadIdx.x == 0) counters[h] = 0u;
-        }
-    }
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ partials, int nsplit, int d,
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict__ partials, int nsplit, int d,
                                                          T* __restrict__ out) {
     const int h = blockIdx.x;
     merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (d + 2), nsplit, d,
                     out + static_cast<int64_t>(h) * d);
 }
 
-__global__ void zero_u32_kernel(unsigned int* p, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
 
-template <typename T, typename IdxT, int LPR, bool FUSED>
-hipError_t launch_partial_t(const T* q, const T* kc, const T* vc, int64_t k_hs, int64_t k_ts, int64_t v_hs,
-                            int64_t v_ts, int64_t prefix_tokens, const T* ck, const T* cv, const IdxT* idx,
-                            int64_t idx_stride, const uint8_t* valid, const int64_t* h2k, int qh, int kvh, int d,
-                            int64_t selected, int split, float* partials, unsigned int* counters, T* out,
-                            hipStream_t stream) {
-    const int nsplit = static_cast<int>((selected + split - 1) / split);
-    const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(d)));
+// Typed arguments of one partial-attention launch.
+template <typename T, typename IdxT>
+struct PartialArgs {
+    const T *q, *kc, *vc, *ck, *cv;
+    int64_t k_hs, k_ts, v_hs, v_ts, prefix_tokens;
+    const IdxT* idx;
+    int64_t idx_stride;
+    const uint8_t* valid;
+    const int64_t* h2k;
+    int qh, kvh, d;
+    int64_t selected;
+    int split;
+    float* partials;
+};
+
+template <int LPR, typename T, typename IdxT>
+hipError_t launch_partial_lpr(const PartialArgs<T, IdxT>& a, hipStream_t stream) {
     constexpr int NB = (sizeof(T) == 4 || LPR == 32) ? 8 : 16;
-    dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(qh));
-    hipLaunchKernelGGL((attn_partial_kernel<T, IdxT, LPR, NB, FUSED>), grid, dim3(kAttnThreads), 0, stream, q, kc,
-                       vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx, idx_stride, valid, h2k, kvh, d, selected,
-                       split, scale, partials, nsplit, counters, out);
+    const int nsplit = static_cast<int>((a.selected + a.split - 1) / a.split);
+    const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(a.d)));
+    dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(a.qh));
+    hipLaunchKernelGGL((attn_partial_kernel<T, IdxT, LPR, NB>), grid, dim3(kAttnThreads), 0, stream, a.q, a.kc, a.vc,
+                       a.k_hs, a.k_ts, a.v_hs, a.v_ts, a.prefix_tokens, a.ck, a.cv, a.idx, a.idx_stride, a.valid,
+                       a.h2k, a.kvh, a.d, a.selected, a.split, scale, a.partials, nsplit);
     return hipGetLastError();
 }
 
-template <typename T, typename IdxT, bool FUSED>
-hipError_t launch_partial_lpr(const T* q, const T* kc, const T* vc, int64_t k_hs, int64_t k_ts, int64_t v_hs,
-                              int64_t v_ts, int64_t prefix_tokens, const T* ck, const T* cv, const IdxT* idx,
-                              int64_t idx_stride, const uint8_t* valid, const int64_t* h2k, int qh, int kvh, int d,
-                              int64_t selected, int split, float* partials, unsigned int* counters, T* out,
-                              hipStream_t stream) {
-    if (d <= 64)
-        return launch_partial_t<T, IdxT, 8, FUSED>(q, kc, vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx,
-                                                   idx_stride, valid, h2k, qh, kvh, d, selected, split, partials, counters,
-                                                   out, stream);
-    if (d <= 128)
-        return launch_partial_t<T, IdxT, 16, FUSED>(q, kc, vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx,
-                                                    idx_stride, valid, h2k, qh, kvh, d, selected, split, partials,
-                                                    counters, out, stream);
-    return launch_partial_t<T, IdxT, 32, FUSED>(q, kc, vc, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck, cv, idx,
-                                                idx_stride, valid, h2k, qh, kvh, d, selected, split, partials, counters,
-                                                out, stream);
+template <typename T, typename IdxT>
+hipError_t launch_partial_t(const PartialArgs<T, IdxT>& a, hipStream_t stream) {
+    if (a.d <= 64) return launch_partial_lpr<8>(a, stream);
+    if (a.d <= 128) return launch_partial_lpr<16>(a, stream);
+    return launch_partial_lpr<32>(a, stream);
 }
 
 template <typename T>
 hipError_t launch_partial_dt(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t k_ts, int64_t v_hs,
                              int64_t v_ts, int64_t prefix_tokens, const void* ck, const void* cv, const void* idx,
                              int index_dtype, int64_t idx_stride, const uint8_t* valid, const int64_t* h2k, int qh,
-                             int kvh, int d, int64_t selected, int split, float* partials, unsigned int* counters, void* out,
-                             hipStream_t stream) {
+                             int kvh, int d, int64_t selected, int split, float* partials, hipStream_t stream) {
     const T* q_ = static_cast<const T*>(q);
     const T* k_ = static_cast<const T*>(kc);
     const T* v_ = static_cast<const T*>(vc);
     const T* ck_ = static_cast<const T*>(ck);
     const T* cv_ = static_cast<const T*>(cv);
-    T* o_ = static_cast<T*>(out);
-    if (counters != nullptr) {
-        if (index_dtype == POPKV_INDEX_I32)
-            return launch_partial_lpr<T, int32_t, true>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
-                                                         static_cast<const int32_t*>(idx), idx_stride, valid, h2k, qh, kvh,
-                                                         d, selected, split, partials, counters, o_, stream);
-        return launch_partial_lpr<T, int64_t, true>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
-                                                     static_cast<const int64_t*>(idx), idx_stride, valid, h2k, qh, kvh, d,
-                                                     selected, split, partials, counters, o_, stream);
+    if (index_dtype == POPKV_INDEX_I32) {
+        PartialArgs<T, int32_t> a{q_, k_, v_, ck_, cv_, k_hs, k_ts, v_hs, v_ts, prefix_tokens,
+                                  static_cast<const int32_t*>(idx), idx_stride, valid, h2k, qh, kvh, d, selected,
+                                  split, partials};
+        return launch_partial_t(a, stream);
     }
-    if (index_dtype == POPKV_INDEX_I32)
-        return launch_partial_lpr<T, int32_t, false>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
-                                                      static_cast<const int32_t*>(idx), idx_stride, valid, h2k, qh, kvh, d,
-                                                      selected, split, partials, nullptr, o_, stream);
-    return launch_partial_lpr<T, int64_t, false>(q_, k_, v_, k_hs, k_ts, v_hs, v_ts, prefix_tokens, ck_, cv_,
-                                                  static_cast<const int64_t*>(idx), idx_stride, valid, h2k, qh, kvh, d,
-                                                  selected, split, partials, nullptr, o_, stream);
+    PartialArgs<T, int64_t> a{q_, k_, v_, ck_, cv_, k_hs, k_ts, v_hs, v_ts, prefix_tokens,
+                              static_cast<const int64_t*>(idx), idx_stride, valid, h2k, qh, kvh, d, selected, split,
+                              partials};
+    return launch_partial_t(a, stream);
 }
 
 }  // namespace
@@ -336,32 +363,29 @@ hipError_t launch_attention_partial(const void* queries, int dtype, const void* 
                                     const void* current_v, const void* indices, int index_dtype,
                                     int64_t index_row_stride, const uint8_t* valid_mask, const int64_t* head_to_kv,
                                     int q_heads, int kv_heads, int head_dim, int64_t selected, int split_tokens,
-                                    float* partials,
-                                    unsigned int* merge_counters, void* merge_output, hipStream_t stream) {
+                                    float* partials, hipStream_t stream) {
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_partial_dt<float>(queries, prefix_k, prefix_v, k_head_stride, k_token_stride, v_head_stride,
                                             v_token_stride, prefix_tokens, current_k, current_v, indices, index_dtype,
-                                            index_row_stride, valid_mask, head_to_kv, q_heads, kv_heads, head_dim, selected,
-                                            split_tokens, partials, merge_counters, merge_output, stream);
+                                            index_row_stride, valid_mask, head_to_kv, q_heads, kv_heads, head_dim,
+                                            selected, split_tokens, partials, stream);
         case POPKV_DTYPE_F16:
             return launch_partial_dt<f16_t>(queries, prefix_k, prefix_v, k_head_stride, k_token_stride, v_head_stride,
                                             v_token_stride, prefix_tokens, current_k, current_v, indices, index_dtype,
-                                            index_row_stride, valid_mask, head_to_kv, q_heads, kv_heads, head_dim, selected,
-                                            split_tokens, partials, merge_counters, merge_output, stream);
+                                            index_row_stride, valid_mask, head_to_kv, q_heads, kv_heads, head_dim,
+                                            selected, split_tokens, partials, stream);
         default:
             return launch_partial_dt<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, k_token_stride,
                                              v_head_stride, v_token_stride, prefix_tokens, current_k, current_v,
                                              indices, index_dtype, index_row_stride, valid_mask, head_to_kv, q_heads,
-                                             kv_heads, head_dim, selected, split_tokens, partials, merge_counters,
-                                             merge_output,
-                                             stream);
+                                             kv_heads, head_dim, selected, split_tokens, partials, stream);
     }
 }
 
 hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t splits, int head_dim, void* output,
                                   int out_dtype, hipStream_t stream) {
-    dim3 grid(static_cast<unsigned>(q_heads)), block(256);
+    dim3 grid(static_cast<unsigned>(q_heads)), block(kMergeThreads);
     const int ns = static_cast<int>(splits);
     switch (out_dtype) {
         case POPKV_DTYPE_F32:
@@ -380,10 +404,5 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
     return hipGetLastError();
 }
 
-hipError_t launch_zero_u32(unsigned int* p, int64_t n, hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, p, n);
-    return hipGetLastError();
-}
 
 }  // namespace popkv

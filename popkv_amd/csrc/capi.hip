@@ -39,6 +39,7 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 constexpr int64_t kMaxSelectTokens = 1024 * 128;
+constexpr int64_t kMaxGroupHeads = 64;
 constexpr int kLayerSplit = 256;
 constexpr size_t kAlign = 256;
 
@@ -46,25 +47,20 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Workspace layout of popkv_layer_step (batch 1, head_dim 128).
 struct StepLayout {
-    size_t q_sign, q_mag, q_low, q_delta, scores, indices, partials, counters, total;
+    size_t hist, scores, indices, partials, total;
     int64_t score_stride, k, nsplit;
 };
 
-StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget, int32_t g) {
+StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     StepLayout L{};
-    const int64_t reps = 128 / g;
     L.k = budget - 1 < tokens ? budget - 1 : tokens;
     L.nsplit = ceil_div(L.k + 1, kLayerSplit);
     L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 64) * 64;
     size_t off = 0;
-    L.q_sign = off; off = align_up(off + qh * 4 * 4);
-    L.q_mag = off; off = align_up(off + qh * 4 * 4);
-    L.q_low = off; off = align_up(off + qh * reps * 4);
-    L.q_delta = off; off = align_up(off + qh * reps * 4);
+    L.hist = off; off = align_up(off + static_cast<size_t>(qh) * 256 * 4);
     L.scores = off; off = align_up(off + static_cast<size_t>(qh * L.score_stride) * 2);
     L.indices = off; off = align_up(off + static_cast<size_t>(qh * (L.k + 1)) * 4);
     L.partials = off; off = align_up(off + static_cast<size_t>(qh * L.nsplit * (128 + 2)) * 4);
-    L.counters = off; off = align_up(off + qh * 4);
     L.total = off;
     return L;
 }
@@ -133,6 +129,7 @@ static int check_score_common(const int64_t* head_to_kv, int64_t batch, int64_t 
     if (batch <= 0 || q_heads <= 0 || kv_heads <= 0) return fail(POPKV_ERR_INVALID, "empty batch or heads");
     if (tokens <= 0 || tokens > capacity) return fail(POPKV_ERR_TOKENS, "invalid score token count");
     if (q_heads % kv_heads != 0) return fail(POPKV_ERR_INVALID, "GQA query heads must be divisible by KV heads");
+    if (q_heads / kv_heads > kMaxGroupHeads) return fail(POPKV_ERR_UNSUPPORTED, "at most 64 query heads per KV head");
     if (batch * q_heads > 65535 || batch * kv_heads > 65535) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
     return POPKV_OK;
 }
@@ -216,8 +213,7 @@ int popkv_topk_select(const void* scores, int64_t rows, int64_t row_stride, int6
     if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens per row");
     if (rows > 0x7fffffff) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
     return launched(popkv::launch_topk_select(static_cast<const uint16_t*>(scores), rows, row_stride, tokens, k,
-                                              current, indices, index_dtype, index_row_stride, nullptr,
-                                              as_stream(stream)),
+                                              current, indices, index_dtype, index_row_stride, as_stream(stream)),
                     "popkv_topk_select");
 }
 
@@ -258,7 +254,7 @@ int popkv_sparse_attention_partial(const void* queries, int32_t dtype, const voi
                                                     indices, index_dtype, selected, valid_mask, head_to_kv,
                                                     static_cast<int>(q_heads), static_cast<int>(kv_heads),
                                                     static_cast<int>(head_dim), selected,
-                                                    split_tokens, partials, nullptr, nullptr, as_stream(stream)),
+                                                    split_tokens, partials, as_stream(stream)),
                     "popkv_sparse_attention_partial");
 }
 
@@ -268,6 +264,7 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
     if (!valid_dtype(out_dtype)) return fail(POPKV_ERR_INVALID, "output must be fp32/fp16/bf16");
     if (q_heads <= 0 || q_heads > 65535 || splits <= 0 || head_dim <= 0)
         return fail(POPKV_ERR_INVALID, "partials must be [QH, splits, D+2]");
+    if (splits > 1024) return fail(POPKV_ERR_UNSUPPORTED, "merge supports at most 1024 splits per head");
     if (head_dim > 256) return fail(POPKV_ERR_UNSUPPORTED, "head_dim must be <= 256");
     return launched(popkv::launch_attention_merge(partials, static_cast<int>(q_heads), splits,
                                                   static_cast<int>(head_dim), output, out_dtype, as_stream(stream)),
@@ -276,7 +273,7 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
 
 size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t budget, int32_t dim_group_size) {
     if (q_heads <= 0 || tokens < 0 || budget <= 1 || !valid_group(dim_group_size)) return 0;
-    return step_layout(q_heads, tokens, budget, dim_group_size).total;
+    return step_layout(q_heads, tokens, budget).total;
 }
 
 int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
@@ -293,7 +290,7 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
     int st = check_score_common(head_to_kv, 1, q_heads, kv_heads, capacity, tokens, dim_group_size);
     if (st) return st;
     if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens");
-    const StepLayout L = step_layout(q_heads, tokens, budget, dim_group_size);
+    const StepLayout L = step_layout(q_heads, tokens, budget);
     if (!workspace || workspace_bytes < L.total)
         return fail(POPKV_ERR_WORKSPACE, "layer step needs %zu workspace bytes", L.total);
     if (!aligned16(workspace)) return fail(POPKV_ERR_INVALID, "workspace must be 16-byte aligned");
@@ -303,39 +300,36 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
         (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
         return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
     char* ws = static_cast<char*>(workspace);
-    int32_t* qs = reinterpret_cast<int32_t*>(ws + L.q_sign);
-    int32_t* qm = reinterpret_cast<int32_t*>(ws + L.q_mag);
-    float* ql = reinterpret_cast<float*>(ws + L.q_low);
-    float* qd = reinterpret_cast<float*>(ws + L.q_delta);
-    uint16_t* scores = reinterpret_cast<uint16_t*>(ws + L.scores);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+    uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
-    unsigned int* counters = reinterpret_cast<unsigned int*>(ws + L.counters);
     void* idx = indices_out ? static_cast<void*>(indices_out) : static_cast<void*>(ws + L.indices);
     const int idx_dtype = indices_out ? POPKV_INDEX_I64 : POPKV_INDEX_I32;
     hipStream_t s = as_stream(stream);
 
-    st = launched(popkv::launch_query_encode(queries, dtype, q_heads, 128, dim_group_size, POPKV_ENCODE_FOLD, qs, qm,
-                                             ql, qd, s),
-                  "popkv_layer_step(encode)");
-    if (st) return st;
-    // Score rows use a padded stride (a multiple of 64 tokens) so every row
-    // starts 128-byte aligned for the select kernel's loads.
-    st = launched(popkv::launch_score_d128(qs, qm, ql, qd, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
-                                           static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
-                                           static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity, tokens,
-                                           dim_group_size, scores, L.score_stride, s),
+    // 1. query encode + popcount score -> radix order keys of the fp16 scores
+    //    (rows padded to a multiple of 64 tokens, so every row starts 128-byte
+    //    aligned) + per-head high-byte key histograms
+    st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
+                                               static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
+                                               static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
+                                               tokens, dim_group_size, keys, L.score_stride, hist, s),
                   "popkv_layer_step(score)");
     if (st) return st;
-    st = launched(popkv::launch_topk_select(scores, q_heads, L.score_stride, tokens, L.k, tokens, idx, idx_dtype,
-                                            L.k + 1, counters, s),
+    // 2. top-k + current token (re-zeroes the histograms)
+    st = launched(popkv::launch_topk_select_keys(keys, hist, q_heads, L.score_stride, tokens, L.k, tokens, idx,
+                                                 idx_dtype, L.k + 1, s),
                   "popkv_layer_step(select)");
     if (st) return st;
-    return launched(popkv::launch_attention_partial(queries, dtype, prefix_k, prefix_v, k_head_stride, 128,
-                                                    v_head_stride, 128, tokens, current_k, current_v, idx, idx_dtype,
-                                                    L.k + 1, nullptr, head_to_kv, static_cast<int>(q_heads),
-                                                    static_cast<int>(kv_heads), 128,
-                                                    L.k + 1, kLayerSplit, partials, counters, output, s),
-                    "popkv_layer_step(attention)");
+    // 3. split partial attention, 4. log-sum-exp merge
+    st = launched(popkv::launch_attention_partial(queries, dtype, prefix_k, prefix_v, k_head_stride, 128,
+                                                  v_head_stride, 128, tokens, current_k, current_v, idx, idx_dtype,
+                                                  L.k + 1, nullptr, head_to_kv, static_cast<int>(q_heads),
+                                                  static_cast<int>(kv_heads), 128, L.k + 1, kLayerSplit, partials, s),
+                  "popkv_layer_step(attention)");
+    if (st) return st;
+    return launched(popkv::launch_attention_merge(partials, static_cast<int>(q_heads), L.nsplit, 128, output, dtype, s),
+                    "popkv_layer_step(merge)");
 }
 
 }  // extern "C"

@@ -120,6 +120,15 @@ __device__ __forceinline__ void finish_rep(float ls, int ln, float hs, int hn, f
     delta = hi - lo;
 }
 
+// Radix order key of an fp16 bit pattern, the map PyTorch's radix top-k
+// uses for half values: negatives bit-inverted, non-negatives with the sign
+// bit set, every NaN mapped to the largest key.  Monotone, and -0 < +0.
+__device__ __forceinline__ uint32_t order_key(uint32_t h) {
+    const bool nan = ((h & 0x7c00u) == 0x7c00u) && (h & 0x3ffu);
+    const uint32_t k = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+    return nan ? 0xffffu : k;
+}
+
 // ---- wave / block reductions --------------------------------------------
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -135,6 +144,24 @@ __device__ __forceinline__ float wave_min(float v) {
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// Sum over each row of 16 lanes (or 8-lane half rows for N = 8) with DPP
+// lane permutations -- VALU-only, no LDS traffic.  Every lane of a row ends
+// with the row's sum.  Control words: quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int N>
+__device__ __forceinline__ float row_sum(float v) {
+    static_assert(N == 8 || N == 16, "DPP row sums cover 8 or 16 lanes");
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    if constexpr (N == 16) v += dpp_mov<0x140>(v);
     return v;
 }
 

@@ -25,6 +25,16 @@ hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const 
                              int dim_group_size, uint16_t* scores, int64_t score_row_stride,
                              hipStream_t stream);
 
+// Layer-step scorer: encodes the raw query rows [batch*QH, 128] in-kernel
+// (fold order), writes the scores' radix order keys (uint16) instead of fp16
+// bits, and adds each row's 256-bin high-byte key histogram into
+// ghist[row][256] (which must hold zeros on entry).
+hipError_t launch_score_d128_raw(const void* queries, int dtype, const int32_t* k_sign, const int32_t* k_mag,
+                                 const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
+                                 int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
+                                 int dim_group_size, uint16_t* keys, int64_t key_row_stride, uint32_t* ghist,
+                                 hipStream_t stream);
+
 hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, const float* q_low,
                                 const float* q_delta, const int32_t* k_sign, const int32_t* k_mag,
                                 const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
@@ -33,7 +43,13 @@ hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, con
 
 hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens,
                               int64_t k, int64_t current, void* indices, int index_dtype,
-                              int64_t index_row_stride, unsigned int* rearm_counters, hipStream_t stream);
+                              int64_t index_row_stride, hipStream_t stream);
+
+// Layer-step select over radix order keys with the high-byte histograms
+// ghist[row][256] the scorer built; re-zeroes ghist.  Rows 16-byte aligned.
+hipError_t launch_topk_select_keys(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride,
+                                   int64_t tokens, int64_t k, int64_t current, void* indices, int index_dtype,
+                                   int64_t index_row_stride, hipStream_t stream);
 
 hipError_t launch_attention_partial(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                     int64_t k_head_stride, int64_t k_token_stride, int64_t v_head_stride,
@@ -41,13 +57,9 @@ hipError_t launch_attention_partial(const void* queries, int dtype, const void* 
                                     const void* current_v, const void* indices, int index_dtype,
                                     int64_t index_row_stride, const uint8_t* valid_mask,
                                     const int64_t* head_to_kv, int q_heads, int kv_heads, int head_dim,
-                                    int64_t selected,
-                                    int split_tokens, float* partials, unsigned int* merge_counters,
-                                    void* merge_output, hipStream_t stream);
+                                    int64_t selected, int split_tokens, float* partials, hipStream_t stream);
 
 hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t splits, int head_dim,
                                   void* output, int out_dtype, hipStream_t stream);
-
-hipError_t launch_zero_u32(unsigned int* p, int64_t n, hipStream_t stream);
 
 }  // namespace popkv

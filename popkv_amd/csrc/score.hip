@@ -18,6 +18,8 @@
 // (v_bcnt_u32_b32) and the fp32 fma chain of popkv_ext.cu:502-515 / :867-870,
 // summed from +0 over representatives, times fp32(1/sqrt(128)), rounded once
 // to fp16 (popkv_ext.cu:757-876).
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -139,17 +141,109 @@ __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm
 
 constexpr int kScoreThreads = 256;
 constexpr int kScoreTokensPerThread = 2;
+constexpr int kMaxGroupHeads = 64;  // query heads per KV head the LDS stage holds
+
+// Query state of one GQA group in LDS.
+template <int G>
+struct GroupState {
+    uint32_t qs[kMaxGroupHeads][4], qm[kMaxGroupHeads][4];
+    float ql[kMaxGroupHeads][128 / G], qd[kMaxGroupHeads][128 / G];
+};
+
+// Encodes the group's query rows (head_dim 128) into `st` in the
+// decode-path order.  Wave w handles heads w, w+4, ...; the caller has
+// already loaded dims lane and lane+64 of those rows into qv[][2] (so the
+// query loads are issued ahead of the token loads).  Each wave forms the
+// whole-head extrema and sign/magnitude words; then one thread per (head,
+// representative) folds its G values in ascending dimension order (adding +0
+// for the other bucket is exact, so the fold is branch-free).  All threads of
+// the block call it.
+template <int G, int MAXW>
+__device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk, GroupState<G>& st, float (*stage)[128],
+                                  float (*thr)[2]) {
+    constexpr int R = 128 / G;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int i = 0; i < MAXW; ++i) {
+        const int h = wave + i * (kScoreThreads / kWave);
+        if (h >= qpk) break;
+        const float v0 = qv[i][0], v1 = qv[i][1];
+        stage[h][lane] = v0;
+        stage[h][lane + 64] = v1;
+        const float mn = wave_min(fminf(v0, v1)), mx = wave_max(fmaxf(v0, v1));
+        const float neg = mn * 0.5f, pos = mx * 0.5f;
+        const bool s0 = v0 >= 0.0f, s1 = v1 >= 0.0f;
+        const bool m0 = s0 ? v0 > pos : v0 < neg, m1 = s1 ? v1 > pos : v1 < neg;
+        const uint64_t bs0 = __ballot(s0), bs1 = __ballot(s1), bm0 = __ballot(m0), bm1 = __ballot(m1);
+        if (lane == 0) {
+            st.qs[h][0] = static_cast<uint32_t>(bs0); st.qs[h][1] = static_cast<uint32_t>(bs0 >> 32);
+            st.qs[h][2] = static_cast<uint32_t>(bs1); st.qs[h][3] = static_cast<uint32_t>(bs1 >> 32);
+            st.qm[h][0] = static_cast<uint32_t>(bm0); st.qm[h][1] = static_cast<uint32_t>(bm0 >> 32);
+            st.qm[h][2] = static_cast<uint32_t>(bm1); st.qm[h][3] = static_cast<uint32_t>(bm1 >> 32);
+            thr[h][0] = neg;
+            thr[h][1] = pos;
+        }
+    }
+    __syncthreads();
+    for (int item = threadIdx.x; item < qpk * R; item += kScoreThreads) {
+        const int h = item / R, r = item % R;
+        const float neg = thr[h][0], pos = thr[h][1];
+        float ls = 0.0f, hs = 0.0f;
+        int hn = 0;
+#pragma unroll
+        for (int j = 0; j < G; j += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(&stage[h][r * G + j]);
+            const float x[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool mg = x[u] >= 0.0f ? x[u] > pos : x[u] < neg;
+                const float a = fabsf(x[u]);
+                ls = ls + (mg ? 0.0f : a);
+                hs = hs + (mg ? a : 0.0f);
+                hn += mg ? 1 : 0;
+            }
+        }
+        finish_rep(ls, G - hn, hs, hn, st.ql[h][r], st.qd[h][r]);
+    }
+    __syncthreads();
+}
+
+// Copies a pre-encoded group state from global memory into `st`.
+template <int G>
+__device__ void load_group_state(const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
+                                 const float* __restrict__ q_low, const float* __restrict__ q_delta,
+                                 int64_t qrow0, int qpk, GroupState<G>& st) {
+    constexpr int R = 128 / G;
+    for (int i = threadIdx.x; i < qpk * 4; i += kScoreThreads) {
+        st.qs[i / 4][i % 4] = static_cast<uint32_t>(q_sign[qrow0 * 4 + i]);
+        st.qm[i / 4][i % 4] = static_cast<uint32_t>(q_mag[qrow0 * 4 + i]);
+    }
+    for (int i = threadIdx.x; i < qpk * R; i += kScoreThreads) {
+        st.ql[i / R][i % R] = q_low[qrow0 * R + i];
+        st.qd[i / R][i % R] = q_delta[qrow0 * R + i];
+    }
+    __syncthreads();
+}
 
 // grid.x: token tiles of kScoreThreads*kScoreTokensPerThread; grid.y: batch*kv_heads.
-template <int G, int QPK>
+// QT is the raw query type when the kernel encodes the query itself
+// (layer step), void when it reads a pre-encoded state.
+template <int G, int QPK, typename QT>
 __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
-    const float* __restrict__ q_low, const float* __restrict__ q_delta,
+    const float* __restrict__ q_low, const float* __restrict__ q_delta, const QT* __restrict__ q_raw,
     const uint4* __restrict__ k_sign, const uint4* __restrict__ k_mag,
     const uint16_t* __restrict__ k_low, const uint16_t* __restrict__ k_delta,
     const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, int qpk_rt,
-    int64_t cap, int64_t tokens, uint16_t* __restrict__ scores, int64_t out_stride) {
+    int64_t cap, int64_t tokens, uint16_t* __restrict__ scores, int64_t out_stride,
+    uint32_t* __restrict__ ghist) {
     constexpr int R = 128 / G;
+    // Layer-step mode (the kernel encodes the raw query): the output holds the
+    // scores' radix order keys instead of fp16 bits, and the per-head 256-bin
+    // histogram of the keys' high byte is accumulated into ghist[row][256]
+    // for the select kernel.
+    constexpr bool STEP = !std::is_void_v<QT>;
     const int qpk = QPK > 0 ? QPK : qpk_rt;
     const int64_t grow = blockIdx.y;
     const int64_t b = grow / kv_heads;
@@ -159,53 +253,102 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const int64_t kvh = min(max(head_to_kv[qh0], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
     const int64_t qrow0 = b * q_heads + qh0;
 
+    // Load order matters: loads retire in issue order (vmcnt), so the raw
+    // query values the encode needs are loaded first, then this thread's
+    // token rows, whose latency then overlaps the encode.
+    constexpr int MAXW = QPK > 0 ? (QPK + kScoreThreads / kWave - 1) / (kScoreThreads / kWave)
+                                 : kMaxGroupHeads / (kScoreThreads / kWave);
+    float qv[std::is_void_v<QT> ? 1 : MAXW][2];
+    if constexpr (!std::is_void_v<QT>) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = threadIdx.x / kWave;
 #pragma unroll
-    for (int it = 0; it < kScoreTokensPerThread; ++it) {
-        const int64_t t = (static_cast<int64_t>(blockIdx.x) * kScoreTokensPerThread + it) * kScoreThreads + threadIdx.x;
+        for (int i = 0; i < MAXW; ++i) {
+            const int h = min(wave + i * (kScoreThreads / kWave), qpk - 1);
+            const QT* src = q_raw + (qrow0 + h) * 128;
+            qv[i][0] = Elem<QT>::load(src, lane);
+            qv[i][1] = Elem<QT>::load(src, lane + 64);
+        }
+    }
+    constexpr int TPT = kScoreTokensPerThread;
+    using RepWord = std::conditional_t<R == 2, uint32_t, std::conditional_t<R == 4, uint2, uint4>>;
+    uint4 s4[TPT], m4[TPT];
+    RepWord lw[TPT], dw[TPT];
+    int64_t tok[TPT];
+#pragma unroll
+    for (int it = 0; it < TPT; ++it) {
+        tok[it] = (static_cast<int64_t>(blockIdx.x) * TPT + it) * kScoreThreads + threadIdx.x;
+        const int64_t krow = kvh * cap + min(tok[it], tokens - 1);
+        s4[it] = k_sign[krow];
+        m4[it] = k_mag[krow];
+        lw[it] = reinterpret_cast<const RepWord*>(k_low)[krow];
+        dw[it] = reinterpret_cast<const RepWord*>(k_delta)[krow];
+    }
+
+    __shared__ GroupState<G> st;
+    __shared__ uint32_t s_hist[STEP ? (QPK > 0 ? QPK : kMaxGroupHeads) : 1][256];
+    if constexpr (STEP) {
+        for (int i = threadIdx.x; i < qpk * 256; i += kScoreThreads) (&s_hist[0][0])[i] = 0u;
+    }
+    if constexpr (std::is_void_v<QT>) {
+        load_group_state<G>(q_sign, q_mag, q_low, q_delta, qrow0, qpk, st);
+    } else {
+        __shared__ __align__(16) float stage[QPK > 0 ? QPK : kMaxGroupHeads][128];
+        __shared__ float thr[QPK > 0 ? QPK : kMaxGroupHeads][2];
+        encode_group_fold<G, MAXW>(qv, qpk, st, stage, thr);
+    }
+
+#pragma unroll
+    for (int it = 0; it < TPT; ++it) {
+        const int64_t t = tok[it];
         if (t >= tokens) break;
-        const int64_t krow = kvh * cap + t;
-        const uint4 s4 = k_sign[krow];
-        const uint4 m4 = k_mag[krow];
-        const uint32_t ks[4] = {s4.x, s4.y, s4.z, s4.w};
-        const uint32_t km[4] = {m4.x, m4.y, m4.z, m4.w};
-        float kl[R], dk[R];
+        const uint32_t ks[4] = {s4[it].x, s4[it].y, s4[it].z, s4[it].w};
+        const uint32_t km[4] = {m4[it].x, m4[it].y, m4[it].z, m4[it].w};
+        uint32_t lws[R / 2], dws[R / 2];
         if constexpr (R == 2) {
-            const uint32_t l2 = reinterpret_cast<const uint32_t*>(k_low)[krow];
-            const uint32_t d2 = reinterpret_cast<const uint32_t*>(k_delta)[krow];
-            kl[0] = bits_f16(l2 & 0xffffu); kl[1] = bits_f16(l2 >> 16);
-            dk[0] = bits_f16(d2 & 0xffffu); dk[1] = bits_f16(d2 >> 16);
+            lws[0] = lw[it]; dws[0] = dw[it];
         } else if constexpr (R == 4) {
-            const uint2 l4 = reinterpret_cast<const uint2*>(k_low)[krow];
-            const uint2 d4 = reinterpret_cast<const uint2*>(k_delta)[krow];
-            const uint32_t lw[2] = {l4.x, l4.y}, dw[2] = {d4.x, d4.y};
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                kl[2 * i] = bits_f16(lw[i] & 0xffffu); kl[2 * i + 1] = bits_f16(lw[i] >> 16);
-                dk[2 * i] = bits_f16(dw[i] & 0xffffu); dk[2 * i + 1] = bits_f16(dw[i] >> 16);
-            }
+            lws[0] = lw[it].x; lws[1] = lw[it].y; dws[0] = dw[it].x; dws[1] = dw[it].y;
         } else {
-            const uint4 l8 = reinterpret_cast<const uint4*>(k_low)[krow];
-            const uint4 d8 = reinterpret_cast<const uint4*>(k_delta)[krow];
-            const uint32_t lw[4] = {l8.x, l8.y, l8.z, l8.w}, dw[4] = {d8.x, d8.y, d8.z, d8.w};
+            lws[0] = lw[it].x; lws[1] = lw[it].y; lws[2] = lw[it].z; lws[3] = lw[it].w;
+            dws[0] = dw[it].x; dws[1] = dw[it].y; dws[2] = dw[it].z; dws[3] = dw[it].w;
+        }
+        float kl[R], dk[R];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                kl[2 * i] = bits_f16(lw[i] & 0xffffu); kl[2 * i + 1] = bits_f16(lw[i] >> 16);
-                dk[2 * i] = bits_f16(dw[i] & 0xffffu); dk[2 * i + 1] = bits_f16(dw[i] >> 16);
-            }
+        for (int i = 0; i < R / 2; ++i) {
+            kl[2 * i] = bits_f16(lws[i] & 0xffffu); kl[2 * i + 1] = bits_f16(lws[i] >> 16);
+            dk[2 * i] = bits_f16(dws[i] & 0xffffu); dk[2 * i + 1] = bits_f16(dws[i] >> 16);
         }
         for (int h = 0; h < qpk; ++h) {
-            const int64_t qrow = qrow0 + h;
+            // The group state is uniform: readfirstlane keeps it in SGPRs.
             uint32_t qs[4], qm[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                qs[w] = static_cast<uint32_t>(q_sign[qrow * 4 + w]);
-                qm[w] = static_cast<uint32_t>(q_mag[qrow * 4 + w]);
+                qs[w] = __builtin_amdgcn_readfirstlane(st.qs[h][w]);
+                qm[w] = __builtin_amdgcn_readfirstlane(st.qm[h][w]);
             }
             float total = 0.0f;
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                total = total + rep_term<G>(qs, qm, ks, km, r, q_low[qrow * R + r], q_delta[qrow * R + r], kl[r], dk[r]);
-            scores[qrow * out_stride + t] = f16_rne(total * 0x1.6a09e6p-4f);  // fp32(1/sqrt(128)) = 0x3DB504F3
+            for (int r = 0; r < R; ++r) {
+                const float ql = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.ql[h][r])));
+                const float dq = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.qd[h][r])));
+                total = total + rep_term<G>(qs, qm, ks, km, r, ql, dq, kl[r], dk[r]);
+            }
+            const uint16_t bits = f16_rne(total * 0x1.6a09e6p-4f);  // fp32(1/sqrt(128)) = 0x3DB504F3
+            if constexpr (STEP) {
+                const uint32_t key = order_key(bits);
+                scores[(qrow0 + h) * out_stride + t] = static_cast<uint16_t>(key);
+                atomicAdd(&s_hist[h][key >> 8], 1u);
+            } else {
+                scores[(qrow0 + h) * out_stride + t] = bits;
+            }
+        }
+    }
+    if constexpr (STEP) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < qpk * 256; i += kScoreThreads) {
+            const uint32_t c = (&s_hist[0][0])[i];
+            if (c != 0u) atomicAdd(&ghist[(qrow0 + i / 256) * 256 + (i & 255)], c);
         }
     }
 }
@@ -278,19 +421,19 @@ hipError_t launch_encode_g(const T* q, int64_t rows, int d, int g, int order, in
     }
 }
 
-template <int G>
-hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float* ql, const float* qd,
+template <int G, typename QT>
+hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float* ql, const float* qd, const QT* q_raw,
                                const int32_t* ks, const int32_t* km, const uint16_t* kl, const uint16_t* kd,
                                const int64_t* h2k, int64_t batch, int qh, int kvh, int64_t cap, int64_t tokens,
-                               uint16_t* out, int64_t out_stride, hipStream_t stream) {
+                               uint16_t* out, int64_t out_stride, uint32_t* ghist, hipStream_t stream) {
     const int qpk = qh / kvh;
     const int64_t per_block = static_cast<int64_t>(kScoreThreads) * kScoreTokensPerThread;
     dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block), static_cast<unsigned>(batch * kvh));
     const uint4* ks4 = reinterpret_cast<const uint4*>(ks);
     const uint4* km4 = reinterpret_cast<const uint4*>(km);
-#define POPKV_SCORE_LAUNCH(Q)                                                                              \
-    hipLaunchKernelGGL((score_d128_kernel<G, Q>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd, ks4, \
-                       km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride)
+#define POPKV_SCORE_LAUNCH(Q)                                                                                 \
+    hipLaunchKernelGGL((score_d128_kernel<G, Q, QT>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd, q_raw, \
+                       ks4, km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride, ghist)
     switch (qpk) {
         case 1: POPKV_SCORE_LAUNCH(1); break;
         case 2: POPKV_SCORE_LAUNCH(2); break;
@@ -300,6 +443,28 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
     }
 #undef POPKV_SCORE_LAUNCH
     return hipGetLastError();
+}
+
+template <typename QT>
+hipError_t launch_score_d128_q(const int32_t* q_sign, const int32_t* q_mag, const float* q_low, const float* q_delta,
+                               const QT* q_raw, const int32_t* k_sign, const int32_t* k_mag, const uint16_t* k_low,
+                               const uint16_t* k_delta, const int64_t* head_to_kv, int64_t batch, int q_heads,
+                               int kv_heads, int64_t capacity, int64_t tokens, int dim_group_size, uint16_t* scores,
+                               int64_t score_row_stride, uint32_t* ghist, hipStream_t stream) {
+    switch (dim_group_size) {
+        case 16:
+            return launch_score_d128_g<16, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
+                                               head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
+                                               score_row_stride, ghist, stream);
+        case 32:
+            return launch_score_d128_g<32, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
+                                               head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
+                                               score_row_stride, ghist, stream);
+        default:
+            return launch_score_d128_g<64, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
+                                               head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
+                                               score_row_stride, ghist, stream);
+    }
 }
 
 }  // namespace
@@ -326,16 +491,30 @@ hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const 
                              const uint16_t* k_delta, const int64_t* head_to_kv, int64_t batch, int q_heads,
                              int kv_heads, int64_t capacity, int64_t tokens, int dim_group_size, uint16_t* scores,
                              int64_t score_row_stride, hipStream_t stream) {
-    switch (dim_group_size) {
-        case 16:
-            return launch_score_d128_g<16>(q_sign, q_mag, q_low, q_delta, k_sign, k_mag, k_low, k_delta, head_to_kv,
-                                           batch, q_heads, kv_heads, capacity, tokens, scores, score_row_stride, stream);
-        case 32:
-            return launch_score_d128_g<32>(q_sign, q_mag, q_low, q_delta, k_sign, k_mag, k_low, k_delta, head_to_kv,
-                                           batch, q_heads, kv_heads, capacity, tokens, scores, score_row_stride, stream);
+    return launch_score_d128_q<void>(q_sign, q_mag, q_low, q_delta, nullptr, k_sign, k_mag, k_low, k_delta,
+                                     head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size, scores,
+                                     score_row_stride, nullptr, stream);
+}
+
+hipError_t launch_score_d128_raw(const void* queries, int dtype, const int32_t* k_sign, const int32_t* k_mag,
+                                 const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
+                                 int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
+                                 int dim_group_size, uint16_t* keys, int64_t key_row_stride, uint32_t* ghist,
+                                 hipStream_t stream) {
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_score_d128_q<float>(nullptr, nullptr, nullptr, nullptr, static_cast<const float*>(queries),
+                                              k_sign, k_mag, k_low, k_delta, head_to_kv, batch, q_heads, kv_heads,
+                                              capacity, tokens, dim_group_size, keys, key_row_stride, ghist, stream);
+        case POPKV_DTYPE_F16:
+            return launch_score_d128_q<f16_t>(nullptr, nullptr, nullptr, nullptr, static_cast<const f16_t*>(queries),
+                                              k_sign, k_mag, k_low, k_delta, head_to_kv, batch, q_heads, kv_heads,
+                                              capacity, tokens, dim_group_size, keys, key_row_stride, ghist, stream);
         default:
-            return launch_score_d128_g<64>(q_sign, q_mag, q_low, q_delta, k_sign, k_mag, k_low, k_delta, head_to_kv,
-                                           batch, q_heads, kv_heads, capacity, tokens, scores, score_row_stride, stream);
+            return launch_score_d128_q<bf16_t>(nullptr, nullptr, nullptr, nullptr,
+                                               static_cast<const bf16_t*>(queries), k_sign, k_mag, k_low, k_delta,
+                                               head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size,
+                                               keys, key_row_stride, ghist, stream);
     }
 }
 

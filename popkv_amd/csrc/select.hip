@@ -4,19 +4,25 @@
 // Replaces torch.topk(scores, k, dim=-1, sorted=False).indices followed by
 // _append_current (reference popkv.py:1094-1098, :287-291).
 //
-// One 1024-thread workgroup (16 wave64s) per row.  Thread i owns a contiguous
-// segment of the row and keeps its keys in registers (two 16-bit keys per
-// VGPR).  The key is PyTorch's radix order of an fp16 bit pattern: negatives
-// bit-inverted, non-negatives with the sign bit set, NaN largest, so -0 < +0.
-//   1. 256-bin histogram of the key's high byte (per-wave LDS histograms),
-//      suffix scan -> the high byte d1 of the k-th largest key;
-//   2. 256-bin histogram of the low byte among keys with high byte d1 ->
-//      the exact k-th largest key T;
-//   3. every key > T is selected; keys == T fill the remaining slots in
-//      ascending token order (a block scan of per-thread tie counts), which is
-//      what PyTorch's gather-top-k does with ties;
-//   4. a block scan of per-thread selection counts gives each thread its
-//      output offset, so indices come out in ascending token order.
+// One 1024-thread workgroup (16 wave64s) per row.  Thread t owns the
+// contiguous segment of SEG tokens [t*SEG, t*SEG + SEG), read with 16-byte
+// loads, and keeps its keys in registers (two 16-bit keys per VGPR) for the
+// whole kernel.  The key is PyTorch's radix order of an fp16 bit pattern:
+// negatives bit-inverted, non-negatives with the sign bit set, NaN largest,
+// so -0 < +0.
+//   1. 256-bin histogram of the key's high byte -> the bin b1 holding the
+//      k-th largest key;
+//   2. 256-bin histogram of the low byte among keys with high byte b1 ->
+//      the exact k-th largest key T.
+//      Both histograms are privatized per lane (bin*64 + lane): PopKV's
+//      scores are peaked, so a shared histogram would serialize on
+//      same-address LDS atomics; with one copy per lane no two lanes of an
+//      instruction touch the same word.  The 64 copies are then summed.
+//   3. keys > T are selected; keys == T fill the remaining slots in ascending
+//      token order (PyTorch's gather-top-k tie rule).  One block scan of the
+//      packed per-thread (greater, equal) counts gives every selected token
+//      its slot in ascending token order; slots are filled in LDS and the
+//      finished list is copied out with coalesced stores.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -25,49 +31,48 @@ namespace {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / kWave;
+constexpr int kBins = 256;  // one byte of the key per level
 
-__device__ __forceinline__ uint32_t order_key(uint32_t h) {
-    const bool nan = ((h & 0x7c00u) == 0x7c00u) && (h & 0x3ffu);
-    const uint32_t k = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
-    return nan ? 0xffffu : k;
-}
-
-// Finds the bin holding the `need`-th largest element of a 256-bin histogram
-// `tot` (1 <= need <= total).  Wave 0 scans bins from the top; the winning
-// lane stores the bin and the count strictly above it.
-__device__ __forceinline__ void find_bin(const uint32_t* tot, uint32_t need, uint32_t* s_bin, uint32_t* s_above) {
-    const int lane = threadIdx.x & (kWave - 1);
-    uint32_t c[4];
+// Finds the bin holding the `need`-th largest element of histogram `hist`
+// (NB bins, 1 <= need <= total) with the whole block: each thread sums a
+// contiguous run of bins from the top, one block scan, then the owning
+// thread scans its run.  Writes the bin and the count strictly above it.
+template <int NB>
+__device__ __forceinline__ void find_bin(const uint32_t* hist, uint32_t need, uint32_t* scan_sh,
+                                         uint32_t* s_bin, uint32_t* s_above) {
+    constexpr int PER = (NB + kSelThreads - 1) / kSelThreads;
+    const int t = threadIdx.x;
+    uint32_t c[PER];
     uint32_t local = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        c[i] = tot[255 - (4 * lane + i)];
+    for (int i = 0; i < PER; ++i) {
+        const int r = t * PER + i;  // rank from the top
+        c[i] = r < NB ? hist[NB - 1 - r] : 0u;
         local += c[i];
     }
-    const uint32_t incl = wave_incl_scan(local, lane);
-    uint32_t running = incl - local;
+    uint32_t total;
+    uint32_t running = block_excl_scan(local, scan_sh, kSelWaves, &total);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < PER; ++i) {
         if (running < need && running + c[i] >= need) {
-            *s_bin = 255u - static_cast<uint32_t>(4 * lane + i);
+            *s_bin = static_cast<uint32_t>(NB - 1 - (t * PER + i));
             *s_above = running;
         }
         running += c[i];
     }
 }
 
-template <int SEG, typename IdxT>
+constexpr int kStageMax = 8192;  // selections staged in LDS (k <= 8192)
+
+template <int SEG, bool VEC, typename IdxT>
 __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
     const uint16_t* __restrict__ scores, int64_t row_stride, int64_t tokens, int64_t k, int64_t current,
-    IdxT* __restrict__ out, int64_t out_stride, unsigned int* __restrict__ rearm) {
+    IdxT* __restrict__ out, int64_t out_stride) {
+    static_assert(SEG % 8 == 0, "segments are whole 16-byte chunks");
     const int64_t row = blockIdx.x;
     const uint16_t* src = scores + row * row_stride;
     IdxT* dst = out + row * out_stride;
     const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    // Re-arms the per-row completion counter of the fused attention merge that
-    // runs after this kernel on the same stream.
-    if (rearm != nullptr && tid == 0) rearm[row] = 0u;
 
     if (k >= tokens) {  // every cached token is selected
         for (int64_t t = tid; t < tokens; t += kSelThreads) dst[t] = static_cast<IdxT>(t);
@@ -79,121 +84,308 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
         return;
     }
 
-    __shared__ uint32_t hist[kSelWaves][256];
-    __shared__ uint32_t tot[256];
+    __shared__ uint32_t hist[kBins * kWave];  // [bin][lane]
+    __shared__ uint32_t tot[kBins];
     __shared__ uint32_t scan_sh[kSelWaves + 1];
     __shared__ uint32_t s_bin, s_above;
+    __shared__ int32_t stage[kStageMax];
+    const int lane = tid & (kWave - 1);
 
-    const int64_t seg = (tokens + kSelThreads - 1) / kSelThreads;
-    const int64_t begin = tid * seg;
-    const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(seg, tokens - begin)));
-
+    // ---- load this thread's segment; absent tokens are never counted (n below)
+    const int64_t begin = static_cast<int64_t>(tid) * SEG;
+    const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(SEG, tokens - begin)));
     uint32_t kp[SEG / 2];
 #pragma unroll
-    for (int j = 0; j < SEG / 2; ++j) {
-        const uint32_t a = (2 * j < n) ? order_key(src[begin + 2 * j]) : 0u;
-        const uint32_t b = (2 * j + 1 < n) ? order_key(src[begin + 2 * j + 1]) : 0u;
-        kp[j] = a | (b << 16);
+    for (int c = 0; c < SEG / 8; ++c) {
+        if (VEC && 8 * c + 8 <= n) {
+            const uint4 u = *reinterpret_cast<const uint4*>(src + begin + 8 * c);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kp[4 * c + j] = order_key(w[j] & 0xffffu) | (order_key(w[j] >> 16) << 16);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 8 * c + 2 * j;
+                const uint32_t a = e < n ? order_key(src[begin + e]) : 0u;
+                const uint32_t b = e + 1 < n ? order_key(src[begin + e + 1]) : 0u;
+                kp[4 * c + j] = a | (b << 16);
+            }
+        }
     }
-#define POPKV_KEY(j) ((kp[(j) >> 1] >> (((j) & 1) * 16)) & 0xffffu)
+#define POPKV_KEY(e) ((kp[(e) >> 1] >> (((e) & 1) * 16)) & 0xffffu)
+
+    // Sums the 64 per-lane copies into tot[]: thread (bin, quarter) adds 16
+    // copies, then the four quarters of a bin (adjacent lanes) combine.  The
+    // copy order is rotated by bin so a wave's 64 reads hit 64 banks.
+    auto reduce_hist = [&]() {
+        const int bin = tid >> 2, q = tid & 3;
+        uint32_t v = 0;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) v += hist[bin * kWave + q * 16 + ((c + bin) & 15)];
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        if (q == 0) tot[bin] = v;
+    };
 
     // ---- level 1: high byte
-    for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&hist[0][0])[i] = 0u;
+    for (int i = tid; i < kBins * kWave; i += kSelThreads) hist[i] = 0u;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < SEG; ++j)
-        if (j < n) atomicAdd(&hist[wave][POPKV_KEY(j) >> 8], 1u);
+    for (int e = 0; e < SEG; ++e)
+        if (e < n) atomicAdd(&hist[(POPKV_KEY(e) >> 8) * kWave + lane], 1u);
     __syncthreads();
-    if (tid < 256) {
-        uint32_t s = 0;
-#pragma unroll
-        for (int w = 0; w < kSelWaves; ++w) s += hist[w][tid];
-        tot[tid] = s;
-    }
+    reduce_hist();
     __syncthreads();
-    if (wave == 0) find_bin(tot, static_cast<uint32_t>(k), &s_bin, &s_above);
+    find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
     __syncthreads();
-    const uint32_t d1 = s_bin;
+    const uint32_t b1 = s_bin;
     const uint32_t above1 = s_above;
 
-    // ---- level 2: low byte within bucket d1
-    for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&hist[0][0])[i] = 0u;
+    // ---- level 2: low byte inside bin b1
+    for (int i = tid; i < kBins * kWave; i += kSelThreads) hist[i] = 0u;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < SEG; ++j) {
-        const uint32_t key = POPKV_KEY(j);
-        if (j < n && (key >> 8) == d1) atomicAdd(&hist[wave][key & 0xffu], 1u);
+    for (int e = 0; e < SEG; ++e) {
+        const uint32_t key = POPKV_KEY(e);
+        if (e < n && (key >> 8) == b1) atomicAdd(&hist[(key & 0xffu) * kWave + lane], 1u);
     }
     __syncthreads();
-    if (tid < 256) {
-        uint32_t s = 0;
-#pragma unroll
-        for (int w = 0; w < kSelWaves; ++w) s += hist[w][tid];
-        tot[tid] = s;
-    }
+    reduce_hist();
     __syncthreads();
-    if (wave == 0) find_bin(tot, static_cast<uint32_t>(k) - above1, &s_bin, &s_above);
+    find_bin<kBins>(tot, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
     __syncthreads();
-    const uint32_t thr = (d1 << 8) | s_bin;
+    const uint32_t thr = (b1 << 8) | s_bin;
     const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
 
-    // ---- level 3: ordered selection
+    // ---- ordered selection: slot of a selected token = (#greater before it)
+    //      + min(#equal before it, need_eq)
     uint32_t n_gt = 0, n_eq = 0;
 #pragma unroll
-    for (int j = 0; j < SEG; ++j) {
-        const uint32_t key = POPKV_KEY(j);
-        if (j < n) {
+    for (int e = 0; e < SEG; ++e) {
+        const uint32_t key = POPKV_KEY(e);
+        if (e < n) {
             n_gt += key > thr ? 1u : 0u;
             n_eq += key == thr ? 1u : 0u;
         }
     }
-    uint32_t total;
-    const uint32_t eq_before = block_excl_scan(n_eq, scan_sh, kSelWaves, &total);
-    const uint32_t take_eq = need_eq > eq_before ? min(need_eq - eq_before, n_eq) : 0u;
-    const uint32_t pos0 = block_excl_scan(n_gt + take_eq, scan_sh, kSelWaves, &total);
-    uint32_t pos = pos0, taken = 0;
+    uint32_t total, gt_before, eq_before;
+    if (tokens <= 0xffff) {  // both prefix counts fit 16 bits: one packed scan
+        const uint32_t packed = block_excl_scan(n_gt | (n_eq << 16), scan_sh, kSelWaves, &total);
+        gt_before = packed & 0xffffu;
+        eq_before = packed >> 16;
+    } else {
+        gt_before = block_excl_scan(n_gt, scan_sh, kSelWaves, &total);
+        eq_before = block_excl_scan(n_eq, scan_sh, kSelWaves, &total);
+    }
+    const bool staged = k <= kStageMax;
 #pragma unroll
-    for (int j = 0; j < SEG; ++j) {
-        const uint32_t key = POPKV_KEY(j);
-        if (j < n) {
-            const bool sel = key > thr || (key == thr && taken < take_eq);
-            taken += (key == thr && taken < take_eq) ? 1u : 0u;
-            if (sel) dst[pos++] = static_cast<IdxT>(begin + j);
+    for (int e = 0; e < SEG; ++e) {
+        const uint32_t key = POPKV_KEY(e);
+        if (e >= n) continue;
+        uint32_t slot = 0xffffffffu;
+        if (key > thr) {
+            slot = gt_before + min(eq_before, need_eq);
+            ++gt_before;
+        } else if (key == thr) {
+            if (eq_before < need_eq) slot = gt_before + eq_before;
+            ++eq_before;
+        }
+        if (slot != 0xffffffffu) {
+            if (staged) stage[slot] = static_cast<int32_t>(begin + e);
+            else dst[slot] = static_cast<IdxT>(begin + e);
         }
     }
 #undef POPKV_KEY
+    if (staged) {
+        __syncthreads();
+        for (int64_t i = tid; i < k; i += kSelThreads) dst[i] = static_cast<IdxT>(stage[i]);
+    }
+    if (tid == 0) dst[k] = static_cast<IdxT>(current);
+}
+
+// Layer-step select.  The input rows already hold radix order keys and the
+// scorer has accumulated each row's high-byte histogram into ghist, so the
+// first radix level costs nothing here: one pass classifies every key against
+// the k-th key's high byte into per-thread bit masks (above / candidate), only
+// the candidates sharing that byte feed a second 256-bin histogram, and the
+// ordered write-out walks the set bits of the selection mask.  ghist is
+// re-zeroed for the next call.
+template <int SEG, typename IdxT>
+__global__ __launch_bounds__(kSelThreads) void topk_select_keys_kernel(
+    const uint16_t* __restrict__ keys, uint32_t* __restrict__ ghist, int64_t row_stride, int64_t tokens, int64_t k,
+    int64_t current, IdxT* __restrict__ out, int64_t out_stride) {
+    constexpr int MW = (SEG + 31) / 32;  // 32-bit mask words per thread
+    const int64_t row = blockIdx.x;
+    const uint16_t* src = keys + row * row_stride;
+    uint32_t* gh = ghist + row * kBins;
+    IdxT* dst = out + row * out_stride;
+    const int tid = threadIdx.x;
+
+    __shared__ uint32_t tot[kBins], hist2[kBins];
+    __shared__ uint32_t scan_sh[kSelWaves + 1];
+    __shared__ uint32_t s_bin, s_above;
+    __shared__ int32_t stage[kStageMax];
+    if (tid < kBins) {
+        tot[tid] = gh[tid];
+        gh[tid] = 0u;
+        hist2[tid] = 0u;
+    }
+    if (k >= tokens) {
+        for (int64_t t = tid; t < tokens; t += kSelThreads) dst[t] = static_cast<IdxT>(t);
+        if (tid == 0) dst[tokens] = static_cast<IdxT>(current);
+        return;
+    }
+    if (k == 0) {
+        if (tid == 0) dst[0] = static_cast<IdxT>(current);
+        return;
+    }
+
+    const int64_t begin = static_cast<int64_t>(tid) * SEG;
+    const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(SEG, tokens - begin)));
+    uint32_t kp[SEG / 2];
+#pragma unroll
+    for (int c = 0; c < SEG / 8; ++c) {
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (8 * c < n) u = *reinterpret_cast<const uint4*>(src + begin + 8 * c);  // rows are padded to 16 bytes
+        kp[4 * c] = u.x; kp[4 * c + 1] = u.y; kp[4 * c + 2] = u.z; kp[4 * c + 3] = u.w;
+    }
+#define POPKV_KEY(e) ((kp[(e) >> 1] >> (((e) & 1) * 16)) & 0xffffu)
+    __syncthreads();
+    find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
+    __syncthreads();
+    const uint32_t b1 = s_bin;
+    const uint32_t above1 = s_above;
+
+    // low-byte histogram of the keys sharing the k-th key's high byte
+#pragma unroll
+    for (int e = 0; e < SEG; ++e) {
+        const uint32_t key = POPKV_KEY(e);
+        if (e < n && (key >> 8) == b1) atomicAdd(&hist2[key & 0xffu], 1u);
+    }
+    __syncthreads();
+    find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
+    __syncthreads();
+    const uint32_t thr = (b1 << 8) | s_bin;
+    const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
+
+    // selection masks: key > T (selected outright) and key == T (ties)
+    uint32_t sel[MW], tie[MW];
+#pragma unroll
+    for (int w = 0; w < MW; ++w) { sel[w] = 0u; tie[w] = 0u; }
+#pragma unroll
+    for (int e = 0; e < SEG; ++e) {
+        const uint32_t key = POPKV_KEY(e);
+        const bool valid = e < n;
+        sel[e / 32] |= static_cast<uint32_t>(valid && key > thr) << (e & 31);
+        tie[e / 32] |= static_cast<uint32_t>(valid && key == thr) << (e & 31);
+    }
+    uint32_t n_gt = 0, n_eq = 0;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) {
+        n_gt += __popc(sel[w]);
+        n_eq += __popc(tie[w]);
+    }
+#undef POPKV_KEY
+    uint32_t total, gt_before, eq_before;
+    if (tokens <= 0xffff) {
+        const uint32_t packed = block_excl_scan(n_gt | (n_eq << 16), scan_sh, kSelWaves, &total);
+        gt_before = packed & 0xffffu;
+        eq_before = packed >> 16;
+    } else {
+        gt_before = block_excl_scan(n_gt, scan_sh, kSelWaves, &total);
+        eq_before = block_excl_scan(n_eq, scan_sh, kSelWaves, &total);
+    }
+    const bool staged = k <= kStageMax;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) {
+        for (uint32_t m = sel[w] | tie[w]; m; m &= m - 1) {
+            const int b = __builtin_ctz(m);
+            uint32_t slot = 0xffffffffu;
+            if ((sel[w] >> b) & 1u) {
+                slot = gt_before + min(eq_before, need_eq);
+                ++gt_before;
+            } else {
+                if (eq_before < need_eq) slot = gt_before + eq_before;
+                ++eq_before;
+            }
+            if (slot != 0xffffffffu) {
+                const int64_t t = begin + w * 32 + b;
+                if (staged) stage[slot] = static_cast<int32_t>(t);
+                else dst[slot] = static_cast<IdxT>(t);
+            }
+        }
+    }
+    if (staged) {
+        __syncthreads();
+        for (int64_t i = tid; i < k; i += kSelThreads) dst[i] = static_cast<IdxT>(stage[i]);
+    }
     if (tid == 0) dst[k] = static_cast<IdxT>(current);
 }
 
 template <typename IdxT>
-hipError_t launch_select_t(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
-                           int64_t current, IdxT* out, int64_t out_stride, unsigned int* rearm,
-                           hipStream_t stream) {
-    const int64_t seg = (tokens + kSelThreads - 1) / kSelThreads;
+hipError_t launch_keys_t(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
+                         int64_t k, int64_t current, IdxT* out, int64_t out_stride, hipStream_t stream) {
+    const int64_t per = (tokens + kSelThreads - 1) / kSelThreads;
     dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
-#define POPKV_SEL(S)                                                                                      \
-    hipLaunchKernelGGL((topk_select_kernel<S, IdxT>), grid, block, 0, stream, scores, row_stride, tokens, k, \
-                       current, out, out_stride, rearm)
-    if (seg <= 8) POPKV_SEL(8);
-    else if (seg <= 16) POPKV_SEL(16);
-    else if (seg <= 32) POPKV_SEL(32);
-    else if (seg <= 64) POPKV_SEL(64);
-    else POPKV_SEL(128);
-#undef POPKV_SEL
+#define POPKV_KEYSEL(S)                                                                                         \
+    hipLaunchKernelGGL((topk_select_keys_kernel<S, IdxT>), grid, block, 0, stream, keys, ghist, row_stride, tokens, \
+                       k, current, out, out_stride)
+    if (per <= 8) POPKV_KEYSEL(8);
+    else if (per <= 16) POPKV_KEYSEL(16);
+    else if (per <= 32) POPKV_KEYSEL(32);
+    else if (per <= 64) POPKV_KEYSEL(64);
+    else POPKV_KEYSEL(128);
+#undef POPKV_KEYSEL
+    return hipGetLastError();
+}
+
+template <int SEG, typename IdxT>
+void launch_seg(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
+                int64_t current, IdxT* out, int64_t out_stride, bool vec, hipStream_t stream) {
+    dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
+    if (vec)
+        hipLaunchKernelGGL((topk_select_kernel<SEG, true, IdxT>), grid, block, 0, stream, scores, row_stride, tokens,
+                           k, current, out, out_stride);
+    else
+        hipLaunchKernelGGL((topk_select_kernel<SEG, false, IdxT>), grid, block, 0, stream, scores, row_stride,
+                           tokens, k, current, out, out_stride);
+}
+
+template <typename IdxT>
+hipError_t launch_select_t(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
+                           int64_t current, IdxT* out, int64_t out_stride, hipStream_t stream) {
+    const int64_t per = (tokens + kSelThreads - 1) / kSelThreads;
+    const bool vec = reinterpret_cast<uintptr_t>(scores) % 16 == 0 && row_stride % 8 == 0;
+    if (per <= 8) launch_seg<8>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
+    else if (per <= 16) launch_seg<16>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
+    else if (per <= 32) launch_seg<32>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
+    else if (per <= 64) launch_seg<64>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
+    else launch_seg<128>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
     return hipGetLastError();
 }
 
 }  // namespace
 
+hipError_t launch_topk_select_keys(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride,
+                                   int64_t tokens, int64_t k, int64_t current, void* indices, int index_dtype,
+                                   int64_t index_row_stride, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (index_dtype == POPKV_INDEX_I32)
+        return launch_keys_t(keys, ghist, rows, row_stride, tokens, k, current, static_cast<int32_t*>(indices),
+                             index_row_stride, stream);
+    return launch_keys_t(keys, ghist, rows, row_stride, tokens, k, current, static_cast<int64_t*>(indices),
+                         index_row_stride, stream);
+}
+
 hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
                               int64_t current, void* indices, int index_dtype, int64_t index_row_stride,
-                              unsigned int* rearm_counters, hipStream_t stream) {
+                              hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     if (index_dtype == POPKV_INDEX_I32)
         return launch_select_t(scores, rows, row_stride, tokens, k, current, static_cast<int32_t*>(indices),
-                               index_row_stride, rearm_counters, stream);
+                               index_row_stride, stream);
     return launch_select_t(scores, rows, row_stride, tokens, k, current, static_cast<int64_t*>(indices),
-                           index_row_stride, rearm_counters, stream);
+                           index_row_stride, stream);
 }
 
 }  // namespace popkv

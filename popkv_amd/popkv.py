@@ -8,8 +8,8 @@ static K/V cache append (popkv.py:105-111, :964-972), ``_append_current`` /
 ``_sparse_layer_indices`` (popkv.py:283-291), and the PopKV branch of
 ``LlamaSparseDecoder.decode`` (popkv.py:1076-1115) as ``popkv_retrieval_step``.
 
-``popkv_layer_step`` is the same step as one C-ABI call: score, top-k and
-split attention with the log-sum-exp merge fused into the attention kernel.
+``popkv_layer_step`` is the same step as one C-ABI call (four kernels:
+encode + score, top-k, split attention, log-sum-exp merge).
 """
 from __future__ import annotations
 
@@ -258,14 +258,17 @@ def popkv_retrieval_step(
 
 
 class LayerStepWorkspace:
-    """Reusable device workspace for ``popkv_layer_step`` (grown on demand)."""
+    """Reusable device workspace for ``popkv_layer_step`` (grown on demand).
+
+    The C ABI requires the workspace to be zero-filled before its first use
+    (each step leaves it reusable), so new buffers are allocated zeroed."""
 
     def __init__(self) -> None:
         self.buffer: torch.Tensor | None = None
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
         if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
-            self.buffer = torch.empty(max(nbytes, 1), device=device, dtype=torch.uint8)
+            self.buffer = torch.zeros(max(nbytes, 1), device=device, dtype=torch.uint8)
         return self.buffer
 
 
@@ -280,8 +283,8 @@ def popkv_layer_step(
     return_indices: bool = False,
 ):
     """One sparse layer's retrieval step (head_dim 128, batch 1) in a single
-    C-ABI call: encode, popcount score, top-k + current, split attention with
-    the merge fused in.  Same result as ``popkv_retrieval_step``.
+    C-ABI call: encode + popcount score, top-k + current, split attention,
+    merge.  Same result as ``popkv_retrieval_step``.
 
     prefix_k/prefix_v: [KVH, L, 128] with unit row stride 128 (any head
     stride); q: [QH, 128]; k, v: [KVH, 128].  Returns out [QH, 128] (and the
@@ -303,7 +306,7 @@ def popkv_layer_step(
     mapping = head_to_kv.to(device=dev, dtype=torch.int64).contiguous()
     nbytes = layer_step_workspace_bytes(q_heads, tokens, budget, cache.dim_group_size)
     if isinstance(workspace, torch.Tensor):
-        ws = workspace
+        ws = workspace  # caller-owned: zero-filled before its first use
     else:
         ws = (workspace or LayerStepWorkspace()).get(nbytes, dev)
     output = torch.empty_like(qc) if out is None else out
