@@ -25,6 +25,8 @@
 // merge inside the partial kernel would need an agent-scope release per
 // workgroup, which on gfx950 writes back the XCD's L2 each time; a separate
 // launch is far cheaper.)
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -60,47 +62,130 @@ __device__ __forceinline__ void merge_state(SoftmaxState& a, float m2, float l2,
     a.m = mm;
 }
 
+// Writes a workgroup's (m, l, acc[d]) to dst: the row slots of each wave
+// (lanes with equal dim slice) merge through shuffles, the waves through LDS.
+// All threads of the block call it.
+template <int LPR>
+__device__ __forceinline__ void store_partial(SoftmaxState st, int lane, int wave, int dim0, int d, float* dst) {
+#pragma unroll
+    for (int m = LPR; m < kWave; m <<= 1) {
+        const float m2 = __shfl_xor(st.m, m);
+        const float l2 = __shfl_xor(st.l, m);
+        float a2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a2[i] = __shfl_xor(st.acc[i], m);
+        merge_state(st, m2, l2, a2);
+    }
+    __shared__ float s_m[kAttnWaves], s_l[kAttnWaves];
+    __shared__ float s_acc[kAttnWaves][256];
+    if (lane < LPR) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_acc[wave][dim0 + i] = st.acc[i];
+        if (lane == 0) { s_m[wave] = st.m; s_l[wave] = st.l; }
+    }
+    __syncthreads();
+    const int dim = threadIdx.x;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, s_m[w]);
+    float l = 0.0f, a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+        if (s_m[w] == -INFINITY) continue;
+        const float wt = __expf(s_m[w] - mx);
+        l += s_l[w] * wt;
+        if (dim < d) a += s_acc[w][dim] * wt;
+    }
+    if (dim < d) dst[2 + dim] = a;
+    if (dim == 0) { dst[0] = mx; dst[1] = l; }
+}
+
 // Merge `nsplit` states [(m, l, acc[D])] of one head into out[0..D).  The
 // states are first staged into LDS with one coalesced burst, so the whole
-// merge pays a single memory latency.
+// merge pays a single memory latency.  With cur_q non-null one more state
+// joins the merge: the current token as a single row, logit
+// cur_q . cur_k * scale and value cur_v; its operands are loaded in the same
+// burst as the states.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxFloats = 16384;  // 64 KB of staged state
+constexpr int kMergeBatch = 16;
 constexpr int kMergeMaxSplits = 1024;
 
 template <typename T>
-__device__ __forceinline__ void merge_splits(const float* __restrict__ st, int nsplit, int d, T* out) {
+__device__ __forceinline__ void merge_splits(const float* __restrict__ st, int nsplit, int d, T* out,
+                                             const T* cur_q = nullptr, const T* cur_k = nullptr,
+                                             const T* cur_v = nullptr, float scale = 0.0f) {
     __shared__ float s_state[kMergeMaxFloats];
     __shared__ float s_w[kMergeMaxSplits];
-    __shared__ float s_den;
+    __shared__ float s_den, s_wc;
+    __shared__ float s_dot[kMergeThreads / kWave];
+    const int tid = threadIdx.x;
     const int n = nsplit * (d + 2);
     const bool staged = n <= kMergeMaxFloats;
-    if (staged) {
-        for (int i = threadIdx.x; i < n; i += kMergeThreads) s_state[i] = st[i];
-        __syncthreads();
+    const bool has_cur = cur_q != nullptr;
+    // the current token's operands for this thread's dimension
+    float cq = 0.0f, ck = 0.0f, cv = 0.0f;
+    if (has_cur && tid < d) {
+        cq = Elem<T>::load(cur_q, tid);
+        ck = Elem<T>::load(cur_k, tid);
+        cv = Elem<T>::load(cur_v, tid);
     }
+    if (staged) {
+        // Batches of kMergeBatch independent loads per thread, all in flight
+        // before the first LDS write (a plain copy loop waits on every load).
+        for (int base = 0; base < n; base += kMergeBatch * kMergeThreads) {
+            float v[kMergeBatch];
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const int i = base + j * kMergeThreads + tid;
+                v[j] = i < n ? st[i] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const int i = base + j * kMergeThreads + tid;
+                if (i < n) s_state[i] = v[j];
+            }
+        }
+    }
+    if (has_cur) {
+        const float prod = wave_sum(cq * ck);
+        if ((tid & (kWave - 1)) == 0) s_dot[tid / kWave] = prod;
+    }
+    __syncthreads();
     const float* src = staged ? s_state : st;
     // split weights e^{m_s - M} (0 for fully masked splits) and the denominator
-    if (threadIdx.x < kWave) {
-        float mx = -INFINITY;
-        for (int s = threadIdx.x; s < nsplit; s += kWave) mx = fmaxf(mx, src[s * (d + 2)]);
+    if (tid < kWave) {
+        float cur_m = -INFINITY;
+        if (has_cur) {
+            float dot = 0.0f;
+            for (int w = 0; w < kMergeThreads / kWave; ++w) dot += s_dot[w];
+            cur_m = dot * scale;
+        }
+        float mx = cur_m;
+        for (int s = tid; s < nsplit; s += kWave) mx = fmaxf(mx, src[s * (d + 2)]);
         mx = wave_max(mx);
         float den = 0.0f;
-        for (int s = threadIdx.x; s < nsplit; s += kWave) {
+        for (int s = tid; s < nsplit; s += kWave) {
             const float m = src[s * (d + 2)];
             const float w = m == -INFINITY ? 0.0f : __expf(m - mx);
             s_w[s] = w;
             den += src[s * (d + 2) + 1] * w;
         }
         den = wave_sum(den);
-        if (threadIdx.x == 0) s_den = den;
+        if (tid == 0) {
+            const float wc = cur_m == -INFINITY ? 0.0f : __expf(cur_m - mx);
+            s_wc = wc;
+            s_den = den + wc;
+        }
     }
     __syncthreads();
-    for (int dim = threadIdx.x; dim < d; dim += kMergeThreads) {
+    for (int dim = tid; dim < d; dim += kMergeThreads) {
         float num = 0.0f;
         for (int s = 0; s < nsplit; ++s) {
             const float w = s_w[s];
             if (w != 0.0f) num += src[s * (d + 2) + 2 + dim] * w;
         }
+        if (has_cur) num += s_wc * (dim == tid ? cv : Elem<T>::load(cur_v, dim));
         Elem<T>::store(out, dim, num / s_den);
     }
 }
@@ -250,44 +335,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         }
     }
 
-    // Merge the row slots of this wave (lanes with equal `sub`).
-#pragma unroll
-    for (int m = LPR; m < kWave; m <<= 1) {
-        const float m2 = __shfl_xor(st.m, m);
-        const float l2 = __shfl_xor(st.l, m);
-        float a2[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a2[i] = __shfl_xor(st.acc[i], m);
-        merge_state(st, m2, l2, a2);
-    }
-
-    // Merge across waves through LDS.
-    __shared__ float s_m[kAttnWaves], s_l[kAttnWaves];
-    __shared__ float s_acc[kAttnWaves][256];
-    if (lane < LPR) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s_acc[wave][dim0 + i] = st.acc[i];
-        if (lane == 0) { s_m[wave] = st.m; s_l[wave] = st.l; }
-    }
-    __syncthreads();
-    float* dst = partials + (static_cast<int64_t>(h) * nsplit + s) * (d + 2);
-    {
-        const int dim = threadIdx.x;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, s_m[w]);
-        float l = 0.0f, a = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) {
-            if (s_m[w] == -INFINITY) continue;
-            const float wt = __expf(s_m[w] - mx);
-            l += s_l[w] * wt;
-            if (dim < d) a += s_acc[w][dim] * wt;
-        }
-        if (dim < d) dst[2 + dim] = a;
-        if (dim == 0) { dst[0] = mx; dst[1] = l; }
-    }
-
+    store_partial<LPR>(st, lane, wave, dim0, d, partials + (static_cast<int64_t>(h) * nsplit + s) * (d + 2));
 }
 
 template <typename T>
@@ -298,6 +346,164 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
                     out + static_cast<int64_t>(h) * d);
 }
 
+
+// ---------------------------------------------------------------- layer step
+
+// Layer-step attention.  The select kernel leaves each head's selection as a
+// bit mask over the prefix tokens (bit t of word t/32).  Workgroup (s, h)
+// takes the selected tokens of ranks [256s, 256s + 256) in ascending token
+// order -- the reference's 256-token split -- so every workgroup gathers the
+// same number of rows: it loads the head's whole mask (4 KB at 32K tokens),
+// one block scan of per-thread popcounts gives every mask word its first
+// rank, and the threads whose words hold the split's ranks write those tokens
+// to LDS.  The current token is not in the mask; the merge adds it.  Rows are
+// contiguous (token stride = head_dim = 128).  For 16-bit types the Q.K
+// products use v_dot2 (two products accumulated in fp32 per instruction).
+constexpr int kSplitRows = 256;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Dot product of 8 packed 16-bit elements with v_dot2 (fp32 accumulation).
+template <typename T>
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
+    auto d2 = [](uint32_t x, uint32_t y, float c) {
+        if constexpr (Elem<T>::kDtype == POPKV_DTYPE_BF16)
+            return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), __builtin_bit_cast(bf16x2_t, y), c,
+                                                   false);
+        else
+            return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, y), c, false);
+    };
+    return d2(a.w, b.w, d2(a.z, b.z, d2(a.y, b.y, d2(a.x, b.x, 0.0f))));
+}
+
+template <typename T, int NB, int WPT>
+__global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
+    const uint32_t* __restrict__ mask, int64_t mask_stride, int64_t tokens, int64_t k,
+    const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials, int nsplit) {
+    static_assert(WPT % 4 == 0, "mask words are read as 16-byte packets");
+    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, ROWS_PER_PASS = SLOTS * kAttnWaves;
+    const int h = blockIdx.y;
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int sub = lane % LPR;
+    const int slot = wave * SLOTS + lane / LPR;
+    const int dim0 = sub * 8;
+    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+
+    // this thread's WPT consecutive mask words, then the query slice
+    const int nwords = static_cast<int>((tokens + 31) / 32);
+    const uint32_t* mrow = mask + static_cast<int64_t>(h) * mask_stride;
+    uint32_t mw[WPT];
+#pragma unroll
+    for (int i = 0; i < WPT; i += 4) {
+        const int e = tid * WPT + i;
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (e < nwords) u = *reinterpret_cast<const uint4*>(mrow + e);  // rows padded to 4 words
+        mw[i] = u.x;
+        mw[i + 1] = e + 1 < nwords ? u.y : 0u;
+        mw[i + 2] = e + 2 < nwords ? u.z : 0u;
+        mw[i + 3] = e + 3 < nwords ? u.w : 0u;
+    }
+    Raw8<T> qr;
+    qr.load(q + static_cast<int64_t>(h) * D + dim0);
+
+    // tokens of ranks [r0, r1) in ascending order -> s_tok
+    __shared__ int32_t s_tok[kSplitRows];
+    __shared__ uint32_t s_scan[kAttnWaves + 1];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) cnt += __popc(mw[i]);
+    uint32_t total;
+    uint32_t rank = block_excl_scan(cnt, s_scan, kAttnWaves, &total);
+    const uint32_t r0 = static_cast<uint32_t>(s) * kSplitRows;
+    const uint32_t r1 = min(r0 + kSplitRows, static_cast<uint32_t>(k));
+    if (rank < r1 && rank + cnt > r0) {
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) {
+            const int32_t tbase = (tid * WPT + i) * 32;
+            for (uint32_t m = mw[i]; m; m &= m - 1) {
+                if (rank >= r0 && rank < r1) s_tok[rank - r0] = tbase + __builtin_ctz(m);
+                ++rank;
+            }
+        }
+    }
+    __syncthreads();
+    const int n_rows = static_cast<int>(r1 - r0);
+
+    const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
+    const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
+    SoftmaxState st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = 0.0f;
+    for (int base = 0; base < n_rows; base += ROWS_PER_PASS * NB) {
+        Raw8<T> kr[NB], vr[NB];
+        bool live[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int r = base + b * ROWS_PER_PASS + slot;
+            live[b] = r < n_rows;
+            // an idle slot re-reads the split's first selected row (its
+            // weight is exactly 0), so no unselected row's data is touched
+            const uint32_t off = static_cast<uint32_t>(s_tok[live[b] ? r : 0]) * (D * sizeof(T));
+            kr[b].load(reinterpret_cast<const T*>(kb + off));
+            vr[b].load(reinterpret_cast<const T*>(vb + off));
+        }
+        float logit[NB];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float dot;
+            if constexpr (sizeof(T) == 2) {
+                dot = dot8<T>(qr.u, kr[b].u);
+            } else {
+                dot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dot = fmaf(qr.get(i), kr[b].get(i), dot);
+            }
+            dot = row_sum<LPR>(dot);
+            logit[b] = live[b] ? dot * scale : -INFINITY;
+            bm = fmaxf(bm, logit[b]);
+        }
+        // every slot has at least its first row live in a non-empty pass, so
+        // bm is finite wherever live[0]; fully idle slots keep m = -inf
+        const float mnew = fmaxf(st.m, bm);
+        if (mnew != -INFINITY) {
+            const float alpha = __expf(st.m - mnew);  // st.m = -inf gives 0
+            st.l *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float p = __expf(logit[b] - mnew);  // -inf logit gives 0
+                st.l += p;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) st.acc[i] = fmaf(p, vr[b].get(i), st.acc[i]);
+            }
+            st.m = mnew;
+        }
+    }
+    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
+}
+
+// Layer-step merge: the split states of head h plus the current token
+// (logit q.cur_k * scale, value cur_v), written in the query dtype.
+template <typename T>
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_current_kernel(
+    const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
+    const T* __restrict__ cur_v, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
+    T* __restrict__ out) {
+    constexpr int D = 128;
+    const int h = blockIdx.x;
+    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (D + 2), nsplit, D, out + static_cast<int64_t>(h) * D,
+                    q + static_cast<int64_t>(h) * D, cur_k + kvh * D, cur_v + kvh * D, scale);
+}
 
 // Typed arguments of one partial-attention launch.
 template <typename T, typename IdxT>
@@ -404,5 +610,71 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
     return hipGetLastError();
 }
 
+
+namespace {
+template <typename T>
+hipError_t launch_rank_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs,
+                         const uint32_t* mask, int64_t mask_stride, int64_t tokens, int64_t k, int nsplit,
+                         const int64_t* h2k, int q_heads, int kv_heads, float* partials, hipStream_t stream) {
+    constexpr int NB = sizeof(T) == 4 ? 8 : 16;
+    const float scale = static_cast<float>(1.0 / sqrt(128.0));
+    dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(q_heads));
+    const int64_t words = (tokens + 31) / 32;
+#define POPKV_RANK(W)                                                                                               \
+    hipLaunchKernelGGL((attn_rank_kernel<T, NB, W>), grid, dim3(kAttnThreads), 0, stream, static_cast<const T*>(q), \
+                       static_cast<const T*>(kc), static_cast<const T*>(vc), k_hs, v_hs, mask, mask_stride, tokens, \
+                       k, h2k, kv_heads, scale, partials, nsplit)
+    if (words <= 4 * kAttnThreads) POPKV_RANK(4);
+    else if (words <= 8 * kAttnThreads) POPKV_RANK(8);
+    else POPKV_RANK(16);
+#undef POPKV_RANK
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_merge_current_t(const float* partials, int nsplit, const void* q, const void* cur_k,
+                                  const void* cur_v, const int64_t* h2k, int q_heads, int kv_heads, void* out,
+                                  hipStream_t stream) {
+    const float scale = static_cast<float>(1.0 / sqrt(128.0));
+    hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kMergeThreads), 0,
+                       stream, partials, nsplit, static_cast<const T*>(q), static_cast<const T*>(cur_k),
+                       static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out));
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attention_ranks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                  int64_t k_head_stride, int64_t v_head_stride, const uint32_t* mask,
+                                  int64_t mask_stride, int64_t tokens, int64_t k, int nsplit,
+                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                  hipStream_t stream) {
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_rank_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, mask, mask_stride,
+                                        tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
+        case POPKV_DTYPE_F16:
+            return launch_rank_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, mask, mask_stride,
+                                        tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
+        default:
+            return launch_rank_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, mask, mask_stride,
+                                         tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
+    }
+}
+
+hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,
+                                const void* current_k, const void* current_v, const int64_t* head_to_kv, int q_heads,
+                                int kv_heads, void* output, hipStream_t stream) {
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_merge_current_t<float>(partials, nsplit, queries, current_k, current_v, head_to_kv, q_heads,
+                                                 kv_heads, output, stream);
+        case POPKV_DTYPE_F16:
+            return launch_merge_current_t<f16_t>(partials, nsplit, queries, current_k, current_v, head_to_kv, q_heads,
+                                                 kv_heads, output, stream);
+        default:
+            return launch_merge_current_t<bf16_t>(partials, nsplit, queries, current_k, current_v, head_to_kv,
+                                                  q_heads, kv_heads, output, stream);
+    }
+}
 
 }  // namespace popkv

@@ -47,20 +47,24 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Workspace layout of popkv_layer_step (batch 1, head_dim 128).
 struct StepLayout {
-    size_t hist, scores, indices, partials, total;
-    int64_t score_stride, k, nsplit;
+    size_t hist, scores, mask, partials, total;
+    int64_t score_stride, mask_stride, k, nsplit;
 };
 
+// Layer-step workspace: [QH][256] u32 key histograms | [QH][score_stride] u16
+// order keys | [QH][mask_stride] u32 selection masks | [QH][nsplit][130] f32
+// split partials (256 selected tokens per split, the reference's split size).
 StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     StepLayout L{};
     L.k = budget - 1 < tokens ? budget - 1 : tokens;
-    L.nsplit = ceil_div(L.k + 1, kLayerSplit);
-    L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 64) * 64;
+    L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 128) * 128;
+    L.mask_stride = L.score_stride / 32;  // a multiple of 4 words
+    L.nsplit = ceil_div(L.k, kLayerSplit);
     size_t off = 0;
     L.hist = off; off = align_up(off + static_cast<size_t>(qh) * 256 * 4);
     L.scores = off; off = align_up(off + static_cast<size_t>(qh * L.score_stride) * 2);
-    L.indices = off; off = align_up(off + static_cast<size_t>(qh * (L.k + 1)) * 4);
-    L.partials = off; off = align_up(off + static_cast<size_t>(qh * L.nsplit * (128 + 2)) * 4);
+    L.mask = off; off = align_up(off + static_cast<size_t>(qh * L.mask_stride) * 4);
+    L.partials = off; off = align_up(off + static_cast<size_t>(qh * (L.nsplit > 0 ? L.nsplit : 1) * (128 + 2)) * 4);
     L.total = off;
     return L;
 }
@@ -302,9 +306,8 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
     char* ws = static_cast<char*>(workspace);
     uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
+    uint32_t* mask = reinterpret_cast<uint32_t*>(ws + L.mask);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
-    void* idx = indices_out ? static_cast<void*>(indices_out) : static_cast<void*>(ws + L.indices);
-    const int idx_dtype = indices_out ? POPKV_INDEX_I64 : POPKV_INDEX_I32;
     hipStream_t s = as_stream(stream);
 
     // 1. query encode + popcount score -> radix order keys of the fp16 scores
@@ -316,19 +319,26 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
                                                tokens, dim_group_size, keys, L.score_stride, hist, s),
                   "popkv_layer_step(score)");
     if (st) return st;
-    // 2. top-k + current token (re-zeroes the histograms)
-    st = launched(popkv::launch_topk_select_keys(keys, hist, q_heads, L.score_stride, tokens, L.k, tokens, idx,
-                                                 idx_dtype, L.k + 1, s),
+    // 2. top-k as a selection bit mask per head (re-zeroes the histograms)
+    st = launched(popkv::launch_topk_mask(keys, hist, q_heads, L.score_stride, tokens, L.k, mask, L.mask_stride, s),
                   "popkv_layer_step(select)");
     if (st) return st;
-    // 3. split partial attention, 4. log-sum-exp merge
-    st = launched(popkv::launch_attention_partial(queries, dtype, prefix_k, prefix_v, k_head_stride, 128,
-                                                  v_head_stride, 128, tokens, current_k, current_v, idx, idx_dtype,
-                                                  L.k + 1, nullptr, head_to_kv, static_cast<int>(q_heads),
-                                                  static_cast<int>(kv_heads), 128, L.k + 1, kLayerSplit, partials, s),
+    if (indices_out) {
+        st = launched(popkv::launch_mask_to_indices(mask, q_heads, L.mask_stride, tokens, L.k, tokens, indices_out,
+                                                    L.k + 1, s),
+                      "popkv_layer_step(indices)");
+        if (st) return st;
+    }
+    // 3. sparse attention over 256-token rank splits of each head's selection,
+    // 4. log-sum-exp merge of the splits and the current token
+    st = launched(popkv::launch_attention_ranks(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride, mask,
+                                                L.mask_stride, tokens, L.k, static_cast<int>(L.nsplit), head_to_kv,
+                                                static_cast<int>(q_heads), static_cast<int>(kv_heads), partials, s),
                   "popkv_layer_step(attention)");
     if (st) return st;
-    return launched(popkv::launch_attention_merge(partials, static_cast<int>(q_heads), L.nsplit, 128, output, dtype, s),
+    return launched(popkv::launch_merge_current(partials, static_cast<int>(L.nsplit), queries, dtype, current_k,
+                                                current_v, head_to_kv, static_cast<int>(q_heads),
+                                                static_cast<int>(kv_heads), output, s),
                     "popkv_layer_step(merge)");
 }
 

@@ -153,7 +153,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+    // bound_ctrl set: every control used here reads a lane inside the same
+    // row, so it changes nothing and lets the move fold into the consumer.
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
 }
 template <int N>
 __device__ __forceinline__ float row_sum(float v) {
@@ -163,6 +165,24 @@ __device__ __forceinline__ float row_sum(float v) {
     v += dpp_mov<0x141>(v);
     if constexpr (N == 16) v += dpp_mov<0x140>(v);
     return v;
+}
+
+// Wave-wide max / min: DPP within each 16-lane row, then the four row
+// results combined through readlane (the result is wave-uniform).  Exact:
+// max / min do not depend on the combination order.
+template <bool MAX>
+__device__ __forceinline__ float wave_extreme(float v) {
+    auto f = [](float a, float b) { return MAX ? fmaxf(a, b) : fminf(a, b); };
+    v = f(v, dpp_mov<0xB1>(v));
+    v = f(v, dpp_mov<0x4E>(v));
+    v = f(v, dpp_mov<0x141>(v));
+    v = f(v, dpp_mov<0x140>(v));
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 48));
+    return f(f(r0, r1), f(r2, r3));
 }
 
 // Inclusive prefix sum across the wave.

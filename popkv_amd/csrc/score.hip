@@ -111,29 +111,46 @@ __global__ __launch_bounds__(kWave) void query_encode_kernel(
 
 // ---------------------------------------------------------------- score, D = 128
 
-// Four signed agreement counts of one representative over the masked bits of
-// word pair (w0, w1) (w1 unused when ONE_WORD), combined with the fp32 chain.
+// Bits of representative r inside 32-bit word w of a 128-bit plane.
+template <int G>
+__device__ __forceinline__ uint32_t rep_mask(int r, int w) {
+    if constexpr (G == 64) return (w / 2 == r) ? 0xffffffffu : 0u;
+    else if constexpr (G == 32) return w == r ? 0xffffffffu : 0u;
+    else return w == r / 2 ? ((r & 1) ? 0xffff0000u : 0x0000ffffu) : 0u;
+}
+
+// popcount of the bits of representative r in a 128-bit plane.
+template <int G>
+__device__ __forceinline__ int rep_popc(const uint32_t* x, int r) {
+    if constexpr (G == 64) return __popc(x[2 * r]) + __popc(x[2 * r + 1]);
+    else if constexpr (G == 32) return __popc(x[r]);
+    else return __popc(x[r / 2] & rep_mask<16>(r, r / 2));
+}
+
+// Four signed agreement counts of representative r (2*popc(x & sel) -
+// popc(sel) over its G dims), combined with the fp32 chain of the reference.
+// pq = popc(query mag bits of r), pk = popc(key mag bits of r): they depend
+// on one side only and are computed once per head / token by the caller.
 template <int G>
 __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm, const uint32_t* ks,
-                                          const uint32_t* km, int r, float ql, float dq, float kl, float dk) {
-    int cs, cq, ck, cqk;
-    if constexpr (G == 64) {
-        const uint32_t m0 = ~(qs[2 * r] ^ ks[2 * r]), m1 = ~(qs[2 * r + 1] ^ ks[2 * r + 1]);
-        const uint32_t b0 = qm[2 * r] & km[2 * r], b1 = qm[2 * r + 1] & km[2 * r + 1];
-        cs = 2 * (__popc(m0) + __popc(m1)) - 64;
-        cq = 2 * (__popc(m0 & qm[2 * r]) + __popc(m1 & qm[2 * r + 1])) - (__popc(qm[2 * r]) + __popc(qm[2 * r + 1]));
-        ck = 2 * (__popc(m0 & km[2 * r]) + __popc(m1 & km[2 * r + 1])) - (__popc(km[2 * r]) + __popc(km[2 * r + 1]));
-        cqk = 2 * (__popc(m0 & b0) + __popc(m1 & b1)) - (__popc(b0) + __popc(b1));
-    } else {
-        const int w = G == 32 ? r : r / 2;
-        const uint32_t mask = G == 32 ? 0xffffffffu : ((r & 1) ? 0xffff0000u : 0x0000ffffu);
-        const uint32_t qmm = qm[w] & mask, kmm = km[w] & mask;
-        const uint32_t match = ~(qs[w] ^ ks[w]) & mask, both = qmm & kmm;
-        cs = 2 * __popc(match) - (G == 32 ? 32 : 16);
-        cq = 2 * __popc(match & qmm) - __popc(qmm);
-        ck = 2 * __popc(match & kmm) - __popc(kmm);
-        cqk = 2 * __popc(match & both) - __popc(both);
+                                          const uint32_t* km, int r, int pq, int pk, float ql, float dq,
+                                          float kl, float dk) {
+    constexpr int NW = G == 64 ? 2 : 1;
+    const int w0 = G == 64 ? 2 * r : (G == 32 ? r : r / 2);
+    int a = 0, aq = 0, ak = 0, aqk = 0, b = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const int w = w0 + i;
+        const uint32_t sel = G == 16 ? rep_mask<16>(r, w) : 0xffffffffu;
+        const uint32_t m = ~(qs[w] ^ ks[w]) & sel;
+        const uint32_t both = qm[w] & km[w] & sel;
+        a += __popc(m);
+        aq += __popc(m & qm[w]);
+        ak += __popc(m & km[w]);
+        aqk += __popc(m & both);
+        b += __popc(both);
     }
+    const int cs = 2 * a - G, cq = 2 * aq - pq, ck = 2 * ak - pk, cqk = 2 * aqk - b;
     return fmaf(ql * kl, static_cast<float>(cs),
                 fmaf(dq * kl, static_cast<float>(cq),
                      fmaf(ql * dk, static_cast<float>(ck), dq * dk * static_cast<float>(cqk))));
@@ -154,13 +171,16 @@ struct GroupState {
 // decode-path order.  Wave w handles heads w, w+4, ...; the caller has
 // already loaded dims lane and lane+64 of those rows into qv[][2] (so the
 // query loads are issued ahead of the token loads).  Each wave forms the
-// whole-head extrema and sign/magnitude words; then one thread per (head,
-// representative) folds its G values in ascending dimension order (adding +0
-// for the other bucket is exact, so the fold is branch-free).  All threads of
-// the block call it.
+// whole-head extrema, the sign/magnitude words and, for every dimension, its
+// contribution to the low and to the high bucket (|q| or +0), staged in LDS.
+// One thread per (head, representative) then runs the two
+// ascending-dimension fp32 add chains over those contributions -- adding +0
+// for the other bucket is exact, so this is the reference's fold -- and the
+// bucket counts are popcounts of the magnitude words.  All threads of the
+// block call it.
 template <int G, int MAXW>
-__device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk, GroupState<G>& st, float (*stage)[128],
-                                  float (*thr)[2]) {
+__device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk, GroupState<G>& st,
+                                                  float (*lo_c)[128], float (*hi_c)[128]) {
     constexpr int R = 128 / G;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -169,40 +189,42 @@ __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk,
         const int h = wave + i * (kScoreThreads / kWave);
         if (h >= qpk) break;
         const float v0 = qv[i][0], v1 = qv[i][1];
-        stage[h][lane] = v0;
-        stage[h][lane + 64] = v1;
-        const float mn = wave_min(fminf(v0, v1)), mx = wave_max(fmaxf(v0, v1));
+        const float mn = wave_extreme<false>(fminf(v0, v1)), mx = wave_extreme<true>(fmaxf(v0, v1));
         const float neg = mn * 0.5f, pos = mx * 0.5f;
         const bool s0 = v0 >= 0.0f, s1 = v1 >= 0.0f;
         const bool m0 = s0 ? v0 > pos : v0 < neg, m1 = s1 ? v1 > pos : v1 < neg;
+        const float a0 = fabsf(v0), a1 = fabsf(v1);
+        lo_c[h][lane] = m0 ? 0.0f : a0;
+        hi_c[h][lane] = m0 ? a0 : 0.0f;
+        lo_c[h][lane + 64] = m1 ? 0.0f : a1;
+        hi_c[h][lane + 64] = m1 ? a1 : 0.0f;
         const uint64_t bs0 = __ballot(s0), bs1 = __ballot(s1), bm0 = __ballot(m0), bm1 = __ballot(m1);
         if (lane == 0) {
             st.qs[h][0] = static_cast<uint32_t>(bs0); st.qs[h][1] = static_cast<uint32_t>(bs0 >> 32);
             st.qs[h][2] = static_cast<uint32_t>(bs1); st.qs[h][3] = static_cast<uint32_t>(bs1 >> 32);
             st.qm[h][0] = static_cast<uint32_t>(bm0); st.qm[h][1] = static_cast<uint32_t>(bm0 >> 32);
             st.qm[h][2] = static_cast<uint32_t>(bm1); st.qm[h][3] = static_cast<uint32_t>(bm1 >> 32);
-            thr[h][0] = neg;
-            thr[h][1] = pos;
         }
     }
     __syncthreads();
     for (int item = threadIdx.x; item < qpk * R; item += kScoreThreads) {
         const int h = item / R, r = item % R;
-        const float neg = thr[h][0], pos = thr[h][1];
         float ls = 0.0f, hs = 0.0f;
-        int hn = 0;
 #pragma unroll
         for (int j = 0; j < G; j += 4) {
-            const float4 f = *reinterpret_cast<const float4*>(&stage[h][r * G + j]);
-            const float x[4] = {f.x, f.y, f.z, f.w};
+            const float4 l4 = *reinterpret_cast<const float4*>(&lo_c[h][r * G + j]);
+            const float4 h4 = *reinterpret_cast<const float4*>(&hi_c[h][r * G + j]);
+            ls = ls + l4.x; ls = ls + l4.y; ls = ls + l4.z; ls = ls + l4.w;
+            hs = hs + h4.x; hs = hs + h4.y; hs = hs + h4.z; hs = hs + h4.w;
+        }
+        // high-bucket count: popcount of the G magnitude bits at r*G
+        int hn = 0;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const bool mg = x[u] >= 0.0f ? x[u] > pos : x[u] < neg;
-                const float a = fabsf(x[u]);
-                ls = ls + (mg ? 0.0f : a);
-                hs = hs + (mg ? a : 0.0f);
-                hn += mg ? 1 : 0;
-            }
+        for (int w = 0; w < 4; ++w) {
+            if ((w + 1) * 32 <= r * G || w * 32 >= (r + 1) * G) continue;
+            uint32_t bits = st.qm[h][w];
+            if constexpr (G == 16) bits = (r & 1) ? (bits >> 16) : (bits & 0xffffu);
+            hn += __popc(bits);
         }
         finish_rep(ls, G - hn, hs, hn, st.ql[h][r], st.qd[h][r]);
     }
@@ -293,17 +315,19 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     if constexpr (std::is_void_v<QT>) {
         load_group_state<G>(q_sign, q_mag, q_low, q_delta, qrow0, qpk, st);
     } else {
-        __shared__ __align__(16) float stage[QPK > 0 ? QPK : kMaxGroupHeads][128];
-        __shared__ float thr[QPK > 0 ? QPK : kMaxGroupHeads][2];
-        encode_group_fold<G, MAXW>(qv, qpk, st, stage, thr);
+        __shared__ __align__(16) float lo_c[QPK > 0 ? QPK : kMaxGroupHeads][128];
+        __shared__ __align__(16) float hi_c[QPK > 0 ? QPK : kMaxGroupHeads][128];
+        encode_group_fold<G, MAXW>(qv, qpk, st, lo_c, hi_c);
     }
 
+    // Token-side operands, decoded once and reused for every head.
+    uint32_t ks[TPT][4], km[TPT][4];
+    float kl[TPT][R], dk[TPT][R];
+    int pk[TPT][R];
 #pragma unroll
     for (int it = 0; it < TPT; ++it) {
-        const int64_t t = tok[it];
-        if (t >= tokens) break;
-        const uint32_t ks[4] = {s4[it].x, s4[it].y, s4[it].z, s4[it].w};
-        const uint32_t km[4] = {m4[it].x, m4[it].y, m4[it].z, m4[it].w};
+        ks[it][0] = s4[it].x; ks[it][1] = s4[it].y; ks[it][2] = s4[it].z; ks[it][3] = s4[it].w;
+        km[it][0] = m4[it].x; km[it][1] = m4[it].y; km[it][2] = m4[it].z; km[it][3] = m4[it].w;
         uint32_t lws[R / 2], dws[R / 2];
         if constexpr (R == 2) {
             lws[0] = lw[it]; dws[0] = dw[it];
@@ -313,30 +337,47 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
             lws[0] = lw[it].x; lws[1] = lw[it].y; lws[2] = lw[it].z; lws[3] = lw[it].w;
             dws[0] = dw[it].x; dws[1] = dw[it].y; dws[2] = dw[it].z; dws[3] = dw[it].w;
         }
-        float kl[R], dk[R];
 #pragma unroll
         for (int i = 0; i < R / 2; ++i) {
-            kl[2 * i] = bits_f16(lws[i] & 0xffffu); kl[2 * i + 1] = bits_f16(lws[i] >> 16);
-            dk[2 * i] = bits_f16(dws[i] & 0xffffu); dk[2 * i + 1] = bits_f16(dws[i] >> 16);
+            kl[it][2 * i] = bits_f16(lws[i] & 0xffffu); kl[it][2 * i + 1] = bits_f16(lws[i] >> 16);
+            dk[it][2 * i] = bits_f16(dws[i] & 0xffffu); dk[it][2 * i + 1] = bits_f16(dws[i] >> 16);
         }
-        for (int h = 0; h < qpk; ++h) {
-            // The group state is uniform: readfirstlane keeps it in SGPRs.
-            uint32_t qs[4], qm[4];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                qs[w] = __builtin_amdgcn_readfirstlane(st.qs[h][w]);
-                qm[w] = __builtin_amdgcn_readfirstlane(st.qm[h][w]);
-            }
+        for (int r = 0; r < R; ++r) pk[it][r] = rep_popc<G>(km[it], r);
+    }
+    for (int h = 0; h < qpk; ++h) {
+        // The group state is uniform: readfirstlane keeps it in SGPRs, read
+        // once per head.
+        uint32_t qs[4], qm[4];
+        float ql[R], dq[R];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            qs[w] = __builtin_amdgcn_readfirstlane(st.qs[h][w]);
+            qm[w] = __builtin_amdgcn_readfirstlane(st.qm[h][w]);
+        }
+        int pq[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ql[r] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.ql[h][r])));
+            dq[r] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.qd[h][r])));
+            pq[r] = rep_popc<G>(qm, r);
+        }
+#pragma unroll
+        for (int it = 0; it < TPT; ++it) {
+            const int64_t t = tok[it];
+            if (t >= tokens) break;
             float total = 0.0f;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float ql = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.ql[h][r])));
-                const float dq = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.qd[h][r])));
-                total = total + rep_term<G>(qs, qm, ks, km, r, ql, dq, kl[r], dk[r]);
-            }
-            const uint16_t bits = f16_rne(total * 0x1.6a09e6p-4f);  // fp32(1/sqrt(128)) = 0x3DB504F3
+            for (int r = 0; r < R; ++r) total = total + rep_term<G>(qs, qm, ks[it], km[it], r, pq[r], pk[it][r], ql[r], dq[r],
+                                                           kl[it][r], dk[it][r]);
+            const float sc = total * 0x1.6a09e6p-4f;  // fp32(1/sqrt(128)) = 0x3DB504F3
+            const uint16_t bits = f16_rne(sc);
             if constexpr (STEP) {
-                const uint32_t key = order_key(bits);
+                // order_key(bits), with the NaN test done on the fp32 value
+                // (an fp32 NaN is exactly an fp16 NaN after the conversion)
+                const uint32_t b = bits;
+                const uint32_t flip = (static_cast<uint32_t>(static_cast<int32_t>(b << 16) >> 31) & 0xffffu) | 0x8000u;
+                const uint32_t key = sc != sc ? 0xffffu : (b ^ flip);
                 scores[(qrow0 + h) * out_stride + t] = static_cast<uint16_t>(key);
                 atomicAdd(&s_hist[h][key >> 8], 1u);
             } else {

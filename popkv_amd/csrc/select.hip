@@ -203,140 +203,181 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
     if (tid == 0) dst[k] = static_cast<IdxT>(current);
 }
 
-// Layer-step select.  The input rows already hold radix order keys and the
-// scorer has accumulated each row's high-byte histogram into ghist, so the
-// first radix level costs nothing here: one pass classifies every key against
-// the k-th key's high byte into per-thread bit masks (above / candidate), only
-// the candidates sharing that byte feed a second 256-bin histogram, and the
-// ordered write-out walks the set bits of the selection mask.  ghist is
-// re-zeroed for the next call.
-template <int SEG, typename IdxT>
-__global__ __launch_bounds__(kSelThreads) void topk_select_keys_kernel(
-    const uint16_t* __restrict__ keys, uint32_t* __restrict__ ghist, int64_t row_stride, int64_t tokens, int64_t k,
-    int64_t current, IdxT* __restrict__ out, int64_t out_stride) {
-    constexpr int MW = (SEG + 31) / 32;  // 32-bit mask words per thread
+// Layer-step select, bit-mask form.  The input rows hold radix order keys and
+// the scorer has accumulated each row's high-byte histogram into ghist, so
+// the first radix level costs nothing here.  Thread t of the block handles
+// tokens t, t + 1024, t + 2048, ...: round j of a wave covers 64 consecutive
+// tokens, so one ballot of a comparison is directly that 64-token word of the
+// selection mask, and lane j of the wave collects round j's word for one
+// store at the end.
+//   1. bin b1 of the k-th largest key from ghist;
+//   2. 256-bin histogram of the low byte of the keys with high byte b1 ->
+//      the k-th largest key T, need_eq = how many keys equal to T are taken;
+//   3. if some keys equal to T are left out, the last one taken is the
+//      need_eq-th in token order (PyTorch's gather-top-k tie rule: the lowest
+//      indices win): per-(round, wave) tie counts and masks, one block scan,
+//      and the owner of the crossing group finds the token tau;
+//   4. mask bit of token t: key > T, or key == T and t <= tau.
+// Absent tokens (past `tokens`) get key 0, below every real key (real keys
+// are >= 0x03ff; NaN patterns map to 0xffff).  JB rounds of keys are held in
+// registers; with MULTI (more than JB rounds) every pass re-reads its keys in
+// batches of JB rounds.  The mask row holds ceil(tokens/64) 64-bit words,
+// bits past `tokens` zero.  ghist is re-zeroed for the next call.
+constexpr int kMaskMaxRounds = 128;                         // tokens <= 131072
+constexpr int kMaskTieSlots = kMaskMaxRounds * kSelWaves;  // per-(round, wave) tie counts
+
+template <int JB, bool MULTI>
+__global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
+    const uint16_t* __restrict__ keys, uint32_t* __restrict__ ghist, int64_t row_stride, int ntok, int k,
+    uint32_t* __restrict__ mask, int64_t mask_stride) {
+    static_assert(JB <= kWave, "one collecting lane per round");
+    constexpr int SLOTS = MULTI ? kMaskTieSlots : JB * kSelWaves;
     const int64_t row = blockIdx.x;
     const uint16_t* src = keys + row * row_stride;
     uint32_t* gh = ghist + row * kBins;
-    IdxT* dst = out + row * out_stride;
+    uint32_t* mrow = mask + row * mask_stride;
     const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int rounds = (ntok + kSelThreads - 1) / kSelThreads;
 
     __shared__ uint32_t tot[kBins], hist2[kBins];
     __shared__ uint32_t scan_sh[kSelWaves + 1];
-    __shared__ uint32_t s_bin, s_above;
-    __shared__ int32_t stage[kStageMax];
+    __shared__ uint32_t s_bin, s_above, s_tau;
+    __shared__ uint32_t s_tie[SLOTS];
+    __shared__ uint64_t s_eq[SLOTS];
     if (tid < kBins) {
         tot[tid] = gh[tid];
         gh[tid] = 0u;
         hist2[tid] = 0u;
     }
-    if (k >= tokens) {
-        for (int64_t t = tid; t < tokens; t += kSelThreads) dst[t] = static_cast<IdxT>(t);
-        if (tid == 0) dst[tokens] = static_cast<IdxT>(current);
-        return;
-    }
-    if (k == 0) {
-        if (tid == 0) dst[0] = static_cast<IdxT>(current);
-        return;
-    }
-
-    const int64_t begin = static_cast<int64_t>(tid) * SEG;
-    const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(SEG, tokens - begin)));
-    uint32_t kp[SEG / 2];
+    // mode 0: nothing selected (k == 0); 1: every token (k >= ntok); 2: threshold
+    const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);
+    uint32_t thr = 0xffffffffu;
+    int tau = ntok;
+    uint32_t kr[JB];
+    auto load = [&](int j0) {
 #pragma unroll
-    for (int c = 0; c < SEG / 8; ++c) {
-        uint4 u = make_uint4(0u, 0u, 0u, 0u);
-        if (8 * c < n) u = *reinterpret_cast<const uint4*>(src + begin + 8 * c);  // rows are padded to 16 bytes
-        kp[4 * c] = u.x; kp[4 * c + 1] = u.y; kp[4 * c + 2] = u.z; kp[4 * c + 3] = u.w;
-    }
-#define POPKV_KEY(e) ((kp[(e) >> 1] >> (((e) & 1) * 16)) & 0xffffu)
-    __syncthreads();
-    find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
-    __syncthreads();
-    const uint32_t b1 = s_bin;
-    const uint32_t above1 = s_above;
-
-    // low-byte histogram of the keys sharing the k-th key's high byte
+        for (int jj = 0; jj < JB; ++jj) {
+            const int t = (j0 + jj) * kSelThreads + tid;
+            const uint32_t v = src[min(t, ntok - 1)];
+            kr[jj] = t < ntok ? v : 0u;
+        }
+    };
+    if (mode == 2) {
+        if (!MULTI) load(0);
+        __syncthreads();
+        find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
+        __syncthreads();
+        const uint32_t b1 = s_bin;
+        const uint32_t above1 = s_above;
+        for (int j0 = 0; j0 < rounds; j0 += JB) {
+            if (MULTI) load(j0);
 #pragma unroll
-    for (int e = 0; e < SEG; ++e) {
-        const uint32_t key = POPKV_KEY(e);
-        if (e < n && (key >> 8) == b1) atomicAdd(&hist2[key & 0xffu], 1u);
-    }
-    __syncthreads();
-    find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
-    __syncthreads();
-    const uint32_t thr = (b1 << 8) | s_bin;
-    const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
-
-    // selection masks: key > T (selected outright) and key == T (ties)
-    uint32_t sel[MW], tie[MW];
+            for (int jj = 0; jj < JB; ++jj)
+                if ((kr[jj] >> 8) == b1) atomicAdd(&hist2[kr[jj] & 0xffu], 1u);
+            if (!MULTI) break;
+        }
+        __syncthreads();
+        find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
+        __syncthreads();
+        thr = (b1 << 8) | s_bin;
+        const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
+        if (need_eq < hist2[s_bin]) {  // some ties left out: find tau (block-uniform branch)
+            for (int j0 = 0; j0 < rounds; j0 += JB) {
+                if (MULTI) load(j0);
+                uint32_t tc = 0, tl = 0, th = 0;
 #pragma unroll
-    for (int w = 0; w < MW; ++w) { sel[w] = 0u; tie[w] = 0u; }
-#pragma unroll
-    for (int e = 0; e < SEG; ++e) {
-        const uint32_t key = POPKV_KEY(e);
-        const bool valid = e < n;
-        sel[e / 32] |= static_cast<uint32_t>(valid && key > thr) << (e & 31);
-        tie[e / 32] |= static_cast<uint32_t>(valid && key == thr) << (e & 31);
-    }
-    uint32_t n_gt = 0, n_eq = 0;
-#pragma unroll
-    for (int w = 0; w < MW; ++w) {
-        n_gt += __popc(sel[w]);
-        n_eq += __popc(tie[w]);
-    }
-#undef POPKV_KEY
-    uint32_t total, gt_before, eq_before;
-    if (tokens <= 0xffff) {
-        const uint32_t packed = block_excl_scan(n_gt | (n_eq << 16), scan_sh, kSelWaves, &total);
-        gt_before = packed & 0xffffu;
-        eq_before = packed >> 16;
-    } else {
-        gt_before = block_excl_scan(n_gt, scan_sh, kSelWaves, &total);
-        eq_before = block_excl_scan(n_eq, scan_sh, kSelWaves, &total);
-    }
-    const bool staged = k <= kStageMax;
-#pragma unroll
-    for (int w = 0; w < MW; ++w) {
-        for (uint32_t m = sel[w] | tie[w]; m; m &= m - 1) {
-            const int b = __builtin_ctz(m);
-            uint32_t slot = 0xffffffffu;
-            if ((sel[w] >> b) & 1u) {
-                slot = gt_before + min(eq_before, need_eq);
-                ++gt_before;
-            } else {
-                if (eq_before < need_eq) slot = gt_before + eq_before;
-                ++eq_before;
+                for (int jj = 0; jj < JB; ++jj) {
+                    const uint64_t eq = __ballot(kr[jj] == thr);
+                    tc = lane == jj ? static_cast<uint32_t>(__popcll(eq)) : tc;
+                    tl = lane == jj ? static_cast<uint32_t>(eq) : tl;
+                    th = lane == jj ? static_cast<uint32_t>(eq >> 32) : th;
+                }
+                if (lane < JB && j0 + lane < rounds) {
+                    const int e = (j0 + lane) * kSelWaves + wave;
+                    s_tie[e] = tc;
+                    s_eq[e] = (static_cast<uint64_t>(th) << 32) | tl;
+                }
+                if (!MULTI) break;
             }
-            if (slot != 0xffffffffu) {
-                const int64_t t = begin + w * 32 + b;
-                if (staged) stage[slot] = static_cast<int32_t>(t);
-                else dst[slot] = static_cast<IdxT>(t);
+            __syncthreads();
+            constexpr int PER = (SLOTS + kSelThreads - 1) / kSelThreads;
+            const int n_slots = rounds * kSelWaves;
+            uint32_t c[PER], local = 0;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int e = tid * PER + i;
+                c[i] = e < n_slots ? s_tie[e] : 0u;
+                local += c[i];
             }
+            uint32_t total;
+            uint32_t run = block_excl_scan(local, scan_sh, kSelWaves, &total);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int e = tid * PER + i;
+                if (run < need_eq && run + c[i] >= need_eq) {
+                    // the (need_eq - run)-th set bit of this group's tie mask
+                    uint64_t m = s_eq[e];
+                    for (uint32_t n = need_eq - run; n > 1; --n) m &= m - 1;
+                    s_tau = static_cast<uint32_t>((e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave +
+                                                  __builtin_ctzll(m));
+                }
+                run += c[i];
+            }
+            __syncthreads();
+            tau = static_cast<int>(s_tau);
         }
     }
-    if (staged) {
-        __syncthreads();
-        for (int64_t i = tid; i < k; i += kSelThreads) dst[i] = static_cast<IdxT>(stage[i]);
+    // mask words
+    for (int j0 = 0; j0 < rounds; j0 += JB) {
+        if (MULTI && mode == 2) load(j0);
+        uint32_t wl = 0, wh = 0;
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+            const int t = (j0 + jj) * kSelThreads + tid;
+            uint64_t word;
+            if (mode == 2) word = __ballot(kr[jj] > thr || (kr[jj] == thr && t <= tau));
+            else word = mode == 1 ? __ballot(t < ntok) : 0ull;
+            wl = lane == jj ? static_cast<uint32_t>(word) : wl;
+            wh = lane == jj ? static_cast<uint32_t>(word >> 32) : wh;
+        }
+        const int wbase = (j0 + lane) * kSelThreads + wave * kWave;
+        if (lane < JB && wbase < ntok) *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(wl, wh);
+        if (!MULTI) break;
     }
-    if (tid == 0) dst[k] = static_cast<IdxT>(current);
 }
 
-template <typename IdxT>
-hipError_t launch_keys_t(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
-                         int64_t k, int64_t current, IdxT* out, int64_t out_stride, hipStream_t stream) {
-    const int64_t per = (tokens + kSelThreads - 1) / kSelThreads;
-    dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
-#define POPKV_KEYSEL(S)                                                                                         \
-    hipLaunchKernelGGL((topk_select_keys_kernel<S, IdxT>), grid, block, 0, stream, keys, ghist, row_stride, tokens, \
-                       k, current, out, out_stride)
-    if (per <= 8) POPKV_KEYSEL(8);
-    else if (per <= 16) POPKV_KEYSEL(16);
-    else if (per <= 32) POPKV_KEYSEL(32);
-    else if (per <= 64) POPKV_KEYSEL(64);
-    else POPKV_KEYSEL(128);
-#undef POPKV_KEYSEL
-    return hipGetLastError();
+// Ascending indices of a selection mask, the current token in slot k.
+// One 1024-thread block per row; thread t owns WPT consecutive mask words.
+template <int WPT, typename IdxT>
+__global__ __launch_bounds__(kSelThreads) void mask_to_indices_kernel(
+    const uint32_t* __restrict__ mask, int64_t mask_stride, int64_t tokens, int64_t k, int64_t current,
+    IdxT* __restrict__ out, int64_t out_stride) {
+    const int64_t row = blockIdx.x;
+    const uint32_t* mrow = mask + row * mask_stride;
+    IdxT* dst = out + row * out_stride;
+    const int tid = threadIdx.x;
+    const int64_t nwords = (tokens + 31) / 32;
+    __shared__ uint32_t scan_sh[kSelWaves + 1];
+    uint32_t w[WPT], cnt = 0;
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+        const int64_t e = static_cast<int64_t>(tid) * WPT + i;
+        w[i] = e < nwords ? mrow[e] : 0u;
+        cnt += __popc(w[i]);
+    }
+    uint32_t total;
+    uint32_t pos = block_excl_scan(cnt, scan_sh, kSelWaves, &total);
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+        const int64_t tbase = (static_cast<int64_t>(tid) * WPT + i) * 32;
+        for (uint32_t m = w[i]; m; m &= m - 1) {
+            if (pos < static_cast<uint64_t>(k)) dst[pos] = static_cast<IdxT>(tbase + __builtin_ctz(m));
+            ++pos;
+        }
+    }
+    if (tid == 0) dst[k] = static_cast<IdxT>(current);
 }
 
 template <int SEG, typename IdxT>
@@ -366,15 +407,38 @@ hipError_t launch_select_t(const uint16_t* scores, int64_t rows, int64_t row_str
 
 }  // namespace
 
-hipError_t launch_topk_select_keys(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride,
-                                   int64_t tokens, int64_t k, int64_t current, void* indices, int index_dtype,
-                                   int64_t index_row_stride, hipStream_t stream) {
+hipError_t launch_topk_mask(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
+                            int64_t k, uint32_t* mask, int64_t mask_stride, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    if (index_dtype == POPKV_INDEX_I32)
-        return launch_keys_t(keys, ghist, rows, row_stride, tokens, k, current, static_cast<int32_t*>(indices),
-                             index_row_stride, stream);
-    return launch_keys_t(keys, ghist, rows, row_stride, tokens, k, current, static_cast<int64_t*>(indices),
-                         index_row_stride, stream);
+    const int64_t rounds = (tokens + kSelThreads - 1) / kSelThreads;
+    const int nt = static_cast<int>(tokens), kk = static_cast<int>(k < tokens ? k : tokens);
+    dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
+#define POPKV_MASK(JB, MULTI)                                                                                   \
+    hipLaunchKernelGGL((topk_mask_kernel<JB, MULTI>), grid, block, 0, stream, keys, ghist, row_stride, nt, kk, \
+                       mask, mask_stride)
+    if (rounds <= 8) POPKV_MASK(8, false);
+    else if (rounds <= 16) POPKV_MASK(16, false);
+    else if (rounds <= 32) POPKV_MASK(32, false);
+    else POPKV_MASK(32, true);
+#undef POPKV_MASK
+    return hipGetLastError();
+}
+
+hipError_t launch_mask_to_indices(const uint32_t* mask, int64_t rows, int64_t mask_stride, int64_t tokens, int64_t k,
+                                  int64_t current, int64_t* indices, int64_t index_row_stride, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t words = (tokens + 31) / 32;
+    dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
+    if (words <= kSelThreads)
+        hipLaunchKernelGGL((mask_to_indices_kernel<1, int64_t>), grid, block, 0, stream, mask, mask_stride, tokens, k,
+                           current, indices, index_row_stride);
+    else if (words <= 2 * kSelThreads)
+        hipLaunchKernelGGL((mask_to_indices_kernel<2, int64_t>), grid, block, 0, stream, mask, mask_stride, tokens, k,
+                           current, indices, index_row_stride);
+    else
+        hipLaunchKernelGGL((mask_to_indices_kernel<4, int64_t>), grid, block, 0, stream, mask, mask_stride, tokens, k,
+                           current, indices, index_row_stride);
+    return hipGetLastError();
 }
 
 hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,

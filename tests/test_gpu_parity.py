@@ -348,6 +348,59 @@ def test_retrieval_step_and_layer_step_match_oracle(method):
     assert torch.equal(o3, o2)
 
 
+def _check_layer_step(w, layer, mapping, cache):
+    sc, idx, out = _oracle_step(w, layer, mapping, cache)
+    o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(got.cpu().numpy(), idx)
+    np.testing.assert_allclose(f32(o), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+    o2 = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                layer.current_v(), mapping, budget=w.budget)
+    assert torch.equal(o2, o)
+
+
+@pytest.mark.parametrize("distinct", [1, 3, 16])
+def test_layer_step_heavy_ties(distinct):
+    """Every prefix key is a copy of one of `distinct` rows, so each head's
+    scores take at most `distinct` values and the k-th key is shared by many
+    tokens: only the lowest-index ties may be taken."""
+    w = workloads.scaled(workloads.C1, context=5000, budget=700)
+    layer = workloads.make_layer(w, seed=5)
+    g = torch.Generator().manual_seed(9)
+    pick = torch.randint(0, distinct, (w.context,), generator=g)
+    layer.keys[:, :] = layer.keys[:, :distinct][:, pick]
+    layer = layer.to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    cache = popkv.build_popkv_cache(layer.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                    reserve_tokens=64)
+    _check_layer_step(w, layer, mapping, cache)
+
+
+@pytest.mark.parametrize("context,budget", [(300, 512), (1025, 1025), (64, 2), (2, 2)])
+def test_layer_step_budget_covers_or_exceeds_context(context, budget):
+    w = workloads.scaled(workloads.C1, context=context, budget=budget)
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_layer_step_dtypes(dtype):
+    base = workloads.scaled(workloads.C1, context=4500, budget=600)
+    w = workloads.Workload(base.name, base.method, base.q_heads, base.kv_heads, 128, base.context, base.budget,
+                           base.token_group, base.dim_group, dtype, 3, True)
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
+@pytest.mark.parametrize("context", [65536, 131072])
+def test_layer_step_long_context(context):
+    """C3's long contexts: more than 32 key rounds per select thread (keys
+    re-read per pass) and 4096-token attention chunks."""
+    w = workloads.scaled(workloads.c3(context), context=context)
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
 def test_retrieval_step_with_torch_topk_hook():
     w = workloads.scaled(workloads.C1, context=3000, budget=512)
     layer, mapping, cache = _layer_setup(w)
