@@ -208,30 +208,33 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
 // the first radix level costs nothing here.  Thread t of the block handles
 // tokens t, t + 1024, t + 2048, ...: round j of a wave covers 64 consecutive
 // tokens, so one ballot of a comparison is directly that 64-token word of the
-// selection mask, and lane j of the wave collects round j's word for one
+// selection mask, and lane j of the wave collects round j's words for one
 // store at the end.
 //   1. bin b1 of the k-th largest key from ghist;
 //   2. 256-bin histogram of the low byte of the keys with high byte b1 ->
 //      the k-th largest key T, need_eq = how many keys equal to T are taken;
-//   3. if some keys equal to T are left out, the last one taken is the
+//   3. one pass builds, per 64-token word, the bits of keys > T and of keys
+//      == T.  If some keys equal to T are left out, the last one taken is the
 //      need_eq-th in token order (PyTorch's gather-top-k tie rule: the lowest
-//      indices win): per-(round, wave) tie counts and masks, one block scan,
-//      and the owner of the crossing group finds the token tau;
-//   4. mask bit of token t: key > T, or key == T and t <= tau.
+//      indices win): the tie words go to LDS, one block scan of their
+//      popcounts finds the word holding it and that word's owner finds the
+//      token tau;
+//   4. mask word = (key > T bits) | (key == T bits of tokens <= tau).
 // Absent tokens (past `tokens`) get key 0, below every real key (real keys
-// are >= 0x03ff; NaN patterns map to 0xffff).  JB rounds of keys are held in
-// registers; with MULTI (more than JB rounds) every pass re-reads its keys in
-// batches of JB rounds.  The mask row holds ceil(tokens/64) 64-bit words,
-// bits past `tokens` zero.  ghist is re-zeroed for the next call.
-constexpr int kMaskMaxRounds = 128;                         // tokens <= 131072
-constexpr int kMaskTieSlots = kMaskMaxRounds * kSelWaves;  // per-(round, wave) tie counts
+// are >= 0x03ff; NaN patterns map to 0xffff).  Rows of up to JB rounds keep
+// their keys and words in registers (tokens <= 32768 for JB = 32); longer
+// rows take the MULTI path, which re-reads keys per pass and keeps the words
+// in LDS.  The mask row holds ceil(tokens/64) 64-bit words, bits past
+// `tokens` zero.  ghist is re-zeroed for the next call.
+constexpr int kMaskMaxRounds = 128;                          // tokens <= 131072
+constexpr int kMaskWordSlots = kMaskMaxRounds * kSelWaves;  // 64-bit words per row
 
 template <int JB, bool MULTI>
 __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
     const uint16_t* __restrict__ keys, uint32_t* __restrict__ ghist, int64_t row_stride, int ntok, int k,
     uint32_t* __restrict__ mask, int64_t mask_stride) {
     static_assert(JB <= kWave, "one collecting lane per round");
-    constexpr int SLOTS = MULTI ? kMaskTieSlots : JB * kSelWaves;
+    constexpr int SLOTS = MULTI ? kMaskWordSlots : JB * kSelWaves;
     const int64_t row = blockIdx.x;
     const uint16_t* src = keys + row * row_stride;
     uint32_t* gh = ghist + row * kBins;
@@ -244,8 +247,8 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
     __shared__ uint32_t tot[kBins], hist2[kBins];
     __shared__ uint32_t scan_sh[kSelWaves + 1];
     __shared__ uint32_t s_bin, s_above, s_tau;
-    __shared__ uint32_t s_tie[SLOTS];
     __shared__ uint64_t s_eq[SLOTS];
+    __shared__ uint64_t s_gt[MULTI ? SLOTS : 1];
     if (tid < kBins) {
         tot[tid] = gh[tid];
         gh[tid] = 0u;
@@ -253,8 +256,20 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
     }
     // mode 0: nothing selected (k == 0); 1: every token (k >= ntok); 2: threshold
     const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);
-    uint32_t thr = 0xffffffffu;
-    int tau = ntok;
+    if (mode != 2) {
+        for (int j0 = 0; j0 < rounds; j0 += JB) {
+            uint32_t wl = 0, wh = 0;
+#pragma unroll
+            for (int jj = 0; jj < JB; ++jj) {
+                const uint64_t word = mode == 1 ? __ballot((j0 + jj) * kSelThreads + tid < ntok) : 0ull;
+                wl = lane == jj ? static_cast<uint32_t>(word) : wl;
+                wh = lane == jj ? static_cast<uint32_t>(word >> 32) : wh;
+            }
+            const int wbase = (j0 + lane) * kSelThreads + wave * kWave;
+            if (lane < JB && wbase < ntok) *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(wl, wh);
+        }
+        return;
+    }
     uint32_t kr[JB];
     auto load = [&](int j0) {
 #pragma unroll
@@ -264,87 +279,102 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
             kr[jj] = t < ntok ? v : 0u;
         }
     };
-    if (mode == 2) {
-        if (!MULTI) load(0);
-        __syncthreads();
-        find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
-        __syncthreads();
-        const uint32_t b1 = s_bin;
-        const uint32_t above1 = s_above;
-        for (int j0 = 0; j0 < rounds; j0 += JB) {
-            if (MULTI) load(j0);
-#pragma unroll
-            for (int jj = 0; jj < JB; ++jj)
-                if ((kr[jj] >> 8) == b1) atomicAdd(&hist2[kr[jj] & 0xffu], 1u);
-            if (!MULTI) break;
-        }
-        __syncthreads();
-        find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
-        __syncthreads();
-        thr = (b1 << 8) | s_bin;
-        const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
-        if (need_eq < hist2[s_bin]) {  // some ties left out: find tau (block-uniform branch)
-            for (int j0 = 0; j0 < rounds; j0 += JB) {
-                if (MULTI) load(j0);
-                uint32_t tc = 0, tl = 0, th = 0;
-#pragma unroll
-                for (int jj = 0; jj < JB; ++jj) {
-                    const uint64_t eq = __ballot(kr[jj] == thr);
-                    tc = lane == jj ? static_cast<uint32_t>(__popcll(eq)) : tc;
-                    tl = lane == jj ? static_cast<uint32_t>(eq) : tl;
-                    th = lane == jj ? static_cast<uint32_t>(eq >> 32) : th;
-                }
-                if (lane < JB && j0 + lane < rounds) {
-                    const int e = (j0 + lane) * kSelWaves + wave;
-                    s_tie[e] = tc;
-                    s_eq[e] = (static_cast<uint64_t>(th) << 32) | tl;
-                }
-                if (!MULTI) break;
-            }
-            __syncthreads();
-            constexpr int PER = (SLOTS + kSelThreads - 1) / kSelThreads;
-            const int n_slots = rounds * kSelWaves;
-            uint32_t c[PER], local = 0;
-#pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const int e = tid * PER + i;
-                c[i] = e < n_slots ? s_tie[e] : 0u;
-                local += c[i];
-            }
-            uint32_t total;
-            uint32_t run = block_excl_scan(local, scan_sh, kSelWaves, &total);
-#pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const int e = tid * PER + i;
-                if (run < need_eq && run + c[i] >= need_eq) {
-                    // the (need_eq - run)-th set bit of this group's tie mask
-                    uint64_t m = s_eq[e];
-                    for (uint32_t n = need_eq - run; n > 1; --n) m &= m - 1;
-                    s_tau = static_cast<uint32_t>((e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave +
-                                                  __builtin_ctzll(m));
-                }
-                run += c[i];
-            }
-            __syncthreads();
-            tau = static_cast<int>(s_tau);
-        }
-    }
-    // mask words
+    if (!MULTI) load(0);
+    __syncthreads();
+    find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
+    __syncthreads();
+    const uint32_t b1 = s_bin;
+    const uint32_t above1 = s_above;
     for (int j0 = 0; j0 < rounds; j0 += JB) {
-        if (MULTI && mode == 2) load(j0);
-        uint32_t wl = 0, wh = 0;
+        if (MULTI) load(j0);
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj)
+            if ((kr[jj] >> 8) == b1) atomicAdd(&hist2[kr[jj] & 0xffu], 1u);
+        if (!MULTI) break;
+    }
+    __syncthreads();
+    find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
+    __syncthreads();
+    const uint32_t thr = (b1 << 8) | s_bin;
+    const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
+    const bool partial = need_eq < hist2[s_bin];  // block-uniform
+
+    // 3. per-word bits of key > T and key == T; lane jj of each wave holds
+    //    round j0 + jj's words
+    uint32_t gl = 0, gh_ = 0, el = 0, eh = 0;
+    for (int j0 = 0; j0 < rounds; j0 += JB) {
+        if (MULTI) load(j0);
 #pragma unroll
         for (int jj = 0; jj < JB; ++jj) {
-            const int t = (j0 + jj) * kSelThreads + tid;
-            uint64_t word;
-            if (mode == 2) word = __ballot(kr[jj] > thr || (kr[jj] == thr && t <= tau));
-            else word = mode == 1 ? __ballot(t < ntok) : 0ull;
-            wl = lane == jj ? static_cast<uint32_t>(word) : wl;
-            wh = lane == jj ? static_cast<uint32_t>(word >> 32) : wh;
+            const uint64_t gt = __ballot(kr[jj] > thr);
+            const uint64_t eq = __ballot(kr[jj] == thr);
+            const bool mine = lane == jj;
+            gl = mine ? static_cast<uint32_t>(gt) : gl;
+            gh_ = mine ? static_cast<uint32_t>(gt >> 32) : gh_;
+            el = mine ? static_cast<uint32_t>(eq) : el;
+            eh = mine ? static_cast<uint32_t>(eq >> 32) : eh;
         }
-        const int wbase = (j0 + lane) * kSelThreads + wave * kWave;
-        if (lane < JB && wbase < ntok) *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(wl, wh);
+        if (lane < JB && j0 + lane < rounds) {
+            const int e = (j0 + lane) * kSelWaves + wave;  // word index in token order
+            if (MULTI || partial) s_eq[e] = (static_cast<uint64_t>(eh) << 32) | el;
+            if (MULTI) s_gt[e] = (static_cast<uint64_t>(gh_) << 32) | gl;
+        }
         if (!MULTI) break;
+    }
+    int tau = ntok;
+    if (partial) {
+        __syncthreads();
+        constexpr int PER = (SLOTS + kSelThreads - 1) / kSelThreads;
+        const int n_slots = rounds * kSelWaves;
+        uint32_t c[PER], local = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = tid * PER + i;
+            c[i] = e < n_slots ? static_cast<uint32_t>(__popcll(s_eq[e])) : 0u;
+            local += c[i];
+        }
+        uint32_t total;
+        uint32_t run = block_excl_scan(local, scan_sh, kSelWaves, &total);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = tid * PER + i;
+            if (run < need_eq && run + c[i] >= need_eq) {
+                // the (need_eq - run)-th set bit of this word's tie bits
+                uint64_t m = s_eq[e];
+                for (uint32_t n = need_eq - run; n > 1; --n) m &= m - 1;
+                s_tau = static_cast<uint32_t>((e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave +
+                                              __builtin_ctzll(m));
+            }
+            run += c[i];
+        }
+        __syncthreads();
+        tau = static_cast<int>(s_tau);
+    }
+    // 4. final words: ties only up to tau
+    auto finish = [&](uint64_t gt, uint64_t eq, int wbase) {
+        if (eq != 0ull && tau < wbase + kWave) {
+            const int keep = tau - wbase + 1;  // tie bits [0, keep) stay
+            eq = keep <= 0 ? 0ull : (eq & ((keep >= kWave) ? ~0ull : ((1ull << keep) - 1ull)));
+        }
+        return gt | eq;
+    };
+    if (!MULTI) {
+        const int wbase = lane * kSelThreads + wave * kWave;
+        if (lane < JB && wbase < ntok) {
+            const uint64_t w = finish((static_cast<uint64_t>(gh_) << 32) | gl, (static_cast<uint64_t>(eh) << 32) | el,
+                                      wbase);
+            *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(static_cast<uint32_t>(w),
+                                                                      static_cast<uint32_t>(w >> 32));
+        }
+    } else {
+        __syncthreads();
+        for (int e = tid; e < rounds * kSelWaves; e += kSelThreads) {
+            const int wbase = (e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave;
+            if (wbase >= ntok) continue;
+            const uint64_t w = finish(s_gt[e], s_eq[e], wbase);
+            *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(static_cast<uint32_t>(w),
+                                                                      static_cast<uint32_t>(w >> 32));
+        }
     }
 }
 
