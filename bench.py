@@ -2,20 +2,22 @@
 """Benchmark of the PopKV decode-time retrieval step on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py --copy-calibration     # plain 256 MiB copies (PMC scale)
 
 A "step" is one sparse layer's retrieval step at configuration C1 (PopKV-S,
 Llama-3.1-8B shapes: 32 query heads / 8 KV heads, head_dim 128, 32K context,
 budget 4096, bf16 K/V): query encode + popcount score over 32767 cached
 tokens + per-head top-4095 + current token + 256-token split sparse
-attention with the log-sum-exp merge -- one ``popkv_layer_step`` C-ABI call,
-replayed from a HIP graph.  Inputs are resident in HBM; eight independent
-K/V + metadata sets (about 1.1 GB) rotate so the 256 MB MALL cannot hold the
-working set.
+attention with the log-sum-exp merge -- one ``popkv_layer_step`` C-ABI call
+(four kernels), replayed from a HIP graph.  Inputs are resident in HBM; eight
+independent K/V + metadata sets (about 1.1 GB) rotate so the 256 MB MALL
+cannot hold the working set.
 
 Prints ONE JSON line: µs per layer step (lower is better), the achieved
-algorithmic HBM GB/s of the step, per-stage kernel times, the roofline of the
-dominant kernel (sparse attention) and a CPU baseline (the C oracle, one
-thread, on a bounded sample of the same workload).
+algorithmic HBM GB/s of the step, per-stage kernel times of the layer step
+(HIP events recorded between its kernels), the roofline of the dominant
+kernel (the layer step's sparse attention) and a CPU baseline (the C oracle,
+one thread, on a bounded sample of the same workload).
 """
 from __future__ import annotations
 
@@ -32,6 +34,13 @@ sys.path.insert(0, str(ROOT))
 METRIC = "µs/layer score+top-k+sparse-attn @32K ctx, B=4096; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 N_BUFFERS = 8
+# HBM bytes per launch of the layer step's attention kernel at C1, from
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script (KiB per
+# dispatch), each scaled by the same counter on a plain 256 MiB copy
+# (bench.py --copy-calibration): FETCH_SIZE reads 131084.5 KiB for the copy's
+# 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).  Attention:
+# FETCH_SIZE 28020.6 KiB, WRITE_SIZE 272.0 KiB per dispatch.
+ATTN_TRAFFIC_BYTES = round(28020.6 * 1024 * (262144 / 131084.5) + 272.0 * 1024)
 
 
 def parse_args():
@@ -42,7 +51,25 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     p.add_argument("--no-graph", action="store_true", help="time eager launches only")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run plain 256 MiB device copies (scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
+
+
+def copy_calibration(steps: int) -> int:
+    """torch's device-to-device copy of a 256 MiB buffer, `steps` times: a
+    kernel of known HBM traffic (256 MiB read + 256 MiB written per dispatch)
+    that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scale against."""
+    import torch
+
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "dispatches": steps}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -51,6 +78,9 @@ def main() -> int:
         print("bench.py measures one GPU: the PopKV retrieval path is built and timed on a single "
               "MI355X (multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
         return 2
+
+    if args.copy_calibration:
+        return copy_calibration(args.steps)
 
     import torch
 
@@ -134,7 +164,21 @@ def main() -> int:
             return 1
     ms_per_step = graph_ms if graph_ms is not None else eager_ms
 
-    # ---- per-stage kernels (same inputs, stand-alone entry points)
+    # ---- the dominant kernel alone: the layer step's sparse attention,
+    #      re-run on the selection the last step left in the workspace
+    #      (popkv_layer_step_attention), timed with HIP events around
+    #      back-to-back launches on the step's stream
+    def attention_only(i: int) -> None:
+        pk, pv, _ = sets[i % N_BUFFERS]
+        popkv.popkv_layer_step_attention(q, pk, pv, mapping, budget=w.budget, workspace=ws)
+
+    for i in range(args.warmup):
+        attention_only(i)
+    attn_step_ms = timed(attention_only, args.steps)
+
+    # ---- reference-API stages (the entry points popkv_cuda / topk /
+    #      sparse_kernels expose, same inputs), for comparison with the
+    #      reference's per-stage numbers
     stage_timer = timed if args.no_graph else graph_timed
     enc = popkv_cuda.query_encode(q.unsqueeze(0).contiguous(), dim_group_size=w.dim_group)
     score_ms = stage_timer(lambda i: popkv_cuda.score_encoded(enc, sets[i % N_BUFFERS][2].packed, head_to_kv=mapping,
@@ -151,7 +195,7 @@ def main() -> int:
     unique_rows = int(sum(torch.unique(indices[h * 4:(h + 1) * 4].flatten()).numel() for h in range(w.kv_heads)))
 
     step_gbps = alg["step"] / (ms_per_step * 1e-3) / 1e9
-    attn_gbps = alg["attention"] / (attn_ms * 1e-3) / 1e9
+    attn_gbps = alg["attention"] / (attn_step_ms * 1e-3) / 1e9
     result = {
         "metric": METRIC,
         "value": round(ms_per_step * 1e3, 3),
@@ -173,16 +217,14 @@ def main() -> int:
         "step_algorithmic_bytes": alg["step"],
         "eager_us_per_layer": round(eager_ms * 1e3, 3),
         "graph_us_per_layer": None if graph_ms is None else round(graph_ms * 1e3, 3),
-        "stages_us": {"encode": round(encode_ms * 1e3, 3), "score": round(score_ms * 1e3, 3),
-                      "select": round(select_ms * 1e3, 3), "attention_partial": round(attn_ms * 1e3, 3)},
-        "stages_GBps": {"score": round(alg["score"] / (score_ms * 1e-3) / 1e9, 1),
-                        "select": round(alg["select"] / (select_ms * 1e-3) / 1e9, 1),
-                        "attention_partial": round(attn_gbps, 1)},
+        "api_stages_us": {"query_encode": round(encode_ms * 1e3, 3), "score_encoded": round(score_ms * 1e3, 3),
+                          "select_with_current": round(select_ms * 1e3, 3),
+                          "indexed_attention_split_partial": round(attn_ms * 1e3, 3)},
         "unique_kv_rows_per_step": unique_rows,
-        "roofline": {"bound": "hbm", "kernel": "attn_partial_kernel", "achieved": round(attn_gbps, 1),
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": alg["attention"],
-                     "avg_launch_us": round(attn_ms * 1e3, 3)},
+        "roofline": {"bound": "hbm", "kernel": "attn_rank_kernel (layer step attention)",
+                     "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
+                     "algorithmic_bytes_per_launch": alg["attention"], "avg_launch_us": round(attn_step_ms * 1e3, 3)},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -170,6 +170,18 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* output, int64_t* indices_out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Re-runs only the sparse-attention kernel of the last popkv_layer_step that
+ * used `workspace` (same shapes and budget): it reads the selection masks the
+ * step left there and rewrites the split partials, touching nothing else, so
+ * it can be repeated.  For timing the step's dominant kernel on its own; no
+ * counterpart in the reference. */
+int popkv_layer_step_attention(const void* queries, int32_t dtype,
+                               const void* prefix_k, const void* prefix_v,
+                               int64_t k_head_stride, int64_t v_head_stride,
+                               const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
+                               int64_t tokens, int64_t budget,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -336,10 +336,36 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads), partials, s),
                   "popkv_layer_step(attention)");
     if (st) return st;
-    return launched(popkv::launch_merge_current(partials, static_cast<int>(L.nsplit), queries, dtype, current_k,
+    st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nsplit), queries, dtype, current_k,
                                                 current_v, head_to_kv, static_cast<int>(q_heads),
                                                 static_cast<int>(kv_heads), output, s),
-                    "popkv_layer_step(merge)");
+                  "popkv_layer_step(merge)");
+    if (st) return st;
+    return POPKV_OK;
+}
+
+int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
+                               int64_t k_head_stride, int64_t v_head_stride, const int64_t* head_to_kv,
+                               int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    if (!queries || !prefix_k || !prefix_v || !head_to_kv || !workspace) return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "tensors must be fp32/fp16/bf16");
+    if (budget <= 1) return fail(POPKV_ERR_INVALID, "budget must reserve at least one retrieved and one current token");
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads > 65535) return fail(POPKV_ERR_INVALID, "empty or too many heads");
+    if (tokens <= 0 || tokens > kMaxSelectTokens) return fail(POPKV_ERR_TOKENS, "invalid score token count");
+    const StepLayout L = step_layout(q_heads, tokens, budget);
+    if (workspace_bytes < L.total) return fail(POPKV_ERR_WORKSPACE, "layer step needs %zu workspace bytes", L.total);
+    const size_t es = elem_size(dtype);
+    if (!aligned16(workspace) || !aligned16(queries) || !aligned16(prefix_k) || !aligned16(prefix_v) ||
+        (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
+        return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
+    char* ws = static_cast<char*>(workspace);
+    return launched(popkv::launch_attention_ranks(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride,
+                                                  reinterpret_cast<const uint32_t*>(ws + L.mask), L.mask_stride,
+                                                  tokens, L.k, static_cast<int>(L.nsplit), head_to_kv,
+                                                  static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                                                  reinterpret_cast<float*>(ws + L.partials), as_stream(stream)),
+                    "popkv_layer_step_attention");
 }
 
 }  // extern "C"

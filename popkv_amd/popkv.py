@@ -13,6 +13,7 @@ encode + score, top-k, split attention, log-sum-exp merge).
 """
 from __future__ import annotations
 
+
 import math
 from dataclasses import dataclass
 from typing import Callable, Sequence
@@ -320,3 +321,22 @@ def popkv_layer_step(
                  kv_heads, tokens, int(budget), cache.dim_group_size, output.data_ptr(), nat.ptr(idx),
                  ws.data_ptr(), ws.numel(), nat.stream_of(dev))
     return (output, idx) if return_indices else output
+
+
+def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor,
+                               head_to_kv: torch.Tensor, *, budget: int,
+                               workspace: LayerStepWorkspace | torch.Tensor) -> None:
+    """Re-run only the sparse-attention kernel of the last ``popkv_layer_step``
+    that used ``workspace`` (same shapes and budget); rewrites the split
+    partials inside the workspace.  A timing aid for the step's dominant
+    kernel."""
+    dev = q.device
+    ws = workspace if isinstance(workspace, torch.Tensor) else workspace.buffer
+    if ws is None:
+        raise ValueError("the workspace has not been used by popkv_layer_step")
+    q_heads, kv_heads, tokens = int(q.shape[0]), int(prefix_k.shape[0]), int(prefix_k.shape[1])
+    mapping = head_to_kv.to(device=dev, dtype=torch.int64).contiguous()
+    with torch.cuda.device(dev):
+        nat.call("popkv_layer_step_attention", q.data_ptr(), nat.dtype_code(q), prefix_k.data_ptr(),
+                 prefix_v.data_ptr(), prefix_k.stride(0), prefix_v.stride(0), mapping.data_ptr(), q_heads, kv_heads,
+                 tokens, int(budget), ws.data_ptr(), ws.numel(), nat.stream_of(dev))
