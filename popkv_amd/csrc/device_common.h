@@ -131,21 +131,12 @@ __device__ __forceinline__ uint32_t order_key(uint32_t h) {
 
 // ---- wave / block reductions --------------------------------------------
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
-}
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
-}
+// Wave-wide max / min / sum, the result in every lane.  max and min are
+// exact in any order; the sum is a fixed tree (DPP within rows, then the four
+// row totals), so it is deterministic but not a left-to-right fold.
+__device__ __forceinline__ float wave_max(float v);
+__device__ __forceinline__ float wave_min(float v);
+__device__ __forceinline__ float wave_sum(float v);
 
 // Sum over each row of 16 lanes (or 8-lane half rows for N = 8) with DPP
 // lane permutations -- VALU-only, no LDS traffic.  Every lane of a row ends
@@ -185,13 +176,36 @@ __device__ __forceinline__ float wave_extreme(float v) {
     return f(f(r0, r1), f(r2, r3));
 }
 
-// Inclusive prefix sum across the wave.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        uint32_t o = __shfl_up(v, off);
-        if (lane >= off) v += o;
-    }
+__device__ __forceinline__ float wave_max(float v) { return wave_extreme<true>(v); }
+__device__ __forceinline__ float wave_min(float v) { return wave_extreme<false>(v); }
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Inclusive prefix sum across the wave with DPP (VALU only): row_shr 1, 2,
+// 4, 8 scan each 16-lane row (lanes without a source add 0), then
+// row_bcast:15 adds lane 15's total to rows 1 and 3 and row_bcast:31 adds
+// lane 31's total to rows 2 and 3.  All 64 lanes must be active.
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, BOUND_ZERO));
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int /*lane*/) {
+    v += dpp_u32<0x111, 0xf, true>(v);
+    v += dpp_u32<0x112, 0xf, true>(v);
+    v += dpp_u32<0x114, 0xf, true>(v);
+    v += dpp_u32<0x118, 0xf, true>(v);
+    v += dpp_u32<0x142, 0xa, false>(v);
+    v += dpp_u32<0x143, 0xc, false>(v);
     return v;
 }
 

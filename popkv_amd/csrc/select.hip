@@ -34,28 +34,25 @@ constexpr int kSelWaves = kSelThreads / kWave;
 constexpr int kBins = 256;  // one byte of the key per level
 
 // Finds the bin holding the `need`-th largest element of histogram `hist`
-// (NB bins, 1 <= need <= total) with the whole block: each thread sums a
-// contiguous run of bins from the top, one block scan, then the owning
-// thread scans its run.  Writes the bin and the count strictly above it.
+// (NB bins, 1 <= need <= total) with one wave: lane l sums the NB/64 bins of
+// ranks [l*PER, l*PER + PER) counted from the top, one DPP wave scan, and the
+// lane holding the crossing rank writes the bin and the count strictly above
+// it.  Called by the whole first wave of the block (no barrier inside).
 template <int NB>
-__device__ __forceinline__ void find_bin(const uint32_t* hist, uint32_t need, uint32_t* scan_sh,
-                                         uint32_t* s_bin, uint32_t* s_above) {
-    constexpr int PER = (NB + kSelThreads - 1) / kSelThreads;
-    const int t = threadIdx.x;
-    uint32_t c[PER];
-    uint32_t local = 0;
+__device__ __forceinline__ void find_bin(const uint32_t* hist, uint32_t need, uint32_t* s_bin, uint32_t* s_above) {
+    constexpr int PER = NB / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    uint32_t c[PER], local = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int r = t * PER + i;  // rank from the top
-        c[i] = r < NB ? hist[NB - 1 - r] : 0u;
+        c[i] = hist[NB - 1 - (lane * PER + i)];
         local += c[i];
     }
-    uint32_t total;
-    uint32_t running = block_excl_scan(local, scan_sh, kSelWaves, &total);
+    uint32_t running = wave_incl_scan(local, lane) - local;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         if (running < need && running + c[i] >= need) {
-            *s_bin = static_cast<uint32_t>(NB - 1 - (t * PER + i));
+            *s_bin = static_cast<uint32_t>(NB - 1 - (lane * PER + i));
             *s_above = running;
         }
         running += c[i];
@@ -136,7 +133,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
     __syncthreads();
     reduce_hist();
     __syncthreads();
-    find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
+    if (tid < kWave) find_bin<kBins>(tot, static_cast<uint32_t>(k), &s_bin, &s_above);
     __syncthreads();
     const uint32_t b1 = s_bin;
     const uint32_t above1 = s_above;
@@ -152,7 +149,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
     __syncthreads();
     reduce_hist();
     __syncthreads();
-    find_bin<kBins>(tot, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
+    if (tid < kWave) find_bin<kBins>(tot, static_cast<uint32_t>(k) - above1, &s_bin, &s_above);
     __syncthreads();
     const uint32_t thr = (b1 << 8) | s_bin;
     const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
@@ -216,9 +213,9 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
 //   3. one pass builds, per 64-token word, the bits of keys > T and of keys
 //      == T.  If some keys equal to T are left out, the last one taken is the
 //      need_eq-th in token order (PyTorch's gather-top-k tie rule: the lowest
-//      indices win): the tie words go to LDS, one block scan of their
-//      popcounts finds the word holding it and that word's owner finds the
-//      token tau;
+//      indices win): the tie words go to LDS, one wave scans their
+//      popcounts, finds the word holding that tie and, one lane per bit,
+//      the token tau;
 //   4. mask word = (key > T bits) | (key == T bits of tokens <= tau).
 // Absent tokens (past `tokens`) get key 0, below every real key (real keys
 // are >= 0x03ff; NaN patterns map to 0xffff).  Rows of up to JB rounds keep
@@ -245,7 +242,6 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
     const int rounds = (ntok + kSelThreads - 1) / kSelThreads;
 
     __shared__ uint32_t tot[kBins], hist2[kBins];
-    __shared__ uint32_t scan_sh[kSelWaves + 1];
     __shared__ uint32_t s_bin, s_above, s_tau;
     __shared__ uint64_t s_eq[SLOTS];
     __shared__ uint64_t s_gt[MULTI ? SLOTS : 1];
@@ -281,7 +277,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
     };
     if (!MULTI) load(0);
     __syncthreads();
-    find_bin<kBins>(tot, static_cast<uint32_t>(k), scan_sh, &s_bin, &s_above);
+    if (tid < kWave) find_bin<kBins>(tot, static_cast<uint32_t>(k), &s_bin, &s_above);
     __syncthreads();
     const uint32_t b1 = s_bin;
     const uint32_t above1 = s_above;
@@ -293,7 +289,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
         if (!MULTI) break;
     }
     __syncthreads();
-    find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, scan_sh, &s_bin, &s_above);
+    if (tid < kWave) find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, &s_bin, &s_above);
     __syncthreads();
     const uint32_t thr = (b1 << 8) | s_bin;
     const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
@@ -323,29 +319,39 @@ __global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
     }
     int tau = ntok;
     if (partial) {
+        // the word holding the need_eq-th tie (token order = word order):
+        // wave 0, lane l owns words [l*PERW, l*PERW + PERW), one DPP scan
         __syncthreads();
-        constexpr int PER = (SLOTS + kSelThreads - 1) / kSelThreads;
-        const int n_slots = rounds * kSelWaves;
-        uint32_t c[PER], local = 0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int e = tid * PER + i;
-            c[i] = e < n_slots ? static_cast<uint32_t>(__popcll(s_eq[e])) : 0u;
-            local += c[i];
-        }
-        uint32_t total;
-        uint32_t run = block_excl_scan(local, scan_sh, kSelWaves, &total);
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int e = tid * PER + i;
-            if (run < need_eq && run + c[i] >= need_eq) {
-                // the (need_eq - run)-th set bit of this word's tie bits
-                uint64_t m = s_eq[e];
-                for (uint32_t n = need_eq - run; n > 1; --n) m &= m - 1;
-                s_tau = static_cast<uint32_t>((e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave +
-                                              __builtin_ctzll(m));
+        if (tid < kWave) {
+            constexpr int PERW = SLOTS / kWave;
+            const int n_slots = rounds * kSelWaves;
+            uint32_t local = 0;
+            for (int i = 0; i < PERW; ++i) {
+                const int e = lane * PERW + i;
+                local += e < n_slots ? static_cast<uint32_t>(__popcll(s_eq[e])) : 0u;
             }
-            run += c[i];
+            const uint32_t excl = wave_incl_scan(local, lane) - local;
+            // the crossing lane, then (uniformly) its crossing word
+            const uint64_t cross = __ballot(excl < need_eq && excl + local >= need_eq);
+            const int owner = static_cast<int>(__builtin_ctzll(cross));
+            uint32_t run = __builtin_amdgcn_readlane(excl, owner);
+            int e = owner * PERW;
+            uint64_t m = s_eq[e];
+            for (int i = 0; i < PERW; ++i) {
+                m = s_eq[owner * PERW + i];
+                const uint32_t c = static_cast<uint32_t>(__popcll(m));
+                e = owner * PERW + i;
+                if (run + c >= need_eq) break;
+                run += c;
+            }
+            // the (need_eq - run)-th set bit of m: lane b holds bit b and its
+            // rank among the set bits below it
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+            const uint64_t hit = __ballot(((m >> lane) & 1ull) && below == need_eq - run - 1);
+            if (lane == 0)
+                s_tau = static_cast<uint32_t>((e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave +
+                                              __builtin_ctzll(hit));
         }
         __syncthreads();
         tau = static_cast<int>(s_tau);
