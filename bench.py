@@ -176,6 +176,21 @@ def main() -> int:
         attention_only(i)
     attn_step_ms = timed(attention_only, args.steps)
 
+    # ---- prepack of the 32K prefix and the per-token append (re-encode of
+    #      the active token group incl. the new token), pack_keys_into into a
+    #      scratch copy of the packed cache, replayed from a HIP graph
+    prefix0 = sets[0][0].contiguous()
+    scratch = tuple(t.clone() for t in sets[0][2].packed)
+    sealed = (L // w.token_group) * w.token_group
+    active = layer.keys[:, sealed:L + 1].to(dev).contiguous()
+    prepack_ms = graph_timed(lambda i: popkv_cuda.pack_keys_into(
+        prefix0, scratch, token_offset=0, token_group_size=w.token_group, dim_group_size=w.dim_group), 4)
+    append_ms = graph_timed(lambda i: popkv_cuda.pack_keys_into(
+        active, scratch, token_offset=sealed, token_group_size=w.token_group, dim_group_size=w.dim_group), reps)
+    meta_row = 32 + 4 * (w.head_dim // w.dim_group)
+    prepack_bytes = w.kv_heads * L * (w.head_dim * 2 + meta_row)
+    append_bytes = w.kv_heads * int(active.shape[1]) * (w.head_dim * 2 + meta_row)
+
     # ---- reference-API stages (the entry points popkv_cuda / topk /
     #      sparse_kernels expose, same inputs), for comparison with the
     #      reference's per-stage numbers
@@ -220,6 +235,10 @@ def main() -> int:
         "api_stages_us": {"query_encode": round(encode_ms * 1e3, 3), "score_encoded": round(score_ms * 1e3, 3),
                           "select_with_current": round(select_ms * 1e3, 3),
                           "indexed_attention_split_partial": round(attn_ms * 1e3, 3)},
+        "prepack": {"tokens": L, "us": round(prepack_ms * 1e3, 3), "algorithmic_bytes": prepack_bytes,
+                    "GBps": round(prepack_bytes / (prepack_ms * 1e-3) / 1e9, 1)},
+        "append": {"active_tokens": int(active.shape[1]), "us": round(append_ms * 1e3, 3),
+                   "algorithmic_bytes": append_bytes, "GBps": round(append_bytes / (append_ms * 1e-3) / 1e9, 1)},
         "unique_kv_rows_per_step": unique_rows,
         "roofline": {"bound": "hbm", "kernel": "attn_rank_kernel (layer step attention)",
                      "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

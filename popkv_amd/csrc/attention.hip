@@ -67,15 +67,18 @@ __device__ __forceinline__ void merge_state(SoftmaxState& a, float m2, float l2,
 // All threads of the block call it.
 template <int LPR>
 __device__ __forceinline__ void store_partial(SoftmaxState st, int lane, int wave, int dim0, int d, float* dst) {
-#pragma unroll
-    for (int m = LPR; m < kWave; m <<= 1) {
-        const float m2 = __shfl_xor(st.m, m);
-        const float l2 = __shfl_xor(st.l, m);
+    auto merge_xor = [&](auto mtag) {
+        constexpr int M = decltype(mtag)::value;
+        const float m2 = lane_xor<M>(st.m);
+        const float l2 = lane_xor<M>(st.l);
         float a2[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a2[i] = __shfl_xor(st.acc[i], m);
+        for (int i = 0; i < 8; ++i) a2[i] = lane_xor<M>(st.acc[i]);
         merge_state(st, m2, l2, a2);
-    }
+    };
+    if constexpr (LPR <= 8) merge_xor(std::integral_constant<int, 8>{});
+    if constexpr (LPR <= 16) merge_xor(std::integral_constant<int, 16>{});
+    merge_xor(std::integral_constant<int, 32>{});
     __shared__ float s_m[kAttnWaves], s_l[kAttnWaves];
     __shared__ float s_acc[kAttnWaves][256];
     if (lane < LPR) {
@@ -418,7 +421,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
 #pragma unroll
     for (int i = 0; i < WPT; ++i) cnt += __popc(mw[i]);
     uint32_t total;
-    uint32_t rank = block_excl_scan(cnt, s_scan, kAttnWaves, &total);
+    uint32_t rank = block_excl_scan_once(cnt, s_scan, kAttnWaves, &total);
     const uint32_t r0 = static_cast<uint32_t>(s) * kSplitRows;
     const uint32_t r1 = min(r0 + kSplitRows, static_cast<uint32_t>(k));
     if (rank < r1 && rank + cnt > r0) {

@@ -191,6 +191,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Value of lane l^16 / l^32 (all 64 lanes active), with gfx950's
+// v_permlane16_swap / v_permlane32_swap instead of an LDS permute.  With both
+// operands equal to x, permlane32_swap returns (x[l & 31], x[(l & 31) + 32])
+// and permlane16_swap returns (x[l & ~16], x[l | 16]) in every lane.
+__device__ __forceinline__ float lane_xor16(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    if constexpr (M == 16) return lane_xor16(v);
+    else if constexpr (M == 32) return lane_xor32(v);
+    else return __shfl_xor(v, M);
+}
+
 // Inclusive prefix sum across the wave with DPP (VALU only): row_shr 1, 2,
 // 4, 8 scan each 16-lane row (lanes without a source add 0), then
 // row_bcast:15 adds lane 15's total to rows 1 and 3 and row_bcast:31 adds
@@ -229,6 +250,26 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, in
     __syncthreads();
     uint32_t base = sh[wave];
     *total = sh[waves];
+    return base + incl - v;
+}
+
+// Exclusive prefix sum across a block of `waves` wave64s with a single
+// barrier: DPP scan inside each wave, wave totals through `sh` (`waves`
+// words).  For one use of `sh` per kernel (nothing may still be reading it).
+// Every thread of the block must call it.
+__device__ __forceinline__ uint32_t block_excl_scan_once(uint32_t v, uint32_t* sh, int waves, uint32_t* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const uint32_t incl = wave_incl_scan(v, lane);
+    if (lane == kWave - 1) sh[wave] = incl;
+    __syncthreads();
+    uint32_t base = 0, tot = 0;
+    for (int w = 0; w < waves; ++w) {
+        const uint32_t x = sh[w];
+        base += w < wave ? x : 0u;
+        tot += x;
+    }
+    *total = tot;
     return base + incl - v;
 }
 

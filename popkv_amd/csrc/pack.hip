@@ -1,16 +1,19 @@
 // Key prepack and per-token append of PopKV retrieval metadata (gfx950).
 //
-// One workgroup of 256 threads per (KV head, token group).
-//   Phase 1 -- threads map to (dimension, token stripe): coalesced row reads,
-//              per-dimension min/max over the group's present tokens, folded
-//              to the thresholds 0.5*max / 0.5*min in LDS.
-//   Phase 2 -- threads map to tokens: each lane re-reads its own row (an L2
-//              hit right after phase 1), forms the sign/magnitude words and
-//              reduces every representative group in registers in the
-//              production tree order, then writes its token's 16-byte plane
-//              words and fp16 representatives with vector stores.
+// head_dim 128 (pack128_kernel): one wave64 per (KV head, token group).
+//   Phase 1 -- lane l owns dims 2l and 2l+1 and streams the group's rows with
+//              coalesced 4-byte loads (256 bytes per wave instruction),
+//              keeping the per-dimension min/max in registers; the thresholds
+//              0.5*max / 0.5*min go to LDS.
+//   Phase 2 -- one token per lane: the lane re-reads its own row (a cache
+//              hit), forms the sign/magnitude words and reduces every
+//              representative group in registers in the production tree
+//              order (G64 pairs dims j and j+32 first), then writes its
+//              token's 16-byte plane words and fp16 representatives.
 // No cross-lane shuffles are needed for the bit-exact sums: the tree lives in
-// one lane's registers.
+// one lane's registers.  Other head sizes (pack_kernel) use 256 threads per
+// group: per-dimension extrema by (dimension, token stripe), then one token
+// per thread.
 //
 // Semantics follow the reference packers: popkv_ext.cu:79-143 (G32),
 // :376-500 (fused G16/G64, head_dim 128), :283-374 (generic G16/G64), with
@@ -179,6 +182,141 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     }
 }
 
+// Two consecutive elements (dims 2l, 2l+1) of a row as float.
+template <typename T> __device__ __forceinline__ void load2(const T* p, float& a, float& b);
+template <> __device__ __forceinline__ void load2<bf16_t>(const bf16_t* p, float& a, float& b) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void load2<f16_t>(const f16_t* p, float& a, float& b) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+    a = bits_f16(u & 0xffffu);
+    b = bits_f16(u >> 16);
+}
+template <> __device__ __forceinline__ void load2<float>(const float* p, float& a, float& b) {
+    const float2 f = *reinterpret_cast<const float2*>(p);
+    a = f.x;
+    b = f.y;
+}
+
+// Low / high bucket sums and counts of one representative (dims r*G ..
+// r*G+G-1 of v[]), in the production tree order.  G64 pairs dims j and j+32
+// before the halving tree, so only 32 partial sums per bucket stay live.
+template <int G>
+__device__ __forceinline__ void rep_sums(const float* v, uint64_t magbits, float& ls, int& ln, float& hs, int& hn) {
+    constexpr int H = G == 64 ? 32 : G;
+    float xl[H], xh[H];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+        const bool m0 = (magbits >> j) & 1ull;
+        const float a0 = fabsf(v[j]);
+        float l = m0 ? 0.0f : a0, h = m0 ? a0 : 0.0f;
+        if constexpr (G == 64) {
+            const bool m1 = (magbits >> (j + 32)) & 1ull;
+            const float a1 = fabsf(v[j + 32]);
+            l = l + (m1 ? 0.0f : a1);
+            h = h + (m1 ? a1 : 0.0f);
+        }
+        xl[j] = l;
+        xh[j] = h;
+    }
+    ls = tree_halving(xl, H);
+    hs = tree_halving(xh, H);
+    hn = __popcll(magbits & (G == 64 ? ~0ull : ((1ull << G) - 1ull)));
+    ln = G - hn;
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(kWave) void pack128_kernel(
+    const T* __restrict__ keys, int64_t head_stride, int64_t tokens, int tg,
+    int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
+    uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta, int64_t cap, int64_t offset) {
+    constexpr int D = 128, R = D / G, PH1 = 32;
+    const int lane = threadIdx.x;
+    const int64_t kvh = blockIdx.y;
+    const int64_t gs = static_cast<int64_t>(blockIdx.x) * tg;
+    const int n = static_cast<int>(min(gs + static_cast<int64_t>(tg), tokens) - gs);
+    const T* base = keys + kvh * head_stride + gs * D;
+
+    // Phase 1: extrema of dims 2*lane, 2*lane+1 over the group's tokens.
+    float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
+    for (int t0 = 0; t0 < n; t0 += PH1) {
+        float a[PH1], b[PH1];
+#pragma unroll
+        for (int i = 0; i < PH1; ++i) {
+            const int t = min(t0 + i, n - 1);  // repeats the last row: min/max unchanged
+            load2<T>(base + static_cast<int64_t>(t) * D + 2 * lane, a[i], b[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < PH1; ++i) {
+            mn0 = fminf(mn0, a[i]); mx0 = fmaxf(mx0, a[i]);
+            mn1 = fminf(mn1, b[i]); mx1 = fmaxf(mx1, b[i]);
+        }
+    }
+    __shared__ float s_hi[D], s_lo[D];
+    s_lo[2 * lane] = mn0 * 0.5f; s_lo[2 * lane + 1] = mn1 * 0.5f;
+    s_hi[2 * lane] = mx0 * 0.5f; s_hi[2 * lane + 1] = mx1 * 0.5f;
+    __syncthreads();
+
+    // Phase 2: one token per lane.
+    for (int t = lane; t < n; t += kWave) {
+        const T* row = base + static_cast<int64_t>(t) * D;
+        const int64_t orow = kvh * cap + offset + gs + t;
+        uint32_t sw[4], mw[4];
+        float lows[R], deltas[R];
+        constexpr int CH = G > 32 ? G : 32;  // dims per chunk: whole plane words and whole reps
+#pragma unroll
+        for (int c = 0; c < D / CH; ++c) {
+            float v[CH];
+#pragma unroll
+            for (int i = 0; i < CH; i += 8) load8<T>(row + c * CH + i, v + i);
+            uint64_t mg = 0;
+#pragma unroll
+            for (int wi = 0; wi < CH / 32; ++wi) {
+                uint32_t sgw = 0, mgw = 0;
+#pragma unroll
+                for (int j = 0; j < 32; ++j) {
+                    const int i = wi * 32 + j, dim = c * CH + i;
+                    const bool sg = v[i] >= 0.0f;
+                    const bool m = sg ? v[i] > s_hi[dim] : v[i] < s_lo[dim];
+                    sgw |= static_cast<uint32_t>(sg) << j;
+                    mgw |= static_cast<uint32_t>(m) << j;
+                }
+                sw[c * (CH / 32) + wi] = sgw;
+                mw[c * (CH / 32) + wi] = mgw;
+                mg |= static_cast<uint64_t>(mgw) << (32 * wi);
+            }
+#pragma unroll
+            for (int rr = 0; rr < CH / G; ++rr) {
+                float ls, hs;
+                int ln, hn;
+                rep_sums<G>(v + rr * G, mg >> (rr * G), ls, ln, hs, hn);
+                finish_rep(ls, ln, hs, hn, lows[c * (CH / G) + rr], deltas[c * (CH / G) + rr]);
+            }
+        }
+        reinterpret_cast<uint4*>(k_sign)[orow] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+        reinterpret_cast<uint4*>(k_mag)[orow] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+        uint32_t lo_p[R / 2], de_p[R / 2];
+#pragma unroll
+        for (int r = 0; r < R / 2; ++r) {
+            lo_p[r] = static_cast<uint32_t>(f16_rne(lows[2 * r])) | (static_cast<uint32_t>(f16_rne(lows[2 * r + 1])) << 16);
+            de_p[r] = static_cast<uint32_t>(f16_rne(deltas[2 * r])) |
+                      (static_cast<uint32_t>(f16_rne(deltas[2 * r + 1])) << 16);
+        }
+        if constexpr (R == 2) {
+            reinterpret_cast<uint32_t*>(k_low)[orow] = lo_p[0];
+            reinterpret_cast<uint32_t*>(k_delta)[orow] = de_p[0];
+        } else if constexpr (R == 4) {
+            reinterpret_cast<uint2*>(k_low)[orow] = make_uint2(lo_p[0], lo_p[1]);
+            reinterpret_cast<uint2*>(k_delta)[orow] = make_uint2(de_p[0], de_p[1]);
+        } else {
+            reinterpret_cast<uint4*>(k_low)[orow] = make_uint4(lo_p[0], lo_p[1], lo_p[2], lo_p[3]);
+            reinterpret_cast<uint4*>(k_delta)[orow] = make_uint4(de_p[0], de_p[1], de_p[2], de_p[3]);
+        }
+    }
+}
+
 template <typename T, int G>
 hipError_t launch_pack_t(const T* keys, int64_t kvh, int64_t tokens, int d, int64_t head_stride,
                          int32_t* ks, int32_t* km, uint16_t* kl, uint16_t* kd, int64_t cap, int64_t off,
@@ -190,8 +328,8 @@ hipError_t launch_pack_t(const T* keys, int64_t kvh, int64_t tokens, int d, int6
                       (reinterpret_cast<uintptr_t>(ks) % 16 == 0) && (reinterpret_cast<uintptr_t>(km) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(kl) % 16 == 0) && (reinterpret_cast<uintptr_t>(kd) % 16 == 0);
     if (fast)
-        hipLaunchKernelGGL((pack_kernel<T, G, true>), grid, dim3(kPackThreads), 0, stream, keys, head_stride,
-                           tokens, d, tg, ks, km, kl, kd, cap, off);
+        hipLaunchKernelGGL((pack128_kernel<T, G>), grid, dim3(kWave), 0, stream, keys, head_stride, tokens, tg, ks,
+                           km, kl, kd, cap, off);
     else
         hipLaunchKernelGGL((pack_kernel<T, G, false>), grid, dim3(kPackThreads), 0, stream, keys, head_stride,
                            tokens, d, tg, ks, km, kl, kd, cap, off);

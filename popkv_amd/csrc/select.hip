@@ -404,7 +404,7 @@ __global__ __launch_bounds__(kSelThreads) void mask_to_indices_kernel(
         cnt += __popc(w[i]);
     }
     uint32_t total;
-    uint32_t pos = block_excl_scan(cnt, scan_sh, kSelWaves, &total);
+    uint32_t pos = block_excl_scan_once(cnt, scan_sh, kSelWaves, &total);
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
         const int64_t tbase = (static_cast<int64_t>(tid) * WPT + i) * 32;
