@@ -1,15 +1,17 @@
 // Key prepack and per-token append of PopKV retrieval metadata (gfx950).
 //
-// head_dim 128 (pack128_kernel): one wave64 per (KV head, token group).
-//   Phase 1 -- lane l owns dims 2l and 2l+1 and streams the group's rows with
-//              coalesced 4-byte loads (256 bytes per wave instruction),
-//              keeping the per-dimension min/max in registers; the thresholds
+// head_dim 128 (pack128_kernel): one workgroup per (KV head, token group),
+// one wave per chunk of max(G, 32) dimensions (2 or 4 waves).
+//   Phase 1 -- lane l owns dims 2l and 2l+1; the waves stream interleaved
+//              rows of the group with coalesced 4-byte loads (256 bytes per
+//              wave instruction), keeping per-dimension min/max in registers;
+//              the partial extrema meet in LDS and the thresholds
 //              0.5*max / 0.5*min go to LDS.
-//   Phase 2 -- one token per lane: the lane re-reads its own row (a cache
-//              hit), forms the sign/magnitude words and reduces every
-//              representative group in registers in the production tree
-//              order (G64 pairs dims j and j+32 first), then writes its
-//              token's 16-byte plane words and fp16 representatives.
+//   Phase 2 -- one token per lane, each wave on its dimension chunk: the
+//              lane re-reads its slice of the row (a cache hit), forms the
+//              sign/magnitude words and reduces its representatives in
+//              registers in the production tree order (G64 pairs dims j and
+//              j+32 first), then writes its words and fp16 representatives.
 // No cross-lane shuffles are needed for the bit-exact sums: the tree lives in
 // one lane's registers.  Other head sizes (pack_kernel) use 256 threads per
 // group: per-dimension extrema by (dimension, token stripe), then one token
@@ -200,52 +202,30 @@ template <> __device__ __forceinline__ void load2<float>(const float* p, float& 
     b = f.y;
 }
 
-// Low / high bucket sums and counts of one representative (dims r*G ..
-// r*G+G-1 of v[]), in the production tree order.  G64 pairs dims j and j+32
-// before the halving tree, so only 32 partial sums per bucket stay live.
-template <int G>
-__device__ __forceinline__ void rep_sums(const float* v, uint64_t magbits, float& ls, int& ln, float& hs, int& hn) {
-    constexpr int H = G == 64 ? 32 : G;
-    float xl[H], xh[H];
-#pragma unroll
-    for (int j = 0; j < H; ++j) {
-        const bool m0 = (magbits >> j) & 1ull;
-        const float a0 = fabsf(v[j]);
-        float l = m0 ? 0.0f : a0, h = m0 ? a0 : 0.0f;
-        if constexpr (G == 64) {
-            const bool m1 = (magbits >> (j + 32)) & 1ull;
-            const float a1 = fabsf(v[j + 32]);
-            l = l + (m1 ? 0.0f : a1);
-            h = h + (m1 ? a1 : 0.0f);
-        }
-        xl[j] = l;
-        xh[j] = h;
-    }
-    ls = tree_halving(xl, H);
-    hs = tree_halving(xh, H);
-    hn = __popcll(magbits & (G == 64 ? ~0ull : ((1ull << G) - 1ull)));
-    ln = G - hn;
-}
+// Waves per workgroup of pack128_kernel: one per chunk of CH = max(G, 32)
+// dimensions (whole plane words and whole representatives).
+template <int G> constexpr int pack128_waves() { return 128 / (G > 32 ? G : 32); }
 
 template <typename T, int G>
-__global__ __launch_bounds__(kWave) void pack128_kernel(
+__global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     const T* __restrict__ keys, int64_t head_stride, int64_t tokens, int tg,
     int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
     uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta, int64_t cap, int64_t offset) {
-    constexpr int D = 128, R = D / G, PH1 = 32;
-    const int lane = threadIdx.x;
+    constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
     const int64_t kvh = blockIdx.y;
     const int64_t gs = static_cast<int64_t>(blockIdx.x) * tg;
     const int n = static_cast<int>(min(gs + static_cast<int64_t>(tg), tokens) - gs);
     const T* base = keys + kvh * head_stride + gs * D;
 
-    // Phase 1: extrema of dims 2*lane, 2*lane+1 over the group's tokens.
+    // Phase 1: extrema of dims 2*lane, 2*lane+1; wave w takes tokens w, w+NW, ...
     float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
-    for (int t0 = 0; t0 < n; t0 += PH1) {
+    for (int t0 = wave; t0 < n; t0 += PH1 * NW) {
         float a[PH1], b[PH1];
 #pragma unroll
         for (int i = 0; i < PH1; ++i) {
-            const int t = min(t0 + i, n - 1);  // repeats the last row: min/max unchanged
+            const int t = min(t0 + i * NW, n - 1);  // repeats the last row: min/max unchanged
             load2<T>(base + static_cast<int64_t>(t) * D + 2 * lane, a[i], b[i]);
         }
 #pragma unroll
@@ -254,65 +234,99 @@ __global__ __launch_bounds__(kWave) void pack128_kernel(
             mn1 = fminf(mn1, b[i]); mx1 = fmaxf(mx1, b[i]);
         }
     }
-    __shared__ float s_hi[D], s_lo[D];
-    s_lo[2 * lane] = mn0 * 0.5f; s_lo[2 * lane + 1] = mn1 * 0.5f;
-    s_hi[2 * lane] = mx0 * 0.5f; s_hi[2 * lane + 1] = mx1 * 0.5f;
+    __shared__ float s_mn[NW][D], s_mx[NW][D];
+    __shared__ float s_hi[D], s_nlo[D];  // 0.5*max and -(0.5*min)
+    s_mn[wave][2 * lane] = mn0; s_mn[wave][2 * lane + 1] = mn1;
+    s_mx[wave][2 * lane] = mx0; s_mx[wave][2 * lane + 1] = mx1;
+    __syncthreads();
+    if (threadIdx.x < D) {
+        float mn = s_mn[0][threadIdx.x], mx = s_mx[0][threadIdx.x];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            mn = fminf(mn, s_mn[w][threadIdx.x]);
+            mx = fmaxf(mx, s_mx[w][threadIdx.x]);
+        }
+        s_nlo[threadIdx.x] = -(mn * 0.5f);
+        s_hi[threadIdx.x] = mx * 0.5f;
+    }
     __syncthreads();
 
-    // Phase 2: one token per lane.
+    // Phase 2: wave w encodes dims [w*CH, w*CH + CH) of one token per lane,
+    // one 32-dimension plane word at a time.  Per dimension: sign
+    // s = v >= 0, magnitude m = s ? v > hi : v < lo; the word bits are
+    // shifted in from the top (w = 2w + bit); |v| goes to the low or the high
+    // bucket.  G64 adds dims j and j+32 (its two plane words) before the
+    // halving tree; G32 / G16 reduce within one word.
+    const int c0 = wave * CH;
     for (int t = lane; t < n; t += kWave) {
-        const T* row = base + static_cast<int64_t>(t) * D;
+        const T* row = base + static_cast<int64_t>(t) * D + c0;
         const int64_t orow = kvh * cap + offset + gs + t;
-        uint32_t sw[4], mw[4];
-        float lows[R], deltas[R];
-        constexpr int CH = G > 32 ? G : 32;  // dims per chunk: whole plane words and whole reps
+        constexpr int NWD = CH / 32, NR = CH / G;
+        uint32_t sw[NWD], mw[NWD];
+        float lows[NR], deltas[NR];
+        float pl[32], ph[32];  // G64: first-level pair sums
 #pragma unroll
-        for (int c = 0; c < D / CH; ++c) {
-            float v[CH];
+        for (int wi = 0; wi < NWD; ++wi) {
+            float v[32];
 #pragma unroll
-            for (int i = 0; i < CH; i += 8) load8<T>(row + c * CH + i, v + i);
-            uint64_t mg = 0;
+            for (int i = 0; i < 32; i += 8) load8<T>(row + wi * 32 + i, v + i);
+            uint32_t sgw = 0, mgw = 0;
+            float xl[32], xh[32];
 #pragma unroll
-            for (int wi = 0; wi < CH / 32; ++wi) {
-                uint32_t sgw = 0, mgw = 0;
+            for (int j = 31; j >= 0; --j) {
+                // m = s ? v > hi : v < lo is |v| > (s ? hi : -lo): for v < 0,
+                // v < lo <=> -v > -lo; for v = -0 both sides read 0 > hi; a
+                // NaN has s = 0 and fails the compare.  The thresholds pass
+                // through an empty asm: the same in every lane, they stay in
+                // VGPRs, and the dimensions stay in order.
+                float hi = s_hi[c0 + wi * 32 + j], nlo = s_nlo[c0 + wi * 32 + j];
+                asm volatile("" : "+v"(hi), "+v"(nlo), "+v"(sgw), "+v"(mgw));
+                const float a = fabsf(v[j]);
+                const bool sg = v[j] >= 0.0f;
+                const bool mg = a > (sg ? hi : nlo);
+                sgw = sgw * 2u + static_cast<uint32_t>(sg);
+                mgw = mgw * 2u + static_cast<uint32_t>(mg);
+                xl[j] = mg ? 0.0f : a;
+                xh[j] = mg ? a : 0.0f;
+            }
+            sw[wi] = sgw;
+            mw[wi] = mgw;
+            if constexpr (G == 64) {
+                if (wi == 0) {
 #pragma unroll
-                for (int j = 0; j < 32; ++j) {
-                    const int i = wi * 32 + j, dim = c * CH + i;
-                    const bool sg = v[i] >= 0.0f;
-                    const bool m = sg ? v[i] > s_hi[dim] : v[i] < s_lo[dim];
-                    sgw |= static_cast<uint32_t>(sg) << j;
-                    mgw |= static_cast<uint32_t>(m) << j;
+                    for (int j = 0; j < 32; ++j) { pl[j] = xl[j]; ph[j] = xh[j]; }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) { pl[j] = pl[j] + xl[j]; ph[j] = ph[j] + xh[j]; }
+                    const int hn = __popc(mw[0]) + __popc(mgw);
+                    finish_rep(tree_halving(pl, 32), 64 - hn, tree_halving(ph, 32), hn, lows[0], deltas[0]);
                 }
-                sw[c * (CH / 32) + wi] = sgw;
-                mw[c * (CH / 32) + wi] = mgw;
-                mg |= static_cast<uint64_t>(mgw) << (32 * wi);
-            }
+            } else if constexpr (G == 32) {
+                const int hn = __popc(mgw);
+                finish_rep(tree_halving(xl, 32), 32 - hn, tree_halving(xh, 32), hn, lows[0], deltas[0]);
+            } else {
 #pragma unroll
-            for (int rr = 0; rr < CH / G; ++rr) {
-                float ls, hs;
-                int ln, hn;
-                rep_sums<G>(v + rr * G, mg >> (rr * G), ls, ln, hs, hn);
-                finish_rep(ls, ln, hs, hn, lows[c * (CH / G) + rr], deltas[c * (CH / G) + rr]);
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int hn = __popc(hf ? (mgw >> 16) : (mgw & 0xffffu));
+                    finish_rep(tree_halving(xl + 16 * hf, 16), 16 - hn, tree_halving(xh + 16 * hf, 16), hn,
+                               lows[hf], deltas[hf]);
+                }
             }
         }
-        reinterpret_cast<uint4*>(k_sign)[orow] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
-        reinterpret_cast<uint4*>(k_mag)[orow] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
-        uint32_t lo_p[R / 2], de_p[R / 2];
+        const int w0 = c0 / 32, r0 = c0 / G;
 #pragma unroll
-        for (int r = 0; r < R / 2; ++r) {
-            lo_p[r] = static_cast<uint32_t>(f16_rne(lows[2 * r])) | (static_cast<uint32_t>(f16_rne(lows[2 * r + 1])) << 16);
-            de_p[r] = static_cast<uint32_t>(f16_rne(deltas[2 * r])) |
-                      (static_cast<uint32_t>(f16_rne(deltas[2 * r + 1])) << 16);
+        for (int wi = 0; wi < NWD; ++wi) {
+            k_sign[orow * 4 + w0 + wi] = static_cast<int32_t>(sw[wi]);
+            k_mag[orow * 4 + w0 + wi] = static_cast<int32_t>(mw[wi]);
         }
-        if constexpr (R == 2) {
-            reinterpret_cast<uint32_t*>(k_low)[orow] = lo_p[0];
-            reinterpret_cast<uint32_t*>(k_delta)[orow] = de_p[0];
-        } else if constexpr (R == 4) {
-            reinterpret_cast<uint2*>(k_low)[orow] = make_uint2(lo_p[0], lo_p[1]);
-            reinterpret_cast<uint2*>(k_delta)[orow] = make_uint2(de_p[0], de_p[1]);
+        if constexpr (NR == 1) {
+            k_low[orow * R + r0] = f16_rne(lows[0]);
+            k_delta[orow * R + r0] = f16_rne(deltas[0]);
         } else {
-            reinterpret_cast<uint4*>(k_low)[orow] = make_uint4(lo_p[0], lo_p[1], lo_p[2], lo_p[3]);
-            reinterpret_cast<uint4*>(k_delta)[orow] = make_uint4(de_p[0], de_p[1], de_p[2], de_p[3]);
+            reinterpret_cast<uint32_t*>(k_low + orow * R + r0)[0] =
+                static_cast<uint32_t>(f16_rne(lows[0])) | (static_cast<uint32_t>(f16_rne(lows[1])) << 16);
+            reinterpret_cast<uint32_t*>(k_delta + orow * R + r0)[0] =
+                static_cast<uint32_t>(f16_rne(deltas[0])) | (static_cast<uint32_t>(f16_rne(deltas[1])) << 16);
         }
     }
 }
@@ -328,8 +342,8 @@ hipError_t launch_pack_t(const T* keys, int64_t kvh, int64_t tokens, int d, int6
                       (reinterpret_cast<uintptr_t>(ks) % 16 == 0) && (reinterpret_cast<uintptr_t>(km) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(kl) % 16 == 0) && (reinterpret_cast<uintptr_t>(kd) % 16 == 0);
     if (fast)
-        hipLaunchKernelGGL((pack128_kernel<T, G>), grid, dim3(kWave), 0, stream, keys, head_stride, tokens, tg, ks,
-                           km, kl, kd, cap, off);
+        hipLaunchKernelGGL((pack128_kernel<T, G>), grid, dim3(kWave * pack128_waves<G>()), 0, stream, keys,
+                           head_stride, tokens, tg, ks, km, kl, kd, cap, off);
     else
         hipLaunchKernelGGL((pack_kernel<T, G, false>), grid, dim3(kPackThreads), 0, stream, keys, head_stride,
                            tokens, d, tg, ks, km, kl, kd, cap, off);
