@@ -51,9 +51,206 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     p.add_argument("--no-graph", action="store_true", help="time eager launches only")
+    p.add_argument("--workload", default="c1",
+                   help="c1 (default), c3-<context> (PopKV-S context sweep), c2-layer<l> (PopKV-Q layer l), c0, "
+                        "c4 (8 sequences x 64K, step = layer step + append), "
+                        "c2 (32-layer PopKV-Q stack, layers 0-1 dense)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run plain 256 MiB device copies (scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
+
+
+def pick_workload(name: str):
+    """The named configuration of workloads.py (C1 is the headline one)."""
+    from popkv_amd import workloads
+
+    if name == "c1":
+        return workloads.C1
+    if name == "c0":
+        return workloads.C0
+    if name.startswith("c3-"):
+        return workloads.c3(int(name[3:]))
+    if name.startswith("c2-layer"):
+        return workloads.c2_layer(int(name[len("c2-layer"):]))
+    raise SystemExit(f"unknown workload {name!r}")
+
+
+def bench_c2(args) -> int:
+    """C2: one decode step through a 32-layer stack at Llama-3.1-8B shapes,
+    32K context, budget 4096, bf16.  Layers 0-1 run dense attention over
+    all tokens (popkv_dense_attention); layers 2-31 run the PopKV-Q layer
+    step (TG 128, G 16).  Each layer has its own K/V, packed cache and query
+    (seed 42 + layer); the 32 layers (4.6 GB) rotate through HBM naturally.
+    The whole stack is one HIP graph; value = µs per stack step."""
+    import torch
+
+    from popkv_amd import popkv, workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n_layers, dense_layers = 32, (0, 1)
+    layers = []
+    for li in range(n_layers):
+        w = workloads.c2_layer(li)
+        lay = workloads.make_layer(w).to(dev)
+        L = lay.prefix_tokens
+        cache = None
+        if li not in dense_layers:
+            cache = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                            reserve_tokens=128)
+        layers.append((w, lay, cache, torch.empty_like(lay.queries)))
+    w0 = layers[0][0]
+    mapping = workloads.head_to_kv(w0, dev)
+    ws, dws = popkv.LayerStepWorkspace(), popkv.LayerStepWorkspace()
+    stream = torch.cuda.current_stream(dev)
+
+    def stack_step() -> None:
+        for li, (w, lay, cache, out) in enumerate(layers):
+            if cache is None:
+                popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(),
+                                           lay.current_v(), mapping, workspace=dws, out=out)
+            else:
+                popkv.popkv_layer_step(lay.queries, cache, lay.prefix_k(), lay.prefix_v(), lay.current_k(),
+                                       lay.current_v(), mapping, budget=w.budget, workspace=ws, out=out)
+
+    for _ in range(max(1, args.warmup // 8)):
+        stack_step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        stack_step()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        stack_step()
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 16)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        g.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    L = w0.prefix_tokens
+    sparse_bytes = workloads.algorithmic_bytes(layers[2][0])["step"]
+    # dense layer: every K/V row of a KV head read once (shared by its GQA
+    # group), plus q in / out per query head
+    dense_bytes = w0.kv_heads * (L + 1) * w0.head_dim * 2 * 2 + w0.q_heads * w0.head_dim * 2 * 2
+    total = (n_layers - len(dense_layers)) * sparse_bytes + len(dense_layers) * dense_bytes
+    print(json.dumps({
+        "metric": "us per decode step through the 32-layer stack (C2: PopKV-Q, layers 0-1 dense); achieved HBM GB/s",
+        "value": round(ms * 1e3, 3), "unit": "us/step", "n_gpus": 1, "steps": reps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded per layer; outlier-channel K, peaked Q; resident in HBM)",
+        "config": {"workload": "C2-popkv-q-32-layers", "layers": n_layers, "dense_layers": list(dense_layers),
+                   "q_heads": w0.q_heads, "kv_heads": w0.kv_heads, "head_dim": w0.head_dim, "context": w0.context,
+                   "budget": w0.budget, "timing": "hip-graph replay of the stack"},
+        "step_algorithmic_bytes": total, "achieved_GBps": round(total / (ms * 1e-3) / 1e9, 1),
+        "per_layer_us": round(ms * 1e3 / n_layers, 3),
+    }), flush=True)
+    return 0
+
+
+def bench_c4(args) -> int:
+    """C4: 8 independent sequences x 64K context (PopKV-S, budget 4096).  The
+    sequences are laid side by side along the head axis -- K/V [8*KVH, C, D],
+    packed caches [8*KVH, cap, ...], queries [8*QH, D] with head i mapped to
+    KV head i // 4 -- so one popkv_layer_step serves the whole batch.  A step
+    is the layer step plus the per-token append (re-encode of each sequence's
+    active token group with the new key); the one-time prepack of the 64K
+    prefixes is timed on its own.  Two input sets rotate (4.3 GB)."""
+    import torch
+
+    from popkv_amd import popkv, popkv_cuda, workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w = workloads.C4
+    B, L = w.batch, w.prefix_tokens
+    layers = [workloads.make_layer(w, seed=w.seed + b) for b in range(B)]
+    keys = torch.cat([x.keys for x in layers], 0)        # [B*KVH, C, D]
+    values = torch.cat([x.values for x in layers], 0)
+    q = torch.cat([x.queries for x in layers], 0).to(dev)  # [B*QH, D]
+    del layers
+    qh, kvh = B * w.q_heads, B * w.kv_heads
+    mapping = torch.arange(qh, device=dev, dtype=torch.long) // (w.q_heads // w.kv_heads)
+    sealed = (L // w.token_group) * w.token_group
+    n_sets = 2
+    sets = []
+    for _ in range(n_sets):
+        k_d, v_d = keys.to(dev), values.to(dev)
+        cache = popkv.build_popkv_cache(k_d[:, :L], group_size=w.token_group, dim_group_size=w.dim_group,
+                                        reserve_tokens=64)
+        active = k_d[:, sealed:L + 1].contiguous()       # active group + the new token
+        sets.append((k_d[:, :L], v_d[:, :L], k_d[:, L].contiguous(), v_d[:, L].contiguous(), cache, active))
+    ws = popkv.LayerStepWorkspace()
+    outs = [torch.empty_like(q) for _ in range(n_sets)]
+    stream = torch.cuda.current_stream(dev)
+
+    def step(i: int) -> None:
+        pk, pv, ck, cv, cache, active = sets[i % n_sets]
+        popkv.popkv_layer_step(q, cache, pk, pv, ck, cv, mapping, budget=w.budget, workspace=ws, out=outs[i % n_sets])
+        popkv_cuda.pack_keys_into(active, cache.packed, token_offset=sealed, token_group_size=w.token_group,
+                                  dim_group_size=w.dim_group)
+
+    prefix_c = [st[0].contiguous() for st in sets]
+
+    def prepack(i: int) -> None:
+        popkv_cuda.pack_keys_into(prefix_c[i % n_sets], sets[i % n_sets][4].packed, token_offset=0,
+                                  token_group_size=w.token_group, dim_group_size=w.dim_group)
+
+    def graph_ms(fn, reps: int) -> float:
+        for i in range(n_sets):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(n_sets):
+                fn(i)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(n_sets):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / (reps * n_sets)
+
+    for i in range(args.warmup):
+        step(i)
+    step_ms = graph_ms(step, max(1, args.steps // n_sets))
+    prepack_ms = graph_ms(prepack, 8)
+    per_seq = workloads.algorithmic_bytes(w)
+    meta_row = 32 + 4 * (w.head_dim // w.dim_group)
+    append_bytes = kvh * int(sets[0][5].shape[1]) * (w.head_dim * 2 + meta_row)
+    step_bytes = B * per_seq["step"] + append_bytes
+    prepack_bytes = B * per_seq["prepack"]
+    print(json.dumps({
+        "metric": "us per batched decode step per layer (C4: 8 x 64K, layer step + append); achieved HBM GB/s",
+        "value": round(step_ms * 1e3, 3), "unit": "us/step-layer", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded per sequence; outlier-channel K, peaked Q; resident in HBM)",
+        "config": {"workload": w.name, "method": w.method, "batch": B, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
+                   "head_dim": w.head_dim, "context": w.context, "budget": w.budget, "rotating_buffers": n_sets,
+                   "timing": "hip-graph replay"},
+        "step_algorithmic_bytes": step_bytes, "achieved_GBps": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
+        "prepack": {"tokens_per_sequence": L, "us": round(prepack_ms * 1e3, 3), "algorithmic_bytes": prepack_bytes,
+                    "GBps": round(prepack_bytes / (prepack_ms * 1e-3) / 1e9, 1)},
+    }), flush=True)
+    return 0
 
 
 def copy_calibration(steps: int) -> int:
@@ -81,6 +278,10 @@ def main() -> int:
 
     if args.copy_calibration:
         return copy_calibration(args.steps)
+    if args.workload == "c4":
+        return bench_c4(args)
+    if args.workload == "c2":
+        return bench_c2(args)
 
     import torch
 
@@ -91,7 +292,7 @@ def main() -> int:
         return 2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    w = workloads.C1
+    w = pick_workload(args.workload)
     L, kk = w.prefix_tokens, w.k
     alg = workloads.algorithmic_bytes(w)
 
@@ -207,7 +408,8 @@ def main() -> int:
         q, sets[i % N_BUFFERS][0], sets[i % N_BUFFERS][1], cur_k, cur_v, indices, mapping, split_tokens=256), reps)
     encode_ms = stage_timer(lambda i: popkv_cuda.query_encode(q.unsqueeze(0).contiguous(),
                                                               dim_group_size=w.dim_group), reps)
-    unique_rows = int(sum(torch.unique(indices[h * 4:(h + 1) * 4].flatten()).numel() for h in range(w.kv_heads)))
+    qpk = w.q_heads // w.kv_heads
+    unique_rows = int(sum(torch.unique(indices[h * qpk:(h + 1) * qpk].flatten()).numel() for h in range(w.kv_heads)))
 
     step_gbps = alg["step"] / (ms_per_step * 1e-3) / 1e9
     attn_gbps = alg["attention"] / (attn_step_ms * 1e-3) / 1e9
@@ -222,8 +424,9 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded C1 distribution: outlier-channel K, peaked Q; generated on host, resident in HBM)",
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w.dtype],
+        "data": ("synthetic (seeded; outlier-channel K, peaked Q; generated on host, resident in HBM)" if w.peaked
+                 else "synthetic (seeded i.i.d. N(0,1) K/V/Q; generated on host, resident in HBM)"),
         "config": {"workload": w.name, "method": w.method, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
                    "head_dim": w.head_dim, "context": w.context, "budget": w.budget, "token_group": w.token_group,
                    "dim_group": w.dim_group, "batch": 1, "rotating_buffers": N_BUFFERS,

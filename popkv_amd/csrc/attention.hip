@@ -380,13 +380,75 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
     return d2(a.w, b.w, d2(a.z, b.z, d2(a.y, b.y, d2(a.x, b.x, 0.0f))));
 }
 
+// Gathers rows tok_of(0 .. n_rows-1) of K/V (head_dim 128, 16 lanes per
+// 256-byte row, NB rows in flight per lane) and folds them into the lane's
+// online-softmax state.  kb / vb point at this lane's 8-element slice of row
+// 0.  An idle slot re-reads row tok_of(0) (its weight is exactly 0), so no
+// row outside the list is touched.
+template <typename T, int NB, typename TokOf>
+__device__ __forceinline__ SoftmaxState attend_rows(const Raw8<T>& qr, const char* kb, const char* vb, int n_rows,
+                                                    TokOf tok_of, float scale, int slot) {
+    constexpr int D = 128, LPR = 16, ROWS_PER_PASS = (kWave / LPR) * kAttnWaves;
+    SoftmaxState st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = 0.0f;
+    for (int base = 0; base < n_rows; base += ROWS_PER_PASS * NB) {
+        Raw8<T> kr[NB], vr[NB];
+        bool live[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int r = base + b * ROWS_PER_PASS + slot;
+            live[b] = r < n_rows;
+            const uint32_t off = static_cast<uint32_t>(tok_of(live[b] ? r : 0)) * (D * sizeof(T));
+            kr[b].load(reinterpret_cast<const T*>(kb + off));
+            vr[b].load(reinterpret_cast<const T*>(vb + off));
+        }
+        float logit[NB];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float dot;
+            if constexpr (sizeof(T) == 2) {
+                dot = dot8<T>(qr.u, kr[b].u);
+            } else {
+                dot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dot = fmaf(qr.get(i), kr[b].get(i), dot);
+            }
+            dot = row_sum<LPR>(dot);
+            logit[b] = live[b] ? dot * scale : -INFINITY;
+            bm = fmaxf(bm, logit[b]);
+        }
+        // every slot has at least its first row live in a non-empty pass, so
+        // bm is finite wherever live[0]; fully idle slots keep m = -inf
+        const float mnew = fmaxf(st.m, bm);
+        if (mnew != -INFINITY) {
+            const float alpha = __expf(st.m - mnew);  // st.m = -inf gives 0
+            st.l *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float p = __expf(logit[b] - mnew);  // -inf logit gives 0
+                st.l += p;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) st.acc[i] = fmaf(p, vr[b].get(i), st.acc[i]);
+            }
+            st.m = mnew;
+        }
+    }
+    return st;
+}
+
 template <typename T, int NB, int WPT>
 __global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint32_t* __restrict__ mask, int64_t mask_stride, int64_t tokens, int64_t k,
     const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials, int nsplit) {
     static_assert(WPT % 4 == 0, "mask words are read as 16-byte packets");
-    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, ROWS_PER_PASS = SLOTS * kAttnWaves;
+    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR;
     const int h = blockIdx.y;
     const int s = blockIdx.x;
     const int tid = threadIdx.x;
@@ -439,58 +501,37 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
 
     const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
     const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
-    SoftmaxState st;
-    st.m = -INFINITY;
-    st.l = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) st.acc[i] = 0.0f;
-    for (int base = 0; base < n_rows; base += ROWS_PER_PASS * NB) {
-        Raw8<T> kr[NB], vr[NB];
-        bool live[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int r = base + b * ROWS_PER_PASS + slot;
-            live[b] = r < n_rows;
-            // an idle slot re-reads the split's first selected row (its
-            // weight is exactly 0), so no unselected row's data is touched
-            const uint32_t off = static_cast<uint32_t>(s_tok[live[b] ? r : 0]) * (D * sizeof(T));
-            kr[b].load(reinterpret_cast<const T*>(kb + off));
-            vr[b].load(reinterpret_cast<const T*>(vb + off));
-        }
-        float logit[NB];
-        float bm = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float dot;
-            if constexpr (sizeof(T) == 2) {
-                dot = dot8<T>(qr.u, kr[b].u);
-            } else {
-                dot = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) dot = fmaf(qr.get(i), kr[b].get(i), dot);
-            }
-            dot = row_sum<LPR>(dot);
-            logit[b] = live[b] ? dot * scale : -INFINITY;
-            bm = fmaxf(bm, logit[b]);
-        }
-        // every slot has at least its first row live in a non-empty pass, so
-        // bm is finite wherever live[0]; fully idle slots keep m = -inf
-        const float mnew = fmaxf(st.m, bm);
-        if (mnew != -INFINITY) {
-            const float alpha = __expf(st.m - mnew);  // st.m = -inf gives 0
-            st.l *= alpha;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const float p = __expf(logit[b] - mnew);  // -inf logit gives 0
-                st.l += p;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) st.acc[i] = fmaf(p, vr[b].get(i), st.acc[i]);
-            }
-            st.m = mnew;
-        }
-    }
+    const SoftmaxState st =
+        attend_rows<T, NB>(qr, kb, vb, n_rows, [&](int r) { return s_tok[r]; }, scale, slot);
+    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
+}
+
+// Dense attention (the reference's full layers, popkv.py:1022-1038): every
+// prefix token attends.  Workgroup (s, h) takes tokens [s*kDenseSplit,
+// (s+1)*kDenseSplit) directly; the current token joins in the merge, as in
+// the layer step.
+constexpr int kDenseSplit = 512;
+
+template <typename T, int NB>
+__global__ __launch_bounds__(kAttnThreads) void attn_dense_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
+    int64_t tokens, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials,
+    int nsplit) {
+    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR;
+    const int h = blockIdx.y;
+    const int s = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int slot = wave * SLOTS + lane / LPR;
+    const int dim0 = (lane % LPR) * 8;
+    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    Raw8<T> qr;
+    qr.load(q + static_cast<int64_t>(h) * D + dim0);
+    const int t0 = s * kDenseSplit;
+    const int n_rows = static_cast<int>(min<int64_t>(kDenseSplit, tokens - t0));
+    const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
+    const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
+    const SoftmaxState st = attend_rows<T, NB>(qr, kb, vb, n_rows, [&](int r) { return t0 + r; }, scale, slot);
     store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
 }
 
@@ -680,4 +721,38 @@ hipError_t launch_merge_current(const float* partials, int nsplit, const void* q
     }
 }
 
+
+namespace {
+template <typename T>
+hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs, int64_t tokens,
+                          int nsplit, const int64_t* h2k, int q_heads, int kv_heads, float* partials,
+                          hipStream_t stream) {
+    constexpr int NB = sizeof(T) == 4 ? 8 : 16;
+    const float scale = static_cast<float>(1.0 / sqrt(128.0));
+    hipLaunchKernelGGL((attn_dense_kernel<T, NB>), dim3(static_cast<unsigned>(nsplit), static_cast<unsigned>(q_heads)),
+                       dim3(kAttnThreads), 0, stream, static_cast<const T*>(q), static_cast<const T*>(kc),
+                       static_cast<const T*>(vc), k_hs, v_hs, tokens, h2k, kv_heads, scale, partials, nsplit);
+    return hipGetLastError();
+}
+}  // namespace
+
+int dense_splits(int64_t tokens) { return static_cast<int>((tokens + kDenseSplit - 1) / kDenseSplit); }
+
+hipError_t launch_attention_dense(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                  int64_t k_head_stride, int64_t v_head_stride, int64_t tokens,
+                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                  hipStream_t stream) {
+    const int ns = dense_splits(tokens);
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_dense_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
+                                         head_to_kv, q_heads, kv_heads, partials, stream);
+        case POPKV_DTYPE_F16:
+            return launch_dense_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
+                                         head_to_kv, q_heads, kv_heads, partials, stream);
+        default:
+            return launch_dense_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
+                                          head_to_kv, q_heads, kv_heads, partials, stream);
+    }
+}
 }  // namespace popkv

@@ -77,6 +77,14 @@ hipError_t launch_attention_ranks(const void* queries, int dtype, const void* pr
                                   const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                   hipStream_t stream);
 
+// Dense attention over every prefix token (head_dim 128, contiguous rows):
+// partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
+int dense_splits(int64_t tokens);
+hipError_t launch_attention_dense(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                  int64_t k_head_stride, int64_t v_head_stride, int64_t tokens,
+                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                  hipStream_t stream);
+
 // Layer-step merge of the split partials plus the current token (head_dim 128).
 hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,
                                 const void* current_k, const void* current_v, const int64_t* head_to_kv, int q_heads,

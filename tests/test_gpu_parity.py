@@ -401,6 +401,51 @@ def test_layer_step_long_context(context):
     _check_layer_step(w, layer, mapping, cache)
 
 
+def test_layer_step_batch_laid_along_heads_equals_per_sequence_steps():
+    """C4's batching: sequences side by side along the head axis (K/V and
+    packed caches [B*KVH, ...], queries [B*QH, D], head i -> KV head i // 4)
+    give exactly the per-sequence results."""
+    w = workloads.scaled(workloads.C1, context=3000, budget=700)
+    seqs = [workloads.make_layer(w, seed=11 + b).to(DEV) for b in range(3)]
+    mapping = workloads.head_to_kv(w, DEV)
+    singles = []
+    for lay in seqs:
+        cache = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                        reserve_tokens=64)
+        singles.append(popkv.popkv_layer_step(lay.queries, cache, lay.prefix_k(), lay.prefix_v(), lay.current_k(),
+                                              lay.current_v(), mapping, budget=w.budget, return_indices=True))
+    keys = torch.cat([x.keys for x in seqs], 0)
+    values = torch.cat([x.values for x in seqs], 0)
+    L = w.prefix_tokens
+    cache = popkv.build_popkv_cache(keys[:, :L], group_size=w.token_group, dim_group_size=w.dim_group,
+                                    reserve_tokens=64)
+    qh = len(seqs) * w.q_heads
+    bmap = torch.arange(qh, device=DEV) // (w.q_heads // w.kv_heads)
+    out, idx = popkv.popkv_layer_step(torch.cat([x.queries for x in seqs], 0), cache, keys[:, :L], values[:, :L],
+                                      keys[:, L].contiguous(), values[:, L].contiguous(), bmap, budget=w.budget,
+                                      return_indices=True)
+    assert torch.equal(idx, torch.cat([i for _, i in singles], 0))
+    assert torch.equal(out, torch.cat([o for o, _ in singles], 0))
+
+
+@pytest.mark.parametrize("context,dtype", [(3000, torch.bfloat16), (700, torch.float32), (1, torch.bfloat16),
+                                           (1537, torch.float16)])
+def test_dense_attention_matches_oracle(context, dtype):
+    """The full layers: every prefix token plus the current one."""
+    base = workloads.scaled(workloads.C1, context=context, budget=2)
+    w = workloads.Workload(base.name, base.method, base.q_heads, base.kv_heads, 128, context, 2, base.token_group,
+                           base.dim_group, dtype, 5, context > 1)
+    lay = workloads.make_layer(w).to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    L = lay.prefix_tokens
+    out = popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v(),
+                                     mapping)
+    idx = np.tile(np.arange(L + 1, dtype=np.int64), (w.q_heads, 1))
+    want = core.attention(f32(lay.queries), f32(lay.prefix_k()), f32(lay.prefix_v()), f32(lay.current_k()),
+                          f32(lay.current_v()), idx, mapping.cpu().numpy())
+    np.testing.assert_allclose(f32(out), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
 def test_retrieval_step_with_torch_topk_hook():
     w = workloads.scaled(workloads.C1, context=3000, budget=512)
     layer, mapping, cache = _layer_setup(w)
