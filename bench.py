@@ -98,20 +98,20 @@ def bench_c2(args) -> int:
         if li not in dense_layers:
             cache = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
                                             reserve_tokens=128)
-        layers.append((w, lay, cache, torch.empty_like(lay.queries)))
+        layers.append((w, lay, cache, torch.empty_like(lay.queries), lay.current_k(), lay.current_v()))
     w0 = layers[0][0]
     mapping = workloads.head_to_kv(w0, dev)
     ws, dws = popkv.LayerStepWorkspace(), popkv.LayerStepWorkspace()
     stream = torch.cuda.current_stream(dev)
 
     def stack_step() -> None:
-        for li, (w, lay, cache, out) in enumerate(layers):
+        for w, lay, cache, out, ck, cv in layers:
             if cache is None:
-                popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(),
-                                           lay.current_v(), mapping, workspace=dws, out=out)
+                popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), ck, cv, workspace=dws,
+                                           out=out)
             else:
-                popkv.popkv_layer_step(lay.queries, cache, lay.prefix_k(), lay.prefix_v(), lay.current_k(),
-                                       lay.current_v(), mapping, budget=w.budget, workspace=ws, out=out)
+                popkv.popkv_layer_step(lay.queries, cache, lay.prefix_k(), lay.prefix_v(), ck, cv, mapping,
+                                       budget=w.budget, workspace=ws, out=out)
 
     for _ in range(max(1, args.warmup // 8)):
         stack_step()

@@ -184,20 +184,21 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype,
 
 /* Dense attention of one decode step over every prefix token plus the
  * current one: out[h] = softmax(q_h . [K_prefix; k_cur] / sqrt(128)) .
- * [V_prefix; v_cur] with KV head head_to_kv[h], written in `dtype` to
- * output [QH, 128].  prefix K/V [KVH, tokens, 128], rows contiguous, any
+ * [V_prefix; v_cur] with the plain GQA grouping (query head h reads KV head
+ * h / (QH / KVH); 1, 2, 4 or 8 query heads per KV head), written in `dtype`
+ * to output [QH, 128].  prefix K/V [KVH, tokens, 128], rows contiguous, any
  * head stride; tokens may be 0.  Needs
  * popkv_dense_attention_workspace_bytes() bytes of 16-byte aligned
  * workspace (no initialisation needed).  Replaces the full-layer branch of
  * LlamaSparseDecoder.decode (reference popkv.py:1022-1038: torch.cat of the
- * prefix and current K/V, then scaled_dot_product_attention). */
+ * prefix and current K/V, then scaled_dot_product_attention on the grouped
+ * view q.view(KVH, QH/KVH, 1, D)). */
 size_t popkv_dense_attention_workspace_bytes(int64_t q_heads, int64_t tokens);
 int popkv_dense_attention(const void* queries, int32_t dtype,
                           const void* prefix_k, const void* prefix_v,
                           int64_t k_head_stride, int64_t v_head_stride,
                           const void* current_k, const void* current_v,
-                          const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
-                          int64_t tokens, void* output,
+                          int64_t q_heads, int64_t kv_heads, int64_t tokens, void* output,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

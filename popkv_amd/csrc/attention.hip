@@ -507,32 +507,93 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
 }
 
 // Dense attention (the reference's full layers, popkv.py:1022-1038): every
-// prefix token attends.  Workgroup (s, h) takes tokens [s*kDenseSplit,
-// (s+1)*kDenseSplit) directly; the current token joins in the merge, as in
-// the layer step.
+// prefix token attends; the current token joins in the merge, as in the
+// layer step.  Splits of kDenseSplit tokens.
 constexpr int kDenseSplit = 512;
 
-template <typename T, int NB>
-__global__ __launch_bounds__(kAttnThreads) void attn_dense_kernel(
+// Dense attention, one GQA group per workgroup: the QPK query heads of KV
+// head g share every K/V row, so workgroup (s, g) reads each row of its
+// 512-token split once and folds it into QPK online-softmax states (one Q.K
+// dot and one V update per head per row).  Memory traffic is one pass over
+// the KV head's rows instead of QPK.
+template <typename T, int NB, int QPK>
+__global__ __launch_bounds__(kAttnThreads) void attn_dense_gqa_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
-    int64_t tokens, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials,
-    int nsplit) {
-    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR;
-    const int h = blockIdx.y;
+    int64_t tokens, float scale, float* __restrict__ partials, int nsplit) {
+    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, ROWS_PER_PASS = SLOTS * kAttnWaves;
+    const int g = blockIdx.y;
     const int s = blockIdx.x;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int slot = wave * SLOTS + lane / LPR;
     const int dim0 = (lane % LPR) * 8;
-    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
-    Raw8<T> qr;
-    qr.load(q + static_cast<int64_t>(h) * D + dim0);
+    Raw8<T> qr[QPK];
+#pragma unroll
+    for (int j = 0; j < QPK; ++j) qr[j].load(q + static_cast<int64_t>(g * QPK + j) * D + dim0);
     const int t0 = s * kDenseSplit;
     const int n_rows = static_cast<int>(min<int64_t>(kDenseSplit, tokens - t0));
-    const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
-    const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
-    const SoftmaxState st = attend_rows<T, NB>(qr, kb, vb, n_rows, [&](int r) { return t0 + r; }, scale, slot);
-    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
+    const char* kb = reinterpret_cast<const char*>(kc + g * k_hs) + dim0 * sizeof(T);
+    const char* vb = reinterpret_cast<const char*>(vc + g * v_hs) + dim0 * sizeof(T);
+    SoftmaxState st[QPK];
+#pragma unroll
+    for (int j = 0; j < QPK; ++j) {
+        st[j].m = -INFINITY;
+        st[j].l = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st[j].acc[i] = 0.0f;
+    }
+    for (int base = 0; base < n_rows; base += ROWS_PER_PASS * NB) {
+        Raw8<T> kr[NB], vr[NB];
+        bool live[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int r = base + b * ROWS_PER_PASS + slot;
+            live[b] = r < n_rows;
+            const uint32_t off = static_cast<uint32_t>(t0 + (live[b] ? r : 0)) * (D * sizeof(T));
+            kr[b].load(reinterpret_cast<const T*>(kb + off));
+            vr[b].load(reinterpret_cast<const T*>(vb + off));
+        }
+#pragma unroll
+        for (int j = 0; j < QPK; ++j) {
+            float logit[NB];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                float dot;
+                if constexpr (sizeof(T) == 2) {
+                    dot = dot8<T>(qr[j].u, kr[b].u);
+                } else {
+                    dot = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) dot = fmaf(qr[j].get(i), kr[b].get(i), dot);
+                }
+                dot = row_sum<LPR>(dot);
+                logit[b] = live[b] ? dot * scale : -INFINITY;
+                bm = fmaxf(bm, logit[b]);
+            }
+            const float mnew = fmaxf(st[j].m, bm);
+            if (mnew != -INFINITY) {
+                const float alpha = __expf(st[j].m - mnew);
+                st[j].l *= alpha;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) st[j].acc[i] *= alpha;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const float p = __expf(logit[b] - mnew);
+                    st[j].l += p;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) st[j].acc[i] = fmaf(p, vr[b].get(i), st[j].acc[i]);
+                }
+                st[j].m = mnew;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < QPK; ++j) {
+        store_partial<LPR>(st[j], lane, wave, dim0, D,
+                           partials + (static_cast<int64_t>(g * QPK + j) * nsplit + s) * (D + 2));
+        __syncthreads();  // store_partial's LDS is reused by the next head
+    }
 }
 
 // Layer-step merge: the split states of head h plus the current token
@@ -544,7 +605,10 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_current_kernel(
     T* __restrict__ out) {
     constexpr int D = 128;
     const int h = blockIdx.x;
-    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    // no mapping: the plain GQA grouping of the dense layers
+    const int64_t kvh = head_to_kv != nullptr
+                            ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
+                            : h / (static_cast<int>(gridDim.x) / kv_heads);
     merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (D + 2), nsplit, D, out + static_cast<int64_t>(h) * D,
                     q + static_cast<int64_t>(h) * D, cur_k + kvh * D, cur_v + kvh * D, scale);
 }
@@ -725,13 +789,20 @@ hipError_t launch_merge_current(const float* partials, int nsplit, const void* q
 namespace {
 template <typename T>
 hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs, int64_t tokens,
-                          int nsplit, const int64_t* h2k, int q_heads, int kv_heads, float* partials,
-                          hipStream_t stream) {
-    constexpr int NB = sizeof(T) == 4 ? 8 : 16;
+                          int nsplit, int q_heads, int kv_heads, float* partials, hipStream_t stream) {
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
-    hipLaunchKernelGGL((attn_dense_kernel<T, NB>), dim3(static_cast<unsigned>(nsplit), static_cast<unsigned>(q_heads)),
-                       dim3(kAttnThreads), 0, stream, static_cast<const T*>(q), static_cast<const T*>(kc),
-                       static_cast<const T*>(vc), k_hs, v_hs, tokens, h2k, kv_heads, scale, partials, nsplit);
+    const dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(kv_heads));
+    const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
+#define POPKV_DENSE(NB, QPK)                                                                                   \
+    hipLaunchKernelGGL((attn_dense_gqa_kernel<T, NB, QPK>), grid, dim3(kAttnThreads), 0, stream, q_, k_, v_, k_hs, \
+                       v_hs, tokens, scale, partials, nsplit)
+    switch (q_heads / kv_heads) {
+        case 1: POPKV_DENSE((sizeof(T) == 4 ? 8 : 16), 1); break;
+        case 2: POPKV_DENSE(8, 2); break;
+        case 4: POPKV_DENSE(8, 4); break;
+        default: POPKV_DENSE(4, 8); break;
+    }
+#undef POPKV_DENSE
     return hipGetLastError();
 }
 }  // namespace
@@ -739,20 +810,19 @@ hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t
 int dense_splits(int64_t tokens) { return static_cast<int>((tokens + kDenseSplit - 1) / kDenseSplit); }
 
 hipError_t launch_attention_dense(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
-                                  int64_t k_head_stride, int64_t v_head_stride, int64_t tokens,
-                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                  hipStream_t stream) {
+                                  int64_t k_head_stride, int64_t v_head_stride, int64_t tokens, int q_heads,
+                                  int kv_heads, float* partials, hipStream_t stream) {
     const int ns = dense_splits(tokens);
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_dense_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
-                                         head_to_kv, q_heads, kv_heads, partials, stream);
+                                         q_heads, kv_heads, partials, stream);
         case POPKV_DTYPE_F16:
             return launch_dense_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
-                                         head_to_kv, q_heads, kv_heads, partials, stream);
+                                         q_heads, kv_heads, partials, stream);
         default:
             return launch_dense_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
-                                          head_to_kv, q_heads, kv_heads, partials, stream);
+                                          q_heads, kv_heads, partials, stream);
     }
 }
 }  // namespace popkv

@@ -376,13 +376,16 @@ size_t popkv_dense_attention_workspace_bytes(int64_t q_heads, int64_t tokens) {
 
 int popkv_dense_attention(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
                           int64_t k_head_stride, int64_t v_head_stride, const void* current_k, const void* current_v,
-                          const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads, int64_t tokens, void* output,
-                          void* workspace, size_t workspace_bytes, void* stream) {
-    if (!queries || !current_k || !current_v || !head_to_kv || !output || !workspace ||
-        (tokens > 0 && (!prefix_k || !prefix_v)))
+                          int64_t q_heads, int64_t kv_heads, int64_t tokens, void* output, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    if (!queries || !current_k || !current_v || !output || !workspace || (tokens > 0 && (!prefix_k || !prefix_v)))
         return fail(POPKV_ERR_INVALID, "null pointer");
     if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "tensors must be fp32/fp16/bf16");
-    if (q_heads <= 0 || kv_heads <= 0 || q_heads > 65535) return fail(POPKV_ERR_INVALID, "empty or too many heads");
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads > 65535 || kv_heads > 65535)
+        return fail(POPKV_ERR_INVALID, "empty or too many heads");
+    const int64_t group = q_heads / kv_heads;
+    if (q_heads % kv_heads != 0 || (group != 1 && group != 2 && group != 4 && group != 8))
+        return fail(POPKV_ERR_UNSUPPORTED, "dense attention supports 1, 2, 4 or 8 query heads per KV head");
     if (tokens < 0 || tokens > (int64_t{1} << 31) / 256) return fail(POPKV_ERR_TOKENS, "invalid token count");
     if (workspace_bytes < popkv_dense_attention_workspace_bytes(q_heads, tokens))
         return fail(POPKV_ERR_WORKSPACE, "dense attention needs %zu workspace bytes",
@@ -396,13 +399,12 @@ int popkv_dense_attention(const void* queries, int32_t dtype, const void* prefix
     const int ns = popkv::dense_splits(tokens);
     if (ns > 0) {
         const int st = launched(popkv::launch_attention_dense(queries, dtype, prefix_k, prefix_v, k_head_stride,
-                                                              v_head_stride, tokens, head_to_kv,
-                                                              static_cast<int>(q_heads), static_cast<int>(kv_heads),
-                                                              partials, s),
+                                                              v_head_stride, tokens, static_cast<int>(q_heads),
+                                                              static_cast<int>(kv_heads), partials, s),
                                 "popkv_dense_attention(attention)");
         if (st) return st;
     }
-    return launched(popkv::launch_merge_current(partials, ns, queries, dtype, current_k, current_v, head_to_kv,
+    return launched(popkv::launch_merge_current(partials, ns, queries, dtype, current_k, current_v, nullptr,
                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads), output, s),
                     "popkv_dense_attention(merge)");
 }

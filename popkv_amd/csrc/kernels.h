@@ -79,11 +79,12 @@ hipError_t launch_attention_ranks(const void* queries, int dtype, const void* pr
 
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
+// Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one
+// workgroup serves a whole group.
 int dense_splits(int64_t tokens);
 hipError_t launch_attention_dense(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
-                                  int64_t k_head_stride, int64_t v_head_stride, int64_t tokens,
-                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                  hipStream_t stream);
+                                  int64_t k_head_stride, int64_t v_head_stride, int64_t tokens, int q_heads,
+                                  int kv_heads, float* partials, hipStream_t stream);
 
 // Layer-step merge of the split partials plus the current token (head_dim 128).
 hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,

@@ -343,13 +343,14 @@ def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v
 
 
 def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor, k: torch.Tensor,
-                         v: torch.Tensor, head_to_kv: torch.Tensor, *,
-                         workspace: LayerStepWorkspace | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                         v: torch.Tensor, *, workspace: LayerStepWorkspace | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
     """Full attention of one decode step over every prefix token plus the
     current one (the reference's full layers, popkv.py:1022-1038), one C-ABI
     call: q [QH, 128], prefix K/V [KVH, L, 128] with contiguous rows, current
-    k/v [KVH, 128] -> [QH, 128].  The workspace holds split partials; do not
-    share it with popkv_layer_step, whose histogram region must stay zero."""
+    k/v [KVH, 128] -> [QH, 128], query head h reading KV head h // (QH/KVH).
+    The workspace holds split partials; do not share it with
+    popkv_layer_step, whose histogram region must stay zero."""
     if q.ndim != 2 or int(q.shape[1]) != 128:
         raise ValueError("dense_attention_step requires q [query heads, 128]")
     if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
@@ -361,13 +362,11 @@ def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torc
     if any(t.dtype != q.dtype for t in (prefix_k, prefix_v, kc, vc)):
         raise RuntimeError("queries, current K/V and prefix K/V must share a dtype")
     q_heads, kv_heads, tokens = int(q.shape[0]), int(prefix_k.shape[0]), int(prefix_k.shape[1])
-    mapping = head_to_kv.to(device=dev, dtype=torch.int64).contiguous()
     nbytes = int(nat.lib().popkv_dense_attention_workspace_bytes(q_heads, tokens))
     ws = (workspace or LayerStepWorkspace()).get(nbytes, dev)
     output = torch.empty_like(qc) if out is None else out
     with torch.cuda.device(dev):
         nat.call("popkv_dense_attention", qc.data_ptr(), nat.dtype_code(qc), prefix_k.data_ptr(), prefix_v.data_ptr(),
-                 prefix_k.stride(0), prefix_v.stride(0), kc.data_ptr(), vc.data_ptr(), mapping.data_ptr(), q_heads,
-                 kv_heads, tokens, output.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_of(dev))
+                 prefix_k.stride(0), prefix_v.stride(0), kc.data_ptr(), vc.data_ptr(), q_heads, kv_heads, tokens,
+                 output.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_of(dev))
     return output
-

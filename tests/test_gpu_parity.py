@@ -438,8 +438,7 @@ def test_dense_attention_matches_oracle(context, dtype):
     lay = workloads.make_layer(w).to(DEV)
     mapping = workloads.head_to_kv(w, DEV)
     L = lay.prefix_tokens
-    out = popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v(),
-                                     mapping)
+    out = popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v())
     idx = np.tile(np.arange(L + 1, dtype=np.int64), (w.q_heads, 1))
     want = core.attention(f32(lay.queries), f32(lay.prefix_k()), f32(lay.prefix_v()), f32(lay.current_k()),
                           f32(lay.current_v()), idx, mapping.cpu().numpy())
