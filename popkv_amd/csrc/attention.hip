@@ -118,7 +118,7 @@ template <typename T>
 __device__ __forceinline__ void merge_splits(const float* __restrict__ st, int nsplit, int d, T* out,
                                              const T* cur_q = nullptr, const T* cur_k = nullptr,
                                              const T* cur_v = nullptr, float scale = 0.0f) {
-    __shared__ float s_state[kMergeMaxFloats];
+    __shared__ __align__(16) float s_state[kMergeMaxFloats];
     __shared__ float s_w[kMergeMaxSplits];
     __shared__ float s_den, s_wc;
     __shared__ float s_dot[kMergeThreads / kWave];
@@ -133,7 +133,26 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ st, int n
         ck = Elem<T>::load(cur_k, tid);
         cv = Elem<T>::load(cur_v, tid);
     }
-    if (staged) {
+    if (staged && n % 4 == 0 && reinterpret_cast<uintptr_t>(st) % 16 == 0) {
+        // 16-byte loads, kMergeBatch of them in flight per thread before the
+        // first LDS write (a plain copy loop waits on every load)
+        const float4* st4 = reinterpret_cast<const float4*>(st);
+        float4* sh4 = reinterpret_cast<float4*>(s_state);
+        const int n4 = n / 4;
+        for (int base = 0; base < n4; base += kMergeBatch * kMergeThreads) {
+            float4 v[kMergeBatch];
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const int i = base + j * kMergeThreads + tid;
+                v[j] = i < n4 ? st4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const int i = base + j * kMergeThreads + tid;
+                if (i < n4) sh4[i] = v[j];
+            }
+        }
+    } else if (staged) {
         // Batches of kMergeBatch independent loads per thread, all in flight
         // before the first LDS write (a plain copy loop waits on every load).
         for (int base = 0; base < n; base += kMergeBatch * kMergeThreads) {
@@ -362,7 +381,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
 // to LDS.  The current token is not in the mask; the merge adds it.  Rows are
 // contiguous (token stride = head_dim = 128).  For 16-bit types the Q.K
 // products use v_dot2 (two products accumulated in fp32 per instruction).
-constexpr int kSplitRows = 256;
+constexpr int kSplitRows = 256;  // selected tokens per workgroup
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -442,7 +461,7 @@ __device__ __forceinline__ SoftmaxState attend_rows(const Raw8<T>& qr, const cha
     return st;
 }
 
-template <typename T, int NB, int WPT>
+template <typename T, int NB, int WPT, int SPLIT = kSplitRows>
 __global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint32_t* __restrict__ mask, int64_t mask_stride, int64_t tokens, int64_t k,
@@ -477,15 +496,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
 
     // tokens of ranks [r0, r1) in ascending order -> s_tok
-    __shared__ int32_t s_tok[kSplitRows];
+    __shared__ int32_t s_tok[SPLIT];
     __shared__ uint32_t s_scan[kAttnWaves + 1];
     uint32_t cnt = 0;
 #pragma unroll
     for (int i = 0; i < WPT; ++i) cnt += __popc(mw[i]);
     uint32_t total;
     uint32_t rank = block_excl_scan_once(cnt, s_scan, kAttnWaves, &total);
-    const uint32_t r0 = static_cast<uint32_t>(s) * kSplitRows;
-    const uint32_t r1 = min(r0 + kSplitRows, static_cast<uint32_t>(k));
+    const uint32_t r0 = static_cast<uint32_t>(s) * SPLIT;
+    const uint32_t r1 = min(r0 + SPLIT, static_cast<uint32_t>(k));
     if (rank < r1 && rank + cnt > r0) {
 #pragma unroll
         for (int i = 0; i < WPT; ++i) {
@@ -724,7 +743,7 @@ template <typename T>
 hipError_t launch_rank_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs,
                          const uint32_t* mask, int64_t mask_stride, int64_t tokens, int64_t k, int nsplit,
                          const int64_t* h2k, int q_heads, int kv_heads, float* partials, hipStream_t stream) {
-    constexpr int NB = sizeof(T) == 4 ? 8 : 16;
+    constexpr int NB = 8;  // 8 rows in flight per lane: two passes cover a 256-row split
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(q_heads));
     const int64_t words = (tokens + 31) / 32;

@@ -40,7 +40,7 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 constexpr int64_t kMaxSelectTokens = 1024 * 128;
 constexpr int64_t kMaxGroupHeads = 64;
-constexpr int kLayerSplit = 256;
+constexpr int kLayerSplit = 256;  // selected tokens per attention workgroup
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
