@@ -171,7 +171,7 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Re-runs only the sparse-attention kernel of the last popkv_layer_step that
- * used `workspace` (same shapes and budget): it reads the selection masks the
+ * used `workspace` (same shapes and budget): it reads the selection lists the
  * step left there and rewrites the split partials, touching nothing else, so
  * it can be repeated.  For timing the step's dominant kernel on its own; no
  * counterpart in the reference. */

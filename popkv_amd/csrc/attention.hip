@@ -371,16 +371,16 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
 
 // ---------------------------------------------------------------- layer step
 
-// Layer-step attention.  The select kernel leaves each head's selection as a
-// bit mask over the prefix tokens (bit t of word t/32).  Workgroup (s, h)
-// takes the selected tokens of ranks [256s, 256s + 256) in ascending token
-// order -- the reference's 256-token split -- so every workgroup gathers the
-// same number of rows: it loads the head's whole mask (4 KB at 32K tokens),
-// one block scan of per-thread popcounts gives every mask word its first
-// rank, and the threads whose words hold the split's ranks write those tokens
-// to LDS.  The current token is not in the mask; the merge adds it.  Rows are
-// contiguous (token stride = head_dim = 128).  For 16-bit types the Q.K
-// products use v_dot2 (two products accumulated in fp32 per instruction).
+// Layer-step attention.  The select kernel leaves each head's k selected
+// tokens as an ascending int32 list.  Workgroup (s, h) takes list entries
+// [256s, 256s + 256) -- the reference's 256-token split -- so every
+// workgroup gathers the same number of rows.  Row slot q (16 lanes, one
+// 16-byte slice of a 256-byte row each) owns the 16 consecutive entries
+// [16q, 16q + 16) of the split and reads them with four 16-byte loads, so the
+// first gathers wait on a single short load.  The current token is not in
+// the list; the merge adds it.  Rows are contiguous (token stride = head_dim
+// = 128).  For 16-bit types the Q.K products use v_dot2 (two products
+// accumulated in fp32 per instruction).
 constexpr int kSplitRows = 256;  // selected tokens per workgroup
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -399,129 +399,107 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
     return d2(a.w, b.w, d2(a.z, b.z, d2(a.y, b.y, d2(a.x, b.x, 0.0f))));
 }
 
-// Gathers rows tok_of(0 .. n_rows-1) of K/V (head_dim 128, 16 lanes per
-// 256-byte row, NB rows in flight per lane) and folds them into the lane's
-// online-softmax state.  kb / vb point at this lane's 8-element slice of row
-// 0.  An idle slot re-reads row tok_of(0) (its weight is exactly 0), so no
-// row outside the list is touched.
-template <typename T, int NB, typename TokOf>
-__device__ __forceinline__ SoftmaxState attend_rows(const Raw8<T>& qr, const char* kb, const char* vb, int n_rows,
-                                                    TokOf tok_of, float scale, int slot) {
-    constexpr int D = 128, LPR = 16, ROWS_PER_PASS = (kWave / LPR) * kAttnWaves;
-    SoftmaxState st;
+__device__ __forceinline__ void init_state(SoftmaxState& st) {
     st.m = -INFINITY;
     st.l = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) st.acc[i] = 0.0f;
-    for (int base = 0; base < n_rows; base += ROWS_PER_PASS * NB) {
-        Raw8<T> kr[NB], vr[NB];
-        bool live[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int r = base + b * ROWS_PER_PASS + slot;
-            live[b] = r < n_rows;
-            const uint32_t off = static_cast<uint32_t>(tok_of(live[b] ? r : 0)) * (D * sizeof(T));
-            kr[b].load(reinterpret_cast<const T*>(kb + off));
-            vr[b].load(reinterpret_cast<const T*>(vb + off));
-        }
-        float logit[NB];
-        float bm = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float dot;
-            if constexpr (sizeof(T) == 2) {
-                dot = dot8<T>(qr.u, kr[b].u);
-            } else {
-                dot = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) dot = fmaf(qr.get(i), kr[b].get(i), dot);
-            }
-            dot = row_sum<LPR>(dot);
-            logit[b] = live[b] ? dot * scale : -INFINITY;
-            bm = fmaxf(bm, logit[b]);
-        }
-        // every slot has at least its first row live in a non-empty pass, so
-        // bm is finite wherever live[0]; fully idle slots keep m = -inf
-        const float mnew = fmaxf(st.m, bm);
-        if (mnew != -INFINITY) {
-            const float alpha = __expf(st.m - mnew);  // st.m = -inf gives 0
-            st.l *= alpha;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const float p = __expf(logit[b] - mnew);  // -inf logit gives 0
-                st.l += p;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) st.acc[i] = fmaf(p, vr[b].get(i), st.acc[i]);
-            }
-            st.m = mnew;
-        }
-    }
-    return st;
 }
 
-template <typename T, int NB, int WPT, int SPLIT = kSplitRows>
-__global__ __launch_bounds__(kAttnThreads) void attn_rank_kernel(
+// Folds NB gathered rows (this lane's 8-element slices of K and V; the 16
+// lanes of a row slot hold one row) into the lane's online-softmax state.
+// Rows with live[b] false get weight exactly 0.
+template <typename T, int NB>
+__device__ __forceinline__ void fold_rows(SoftmaxState& st, const Raw8<T>& qr, const Raw8<T> (&kr)[NB],
+                                          const Raw8<T> (&vr)[NB], const bool (&live)[NB], float scale) {
+    float logit[NB];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        float dot;
+        if constexpr (sizeof(T) == 2) {
+            dot = dot8<T>(qr.u, kr[b].u);
+        } else {
+            dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dot = fmaf(qr.get(i), kr[b].get(i), dot);
+        }
+        dot = row_sum<16>(dot);
+        logit[b] = live[b] ? dot * scale : -INFINITY;
+        bm = fmaxf(bm, logit[b]);
+    }
+    const float mnew = fmaxf(st.m, bm);
+    if (mnew != -INFINITY) {
+        const float alpha = __expf(st.m - mnew);  // st.m = -inf gives 0
+        st.l *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float p = __expf(logit[b] - mnew);  // -inf logit gives 0
+            st.l += p;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st.acc[i] = fmaf(p, vr[b].get(i), st.acc[i]);
+        }
+        st.m = mnew;
+    }
+}
+
+template <typename T, int NB, int SPLIT = kSplitRows>
+__global__ __launch_bounds__(kAttnThreads) void attn_list_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
-    const uint32_t* __restrict__ mask, int64_t mask_stride, int64_t tokens, int64_t k,
+    const int32_t* __restrict__ list, int64_t list_stride, int64_t tokens, int64_t k,
     const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials, int nsplit) {
-    static_assert(WPT % 4 == 0, "mask words are read as 16-byte packets");
-    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR;
+    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
+    constexpr int RPS = SPLIT / NSLOT;  // list entries per row slot
+    static_assert(RPS % 4 == 0 && RPS % NB == 0, "a slot's entries are read as 16-byte packets, NB per pass");
     const int h = blockIdx.y;
     const int s = blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const int sub = lane % LPR;
     const int slot = wave * SLOTS + lane / LPR;
-    const int dim0 = sub * 8;
+    const int dim0 = (lane % LPR) * 8;
     const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
 
-    // this thread's WPT consecutive mask words, then the query slice
-    const int nwords = static_cast<int>((tokens + 31) / 32);
-    const uint32_t* mrow = mask + static_cast<int64_t>(h) * mask_stride;
-    uint32_t mw[WPT];
+    // this slot's list entries first (the gathers depend on them), then the
+    // query slice
+    const int n_rows = static_cast<int>(min<int64_t>(SPLIT, k - static_cast<int64_t>(s) * SPLIT));
+    const int32_t* lrow = list + static_cast<int64_t>(h) * list_stride + static_cast<int64_t>(s) * SPLIT + slot * RPS;
+    int32_t tk[RPS];
 #pragma unroll
-    for (int i = 0; i < WPT; i += 4) {
-        const int e = tid * WPT + i;
-        uint4 u = make_uint4(0u, 0u, 0u, 0u);
-        if (e < nwords) u = *reinterpret_cast<const uint4*>(mrow + e);  // rows padded to 4 words
-        mw[i] = u.x;
-        mw[i + 1] = e + 1 < nwords ? u.y : 0u;
-        mw[i + 2] = e + 2 < nwords ? u.z : 0u;
-        mw[i + 3] = e + 3 < nwords ? u.w : 0u;
+    for (int i = 0; i < RPS; i += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(lrow + i);
+        tk[i] = v.x;
+        tk[i + 1] = v.y;
+        tk[i + 2] = v.z;
+        tk[i + 3] = v.w;
     }
     Raw8<T> qr;
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
-
-    // tokens of ranks [r0, r1) in ascending order -> s_tok
-    __shared__ int32_t s_tok[SPLIT];
-    __shared__ uint32_t s_scan[kAttnWaves + 1];
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int i = 0; i < WPT; ++i) cnt += __popc(mw[i]);
-    uint32_t total;
-    uint32_t rank = block_excl_scan_once(cnt, s_scan, kAttnWaves, &total);
-    const uint32_t r0 = static_cast<uint32_t>(s) * SPLIT;
-    const uint32_t r1 = min(r0 + SPLIT, static_cast<uint32_t>(k));
-    if (rank < r1 && rank + cnt > r0) {
-#pragma unroll
-        for (int i = 0; i < WPT; ++i) {
-            const int32_t tbase = (tid * WPT + i) * 32;
-            for (uint32_t m = mw[i]; m; m &= m - 1) {
-                if (rank >= r0 && rank < r1) s_tok[rank - r0] = tbase + __builtin_ctz(m);
-                ++rank;
-            }
-        }
-    }
-    __syncthreads();
-    const int n_rows = static_cast<int>(r1 - r0);
-
     const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
     const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
-    const SoftmaxState st =
-        attend_rows<T, NB>(qr, kb, vb, n_rows, [&](int r) { return s_tok[r]; }, scale, slot);
+    // entries past the split's rows are never dereferenced: their slot reads
+    // token 0 with weight 0; list values are clamped into the cache
+    const uint32_t tmax = static_cast<uint32_t>(tokens - 1);
+
+    SoftmaxState st;
+    init_state(st);
+#pragma unroll
+    for (int p = 0; p < RPS / NB; ++p) {
+        Raw8<T> kr[NB], vr[NB];
+        bool live[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int j = p * NB + b;
+            live[b] = slot * RPS + j < n_rows;
+            const uint32_t t = live[b] ? min(static_cast<uint32_t>(tk[j]), tmax) : 0u;
+            const uint32_t off = t * (D * sizeof(T));
+            kr[b].load(reinterpret_cast<const T*>(kb + off));
+            vr[b].load(reinterpret_cast<const T*>(vb + off));
+        }
+        fold_rows<T, NB>(st, qr, kr, vr, live, scale);
+    }
     store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
 }
 
@@ -555,12 +533,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_gqa_kernel(
     const char* vb = reinterpret_cast<const char*>(vc + g * v_hs) + dim0 * sizeof(T);
     SoftmaxState st[QPK];
 #pragma unroll
-    for (int j = 0; j < QPK; ++j) {
-        st[j].m = -INFINITY;
-        st[j].l = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) st[j].acc[i] = 0.0f;
-    }
+    for (int j = 0; j < QPK; ++j) init_state(st[j]);
     for (int base = 0; base < n_rows; base += ROWS_PER_PASS * NB) {
         Raw8<T> kr[NB], vr[NB];
         bool live[NB];
@@ -573,39 +546,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_gqa_kernel(
             vr[b].load(reinterpret_cast<const T*>(vb + off));
         }
 #pragma unroll
-        for (int j = 0; j < QPK; ++j) {
-            float logit[NB];
-            float bm = -INFINITY;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                float dot;
-                if constexpr (sizeof(T) == 2) {
-                    dot = dot8<T>(qr[j].u, kr[b].u);
-                } else {
-                    dot = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) dot = fmaf(qr[j].get(i), kr[b].get(i), dot);
-                }
-                dot = row_sum<LPR>(dot);
-                logit[b] = live[b] ? dot * scale : -INFINITY;
-                bm = fmaxf(bm, logit[b]);
-            }
-            const float mnew = fmaxf(st[j].m, bm);
-            if (mnew != -INFINITY) {
-                const float alpha = __expf(st[j].m - mnew);
-                st[j].l *= alpha;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) st[j].acc[i] *= alpha;
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const float p = __expf(logit[b] - mnew);
-                    st[j].l += p;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) st[j].acc[i] = fmaf(p, vr[b].get(i), st[j].acc[i]);
-                }
-                st[j].m = mnew;
-            }
-        }
+        for (int j = 0; j < QPK; ++j) fold_rows<T, NB>(st[j], qr[j], kr, vr, live, scale);
     }
 #pragma unroll
     for (int j = 0; j < QPK; ++j) {
@@ -740,21 +681,15 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
 
 namespace {
 template <typename T>
-hipError_t launch_rank_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs,
-                         const uint32_t* mask, int64_t mask_stride, int64_t tokens, int64_t k, int nsplit,
+hipError_t launch_list_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs,
+                         const int32_t* list, int64_t list_stride, int64_t tokens, int64_t k, int nsplit,
                          const int64_t* h2k, int q_heads, int kv_heads, float* partials, hipStream_t stream) {
-    constexpr int NB = 8;  // 8 rows in flight per lane: two passes cover a 256-row split
+    constexpr int NB = 8;  // 8 rows in flight per lane: two passes cover a slot's 16 entries
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(q_heads));
-    const int64_t words = (tokens + 31) / 32;
-#define POPKV_RANK(W)                                                                                               \
-    hipLaunchKernelGGL((attn_rank_kernel<T, NB, W>), grid, dim3(kAttnThreads), 0, stream, static_cast<const T*>(q), \
-                       static_cast<const T*>(kc), static_cast<const T*>(vc), k_hs, v_hs, mask, mask_stride, tokens, \
-                       k, h2k, kv_heads, scale, partials, nsplit)
-    if (words <= 4 * kAttnThreads) POPKV_RANK(4);
-    else if (words <= 8 * kAttnThreads) POPKV_RANK(8);
-    else POPKV_RANK(16);
-#undef POPKV_RANK
+    hipLaunchKernelGGL((attn_list_kernel<T, NB>), grid, dim3(kAttnThreads), 0, stream, static_cast<const T*>(q),
+                       static_cast<const T*>(kc), static_cast<const T*>(vc), k_hs, v_hs, list, list_stride, tokens, k,
+                       h2k, kv_heads, scale, partials, nsplit);
     return hipGetLastError();
 }
 
@@ -770,20 +705,21 @@ hipError_t launch_merge_current_t(const float* partials, int nsplit, const void*
 }
 }  // namespace
 
-hipError_t launch_attention_ranks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
-                                  int64_t k_head_stride, int64_t v_head_stride, const uint32_t* mask,
-                                  int64_t mask_stride, int64_t tokens, int64_t k, int nsplit,
-                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                  hipStream_t stream) {
+hipError_t launch_attention_list(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                 int64_t k_head_stride, int64_t v_head_stride, const int32_t* list,
+                                 int64_t list_stride, int64_t tokens, int64_t k, int nsplit,
+                                 const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                 hipStream_t stream) {
+    if (nsplit <= 0 || q_heads <= 0) return hipSuccess;
     switch (dtype) {
         case POPKV_DTYPE_F32:
-            return launch_rank_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, mask, mask_stride,
+            return launch_list_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, list, list_stride,
                                         tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
         case POPKV_DTYPE_F16:
-            return launch_rank_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, mask, mask_stride,
+            return launch_list_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, list, list_stride,
                                         tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
         default:
-            return launch_rank_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, mask, mask_stride,
+            return launch_list_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, list, list_stride,
                                          tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
     }
 }

@@ -47,23 +47,24 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Workspace layout of popkv_layer_step (batch 1, head_dim 128).
 struct StepLayout {
-    size_t hist, scores, mask, partials, total;
-    int64_t score_stride, mask_stride, k, nsplit;
+    size_t hist, scores, list, partials, total;
+    int64_t score_stride, list_stride, k, nsplit;
 };
 
 // Layer-step workspace: [QH][256] u32 key histograms | [QH][score_stride] u16
-// order keys | [QH][mask_stride] u32 selection masks | [QH][nsplit][130] f32
-// split partials (256 selected tokens per split, the reference's split size).
+// order keys | [QH][list_stride] i32 ascending selection lists |
+// [QH][nsplit][130] f32 split partials (256 selected tokens per split, the
+// reference's split size).
 StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     StepLayout L{};
     L.k = budget - 1 < tokens ? budget - 1 : tokens;
     L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 128) * 128;
-    L.mask_stride = L.score_stride / 32;  // a multiple of 4 words
     L.nsplit = ceil_div(L.k, kLayerSplit);
+    L.list_stride = (L.nsplit > 0 ? L.nsplit : 1) * kLayerSplit;  // whole splits: 16-byte loads stay in the row
     size_t off = 0;
     L.hist = off; off = align_up(off + static_cast<size_t>(qh) * 256 * 4);
     L.scores = off; off = align_up(off + static_cast<size_t>(qh * L.score_stride) * 2);
-    L.mask = off; off = align_up(off + static_cast<size_t>(qh * L.mask_stride) * 4);
+    L.list = off; off = align_up(off + static_cast<size_t>(qh * L.list_stride) * 4);
     L.partials = off; off = align_up(off + static_cast<size_t>(qh * (L.nsplit > 0 ? L.nsplit : 1) * (128 + 2)) * 4);
     L.total = off;
     return L;
@@ -306,7 +307,7 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
     char* ws = static_cast<char*>(workspace);
     uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
-    uint32_t* mask = reinterpret_cast<uint32_t*>(ws + L.mask);
+    int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
     hipStream_t s = as_stream(stream);
 
@@ -319,21 +320,18 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
                                                tokens, dim_group_size, keys, L.score_stride, hist, s),
                   "popkv_layer_step(score)");
     if (st) return st;
-    // 2. top-k as a selection bit mask per head (re-zeroes the histograms)
-    st = launched(popkv::launch_topk_mask(keys, hist, q_heads, L.score_stride, tokens, L.k, mask, L.mask_stride, s),
+    // 2. top-k as an ascending token list per head (re-zeroes the
+    //    histograms), also written as int64 with the current token in slot k
+    //    when indices_out is given
+    st = launched(popkv::launch_topk_list(keys, hist, q_heads, L.score_stride, tokens, L.k, list, L.list_stride,
+                                          indices_out, L.k + 1, tokens, s),
                   "popkv_layer_step(select)");
     if (st) return st;
-    if (indices_out) {
-        st = launched(popkv::launch_mask_to_indices(mask, q_heads, L.mask_stride, tokens, L.k, tokens, indices_out,
-                                                    L.k + 1, s),
-                      "popkv_layer_step(indices)");
-        if (st) return st;
-    }
-    // 3. sparse attention over 256-token rank splits of each head's selection,
+    // 3. sparse attention over 256-token splits of each head's list,
     // 4. log-sum-exp merge of the splits and the current token
-    st = launched(popkv::launch_attention_ranks(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride, mask,
-                                                L.mask_stride, tokens, L.k, static_cast<int>(L.nsplit), head_to_kv,
-                                                static_cast<int>(q_heads), static_cast<int>(kv_heads), partials, s),
+    st = launched(popkv::launch_attention_list(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride, list,
+                                               L.list_stride, tokens, L.k, static_cast<int>(L.nsplit), head_to_kv,
+                                               static_cast<int>(q_heads), static_cast<int>(kv_heads), partials, s),
                   "popkv_layer_step(attention)");
     if (st) return st;
     st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nsplit), queries, dtype, current_k,
@@ -360,11 +358,11 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* p
         (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
         return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
     char* ws = static_cast<char*>(workspace);
-    return launched(popkv::launch_attention_ranks(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride,
-                                                  reinterpret_cast<const uint32_t*>(ws + L.mask), L.mask_stride,
-                                                  tokens, L.k, static_cast<int>(L.nsplit), head_to_kv,
-                                                  static_cast<int>(q_heads), static_cast<int>(kv_heads),
-                                                  reinterpret_cast<float*>(ws + L.partials), as_stream(stream)),
+    return launched(popkv::launch_attention_list(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride,
+                                                 reinterpret_cast<const int32_t*>(ws + L.list), L.list_stride, tokens,
+                                                 L.k, static_cast<int>(L.nsplit), head_to_kv,
+                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                                                 reinterpret_cast<float*>(ws + L.partials), as_stream(stream)),
                     "popkv_layer_step_attention");
 }
 

@@ -46,15 +46,13 @@ hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_
                               int64_t index_row_stride, hipStream_t stream);
 
 // Layer-step select over radix order keys with the high-byte histograms
-// ghist[row][256] the scorer built: writes each row's selection as a bit mask
-// (ceil(tokens/64) 64-bit words, mask_stride 32-bit words per row, 8-byte
-// aligned) and re-zeroes ghist.  tokens <= 131072.
-hipError_t launch_topk_mask(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
-                            int64_t k, uint32_t* mask, int64_t mask_stride, hipStream_t stream);
-
-// Ascending int64 indices of a selection mask with `current` in slot k.
-hipError_t launch_mask_to_indices(const uint32_t* mask, int64_t rows, int64_t mask_stride, int64_t tokens, int64_t k,
-                                  int64_t current, int64_t* indices, int64_t index_row_stride, hipStream_t stream);
+// ghist[row][256] the scorer built: writes each row's k selected tokens in
+// ascending order to list[row][0..k) (int32) and, with idx64 non-null, to
+// idx64[row][0..k) as int64 with `current` in slot k; re-zeroes ghist.
+// tokens <= 131072.
+hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
+                            int64_t k, int32_t* list, int64_t list_stride, int64_t* idx64, int64_t idx_stride,
+                            int64_t current, hipStream_t stream);
 
 hipError_t launch_attention_partial(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                     int64_t k_head_stride, int64_t k_token_stride, int64_t v_head_stride,
@@ -68,14 +66,14 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
                                   void* output, int out_dtype, hipStream_t stream);
 
 // Layer-step attention (head_dim 128, contiguous rows): workgroup (s, h)
-// attends over the selected tokens of ranks [256s, 256s + 256) of head h's
-// mask (rows padded to a multiple of 4 words, tokens <= 131072) and writes
-// partials[h][s][130].
-hipError_t launch_attention_ranks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
-                                  int64_t k_head_stride, int64_t v_head_stride, const uint32_t* mask,
-                                  int64_t mask_stride, int64_t tokens, int64_t k, int nsplit,
-                                  const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                  hipStream_t stream);
+// attends over entries [256s, 256s + 256) of head h's ascending selection
+// list (rows of list_stride >= 256 * nsplit int32 entries, 16-byte aligned;
+// entries past k are never dereferenced) and writes partials[h][s][130].
+hipError_t launch_attention_list(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                 int64_t k_head_stride, int64_t v_head_stride, const int32_t* list,
+                                 int64_t list_stride, int64_t tokens, int64_t k, int nsplit,
+                                 const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                 hipStream_t stream);
 
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.

@@ -200,220 +200,184 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
     if (tid == 0) dst[k] = static_cast<IdxT>(current);
 }
 
-// Layer-step select, bit-mask form.  The input rows hold radix order keys and
+// Layer-step select, list form.  The input rows hold radix order keys and
 // the scorer has accumulated each row's high-byte histogram into ghist, so
-// the first radix level costs nothing here.  Thread t of the block handles
-// tokens t, t + 1024, t + 2048, ...: round j of a wave covers 64 consecutive
-// tokens, so one ballot of a comparison is directly that 64-token word of the
-// selection mask, and lane j of the wave collects round j's words for one
-// store at the end.
-//   1. bin b1 of the k-th largest key from ghist;
+// the first radix level costs nothing here.  One 1024-thread workgroup per
+// row; thread t owns the SEG consecutive tokens [t*SEG, t*SEG + SEG), read
+// with 16-byte loads and kept packed two keys per register.
+//   1. bin b1 of the k-th largest key from ghist (one wave);
 //   2. 256-bin histogram of the low byte of the keys with high byte b1 ->
-//      the k-th largest key T, need_eq = how many keys equal to T are taken;
-//   3. one pass builds, per 64-token word, the bits of keys > T and of keys
-//      == T.  If some keys equal to T are left out, the last one taken is the
-//      need_eq-th in token order (PyTorch's gather-top-k tie rule: the lowest
-//      indices win): the tie words go to LDS, one wave scans their
-//      popcounts, finds the word holding that tie and, one lane per bit,
-//      the token tau;
-//   4. mask word = (key > T bits) | (key == T bits of tokens <= tau).
-// Absent tokens (past `tokens`) get key 0, below every real key (real keys
-// are >= 0x03ff; NaN patterns map to 0xffff).  Rows of up to JB rounds keep
-// their keys and words in registers (tokens <= 32768 for JB = 32); longer
-// rows take the MULTI path, which re-reads keys per pass and keeps the words
-// in LDS.  The mask row holds ceil(tokens/64) 64-bit words, bits past
-// `tokens` zero.  ghist is re-zeroed for the next call.
-constexpr int kMaskMaxRounds = 128;                          // tokens <= 131072
-constexpr int kMaskWordSlots = kMaskMaxRounds * kSelWaves;  // 64-bit words per row
-
-template <int JB, bool MULTI>
-__global__ __launch_bounds__(kSelThreads) void topk_mask_kernel(
+//      the k-th largest key T and need_eq = how many keys equal to T are
+//      taken (the lowest-index ties: PyTorch's gather-top-k rule);
+//   3. per thread, bit masks of its keys > T and >= T, two instructions per
+//      key and mask: bit = sign of (T - key) (resp. T - 1 - key), shifted
+//      in with v_alignbit;
+//   4. one block scan of the per-thread (greater, equal) counts: a selected
+//      token's rank = greater tokens before it + min(ties before it,
+//      need_eq); the thread takes the first min(its ties, need_eq - ties
+//      taken before it) of its own ties;
+//   5. the thread writes its selected tokens (set bits of its mask, in
+//      ascending order) to list[rank...].
+// The VALU work per key is a few instructions, which matters: the kernel
+// runs on one CU per row.  The list row receives the k selected tokens in
+// ascending order (int32); with idx64 non-null the same tokens are written
+// as int64 followed by `current` in slot k (the reference's _append_current
+// layout).  Absent tokens (past `tokens`) get key 0, below every real key
+// (real keys are >= 0x03ff; NaN patterns map to 0xffff).  ghist is
+// re-zeroed for the next call.
+template <int SEG>
+__global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
     const uint16_t* __restrict__ keys, uint32_t* __restrict__ ghist, int64_t row_stride, int ntok, int k,
-    uint32_t* __restrict__ mask, int64_t mask_stride) {
-    static_assert(JB <= kWave, "one collecting lane per round");
-    constexpr int SLOTS = MULTI ? kMaskWordSlots : JB * kSelWaves;
+    int32_t* __restrict__ list, int64_t list_stride, int64_t* __restrict__ idx64, int64_t idx_stride,
+    int64_t current) {
+    static_assert(SEG % 8 == 0 && SEG <= 128, "whole 16-byte chunks, at most four 32-bit masks");
+    constexpr int NM = (SEG + 31) / 32;   // 32-bit masks per thread
+    constexpr int MB = SEG < 32 ? SEG : 32;  // bits per mask
     const int64_t row = blockIdx.x;
     const uint16_t* src = keys + row * row_stride;
     uint32_t* gh = ghist + row * kBins;
-    uint32_t* mrow = mask + row * mask_stride;
+    int32_t* lrow = list + row * list_stride;
+    int64_t* irow = idx64 != nullptr ? idx64 + row * idx_stride : nullptr;
     const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
-    const int rounds = (ntok + kSelThreads - 1) / kSelThreads;
 
     __shared__ uint32_t tot[kBins], hist2[kBins];
-    __shared__ uint32_t s_bin, s_above, s_tau;
-    __shared__ uint64_t s_eq[SLOTS];
-    __shared__ uint64_t s_gt[MULTI ? SLOTS : 1];
+    __shared__ uint32_t s_bin, s_above;
+    __shared__ uint32_t scan_a[kSelWaves + 1], scan_b[kSelWaves + 1];
     if (tid < kBins) {
         tot[tid] = gh[tid];
         gh[tid] = 0u;
         hist2[tid] = 0u;
     }
+    if (irow != nullptr && tid == 0) irow[k] = current;
     // mode 0: nothing selected (k == 0); 1: every token (k >= ntok); 2: threshold
     const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);
     if (mode != 2) {
-        for (int j0 = 0; j0 < rounds; j0 += JB) {
-            uint32_t wl = 0, wh = 0;
-#pragma unroll
-            for (int jj = 0; jj < JB; ++jj) {
-                const uint64_t word = mode == 1 ? __ballot((j0 + jj) * kSelThreads + tid < ntok) : 0ull;
-                wl = lane == jj ? static_cast<uint32_t>(word) : wl;
-                wh = lane == jj ? static_cast<uint32_t>(word >> 32) : wh;
+        if (mode == 1) {
+            for (int t = tid; t < ntok; t += kSelThreads) {
+                lrow[t] = t;
+                if (irow != nullptr) irow[t] = t;
             }
-            const int wbase = (j0 + lane) * kSelThreads + wave * kWave;
-            if (lane < JB && wbase < ntok) *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(wl, wh);
         }
         return;
     }
-    uint32_t kr[JB];
-    auto load = [&](int j0) {
+
+    // keys of tokens [begin, begin + n); the rest of the segment reads as 0.
+    // Rows are padded to a multiple of 128 keys, so a chunk that starts
+    // inside the row ends inside it.  Segments of up to 64 keys stay in
+    // registers; longer ones are re-read 32 keys at a time in each pass.
+    constexpr bool RELOAD = SEG > 64;
+    constexpr int KW = RELOAD ? 16 : SEG / 2;  // registers of packed keys
+    const int begin = tid * SEG;
+    const int n = max(0, min(SEG, ntok - begin));
+    uint32_t kp[KW];
+    // chunks [c0, c0 + KW/4) of 8 keys into kp
+    // `after` orders a re-read after the work on the previous keys: an
+    // opaque copy of the row pointer that depends on it keeps the compiler
+    // from issuing every pass's loads at once (which would spill)
+    auto load_keys = [&](int c0, uint32_t after) {
+        const uint16_t* rowp = src;
+        if (RELOAD) asm volatile("" : "+s"(rowp) : "v"(after) : "memory");
+        const uint16_t* seg = rowp + begin;
 #pragma unroll
-        for (int jj = 0; jj < JB; ++jj) {
-            const int t = (j0 + jj) * kSelThreads + tid;
-            const uint32_t v = src[min(t, ntok - 1)];
-            kr[jj] = t < ntok ? v : 0u;
+        for (int c = 0; c < KW / 4; ++c) {
+            const int e0 = 8 * (c0 + c);
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (e0 < n) u = *reinterpret_cast<const uint4*>(seg + e0);
+            if (e0 + 8 > n) {  // the segment's tail: keys e >= n read as 0
+                const int v = n - e0;  // keys of this chunk that exist (may be <= 0)
+                u.x &= (v > 1 ? 0xffffffffu : 0u) | (v > 0 ? 0x0000ffffu : 0u);
+                u.y &= (v > 3 ? 0xffffffffu : 0u) | (v > 2 ? 0x0000ffffu : 0u);
+                u.z &= (v > 5 ? 0xffffffffu : 0u) | (v > 4 ? 0x0000ffffu : 0u);
+                u.w &= (v > 7 ? 0xffffffffu : 0u) | (v > 6 ? 0x0000ffffu : 0u);
+            }
+            kp[4 * c] = u.x;
+            kp[4 * c + 1] = u.y;
+            kp[4 * c + 2] = u.z;
+            kp[4 * c + 3] = u.w;
         }
     };
-    if (!MULTI) load(0);
+#define POPKV_KEY(e) ((kp[(e) >> 1] >> (((e) & 1) * 16)) & 0xffffu)
+    if (!RELOAD) load_keys(0, 0u);
     __syncthreads();
     if (tid < kWave) find_bin<kBins>(tot, static_cast<uint32_t>(k), &s_bin, &s_above);
     __syncthreads();
     const uint32_t b1 = s_bin;
     const uint32_t above1 = s_above;
-    for (int j0 = 0; j0 < rounds; j0 += JB) {
-        if (MULTI) load(j0);
 #pragma unroll
-        for (int jj = 0; jj < JB; ++jj)
-            if ((kr[jj] >> 8) == b1) atomicAdd(&hist2[kr[jj] & 0xffu], 1u);
-        if (!MULTI) break;
+    for (int i = 0; i < (RELOAD ? SEG / 32 : 1); ++i) {
+        if (RELOAD) load_keys(4 * i, 0u);
+#pragma unroll
+        for (int e = 0; e < 2 * KW; ++e) {
+            const uint32_t key = POPKV_KEY(e);
+            if ((key >> 8) == b1) atomicAdd(&hist2[key & 0xffu], 1u);
+        }
     }
     __syncthreads();
     if (tid < kWave) find_bin<kBins>(hist2, static_cast<uint32_t>(k) - above1, &s_bin, &s_above);
     __syncthreads();
-    const uint32_t thr = (b1 << 8) | s_bin;
+    const uint32_t thr = (b1 << 8) | s_bin;  // >= 0x03ff
     const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
-    const bool partial = need_eq < hist2[s_bin];  // block-uniform
 
-    // 3. per-word bits of key > T and key == T; lane jj of each wave holds
-    //    round j0 + jj's words
-    uint32_t gl = 0, gh_ = 0, el = 0, eh = 0;
-    for (int j0 = 0; j0 < rounds; j0 += JB) {
-        if (MULTI) load(j0);
+    // 3. masks: bit e of m_gt[i] / m_ge[i] = key 32 i + e > T / >= T
+    uint32_t m_gt[NM], m_eq[NM];
+    uint32_t n_gt = 0, n_eq = 0;
 #pragma unroll
-        for (int jj = 0; jj < JB; ++jj) {
-            const uint64_t gt = __ballot(kr[jj] > thr);
-            const uint64_t eq = __ballot(kr[jj] == thr);
-            const bool mine = lane == jj;
-            gl = mine ? static_cast<uint32_t>(gt) : gl;
-            gh_ = mine ? static_cast<uint32_t>(gt >> 32) : gh_;
-            el = mine ? static_cast<uint32_t>(eq) : el;
-            eh = mine ? static_cast<uint32_t>(eq >> 32) : eh;
+    for (int i = 0; i < NM; ++i) {
+        if (RELOAD) load_keys(4 * i, n_gt + n_eq);
+        const int eb = RELOAD ? 0 : 32 * i;  // mask i's first key in kp
+        uint32_t g = 0, ge = 0;
+#pragma unroll
+        for (int e = MB - 1; e >= 0; --e) {
+            const uint32_t key = POPKV_KEY(eb + e);
+            g = __builtin_amdgcn_alignbit(g, thr - key, 31);
+            ge = __builtin_amdgcn_alignbit(ge, thr - 1u - key, 31);
         }
-        if (lane < JB && j0 + lane < rounds) {
-            const int e = (j0 + lane) * kSelWaves + wave;  // word index in token order
-            if (MULTI || partial) s_eq[e] = (static_cast<uint64_t>(eh) << 32) | el;
-            if (MULTI) s_gt[e] = (static_cast<uint64_t>(gh_) << 32) | gl;
-        }
-        if (!MULTI) break;
+        m_gt[i] = g;
+        m_eq[i] = ge & ~g;
+        n_gt += __popc(g);
+        n_eq += __popc(m_eq[i]);
     }
-    int tau = ntok;
-    if (partial) {
-        // the word holding the need_eq-th tie (token order = word order):
-        // wave 0, lane l owns words [l*PERW, l*PERW + PERW), one DPP scan
-        __syncthreads();
-        if (tid < kWave) {
-            constexpr int PERW = SLOTS / kWave;
-            const int n_slots = rounds * kSelWaves;
-            uint32_t local = 0;
-            for (int i = 0; i < PERW; ++i) {
-                const int e = lane * PERW + i;
-                local += e < n_slots ? static_cast<uint32_t>(__popcll(s_eq[e])) : 0u;
-            }
-            const uint32_t excl = wave_incl_scan(local, lane) - local;
-            // the crossing lane, then (uniformly) its crossing word
-            const uint64_t cross = __ballot(excl < need_eq && excl + local >= need_eq);
-            const int owner = static_cast<int>(__builtin_ctzll(cross));
-            uint32_t run = __builtin_amdgcn_readlane(excl, owner);
-            int e = owner * PERW;
-            uint64_t m = s_eq[e];
-            for (int i = 0; i < PERW; ++i) {
-                m = s_eq[owner * PERW + i];
-                const uint32_t c = static_cast<uint32_t>(__popcll(m));
-                e = owner * PERW + i;
-                if (run + c >= need_eq) break;
-                run += c;
-            }
-            // the (need_eq - run)-th set bit of m: lane b holds bit b and its
-            // rank among the set bits below it
-            const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-            const uint64_t hit = __ballot(((m >> lane) & 1ull) && below == need_eq - run - 1);
-            if (lane == 0)
-                s_tau = static_cast<uint32_t>((e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave +
-                                              __builtin_ctzll(hit));
-        }
-        __syncthreads();
-        tau = static_cast<int>(s_tau);
-    }
-    // 4. final words: ties only up to tau
-    auto finish = [&](uint64_t gt, uint64_t eq, int wbase) {
-        if (eq != 0ull && tau < wbase + kWave) {
-            const int keep = tau - wbase + 1;  // tie bits [0, keep) stay
-            eq = keep <= 0 ? 0ull : (eq & ((keep >= kWave) ? ~0ull : ((1ull << keep) - 1ull)));
-        }
-        return gt | eq;
-    };
-    if (!MULTI) {
-        const int wbase = lane * kSelThreads + wave * kWave;
-        if (lane < JB && wbase < ntok) {
-            const uint64_t w = finish((static_cast<uint64_t>(gh_) << 32) | gl, (static_cast<uint64_t>(eh) << 32) | el,
-                                      wbase);
-            *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(static_cast<uint32_t>(w),
-                                                                      static_cast<uint32_t>(w >> 32));
-        }
+#undef POPKV_KEY
+    // 4. ranks.  For rows of up to 65536 tokens both exclusive prefixes fit
+    //    16 bits and one packed scan serves both.
+    uint32_t total, gt_before, eq_before;
+    if (SEG <= 64) {
+        const uint32_t packed = block_excl_scan_once(n_gt | (n_eq << 16), scan_a, kSelWaves, &total);
+        gt_before = packed & 0xffffu;
+        eq_before = packed >> 16;
     } else {
-        __syncthreads();
-        for (int e = tid; e < rounds * kSelWaves; e += kSelThreads) {
-            const int wbase = (e / kSelWaves) * kSelThreads + (e % kSelWaves) * kWave;
-            if (wbase >= ntok) continue;
-            const uint64_t w = finish(s_gt[e], s_eq[e], wbase);
-            *reinterpret_cast<uint2*>(mrow + wbase / 32) = make_uint2(static_cast<uint32_t>(w),
-                                                                      static_cast<uint32_t>(w >> 32));
+        gt_before = block_excl_scan_once(n_gt, scan_a, kSelWaves, &total);
+        eq_before = block_excl_scan_once(n_eq, scan_b, kSelWaves, &total);
+    }
+    // (taken_before is formed first and the subtraction below never wraps:
+    // a ternary "eq_before >= need_eq ? 0 : need_eq - eq_before" here was
+    // miscompiled by this toolchain's optimizer, which dropped the later
+    // min as if the subtraction's no-wrap flag held everywhere)
+    const uint32_t taken_before = min(eq_before, need_eq);
+    uint32_t take_ties = min(n_eq, need_eq - taken_before);  // this thread's ties taken
+    uint32_t pos = gt_before + taken_before;
+    // 5. writes, mask by mask in token order
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+        uint32_t ties = m_eq[i];
+        const uint32_t c = static_cast<uint32_t>(__popc(ties));
+        if (take_ties < c) {  // keep only the first take_ties ties
+            uint32_t rest = ties;
+            for (uint32_t j = 0; j < take_ties; ++j) rest &= rest - 1u;
+            ties &= ~rest;
+            take_ties = 0;
+        } else {
+            take_ties -= c;
         }
-    }
-}
-
-// Ascending indices of a selection mask, the current token in slot k.
-// One 1024-thread block per row; thread t owns WPT consecutive mask words.
-template <int WPT, typename IdxT>
-__global__ __launch_bounds__(kSelThreads) void mask_to_indices_kernel(
-    const uint32_t* __restrict__ mask, int64_t mask_stride, int64_t tokens, int64_t k, int64_t current,
-    IdxT* __restrict__ out, int64_t out_stride) {
-    const int64_t row = blockIdx.x;
-    const uint32_t* mrow = mask + row * mask_stride;
-    IdxT* dst = out + row * out_stride;
-    const int tid = threadIdx.x;
-    const int64_t nwords = (tokens + 31) / 32;
-    __shared__ uint32_t scan_sh[kSelWaves + 1];
-    uint32_t w[WPT], cnt = 0;
-#pragma unroll
-    for (int i = 0; i < WPT; ++i) {
-        const int64_t e = static_cast<int64_t>(tid) * WPT + i;
-        w[i] = e < nwords ? mrow[e] : 0u;
-        cnt += __popc(w[i]);
-    }
-    uint32_t total;
-    uint32_t pos = block_excl_scan_once(cnt, scan_sh, kSelWaves, &total);
-#pragma unroll
-    for (int i = 0; i < WPT; ++i) {
-        const int64_t tbase = (static_cast<int64_t>(tid) * WPT + i) * 32;
-        for (uint32_t m = w[i]; m; m &= m - 1) {
-            if (pos < static_cast<uint64_t>(k)) dst[pos] = static_cast<IdxT>(tbase + __builtin_ctz(m));
+        for (uint32_t m = m_gt[i] | ties; m != 0u; m &= m - 1u) {
+            const int32_t t = begin + 32 * i + __builtin_ctz(m);
+            if (pos < static_cast<uint32_t>(k)) {
+                lrow[pos] = t;
+                if (irow != nullptr) irow[pos] = t;
+            }
             ++pos;
         }
     }
-    if (tid == 0) dst[k] = static_cast<IdxT>(current);
 }
 
 template <int SEG, typename IdxT>
@@ -443,37 +407,22 @@ hipError_t launch_select_t(const uint16_t* scores, int64_t rows, int64_t row_str
 
 }  // namespace
 
-hipError_t launch_topk_mask(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
-                            int64_t k, uint32_t* mask, int64_t mask_stride, hipStream_t stream) {
+hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
+                            int64_t k, int32_t* list, int64_t list_stride, int64_t* idx64, int64_t idx_stride,
+                            int64_t current, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    const int64_t rounds = (tokens + kSelThreads - 1) / kSelThreads;
+    const int64_t per = (tokens + kSelThreads - 1) / kSelThreads;
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k < tokens ? k : tokens);
     dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
-#define POPKV_MASK(JB, MULTI)                                                                                   \
-    hipLaunchKernelGGL((topk_mask_kernel<JB, MULTI>), grid, block, 0, stream, keys, ghist, row_stride, nt, kk, \
-                       mask, mask_stride)
-    if (rounds <= 8) POPKV_MASK(8, false);
-    else if (rounds <= 16) POPKV_MASK(16, false);
-    else if (rounds <= 32) POPKV_MASK(32, false);
-    else POPKV_MASK(32, true);
-#undef POPKV_MASK
-    return hipGetLastError();
-}
-
-hipError_t launch_mask_to_indices(const uint32_t* mask, int64_t rows, int64_t mask_stride, int64_t tokens, int64_t k,
-                                  int64_t current, int64_t* indices, int64_t index_row_stride, hipStream_t stream) {
-    if (rows <= 0) return hipSuccess;
-    const int64_t words = (tokens + 31) / 32;
-    dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
-    if (words <= kSelThreads)
-        hipLaunchKernelGGL((mask_to_indices_kernel<1, int64_t>), grid, block, 0, stream, mask, mask_stride, tokens, k,
-                           current, indices, index_row_stride);
-    else if (words <= 2 * kSelThreads)
-        hipLaunchKernelGGL((mask_to_indices_kernel<2, int64_t>), grid, block, 0, stream, mask, mask_stride, tokens, k,
-                           current, indices, index_row_stride);
-    else
-        hipLaunchKernelGGL((mask_to_indices_kernel<4, int64_t>), grid, block, 0, stream, mask, mask_stride, tokens, k,
-                           current, indices, index_row_stride);
+#define POPKV_LIST(SEG)                                                                                          \
+    hipLaunchKernelGGL((topk_list_kernel<SEG>), grid, block, 0, stream, keys, ghist, row_stride, nt, kk, list, \
+                       list_stride, idx64, idx_stride, current)
+    if (per <= 8) POPKV_LIST(8);
+    else if (per <= 16) POPKV_LIST(16);
+    else if (per <= 32) POPKV_LIST(32);
+    else if (per <= 64) POPKV_LIST(64);
+    else POPKV_LIST(128);
+#undef POPKV_LIST
     return hipGetLastError();
 }
 
