@@ -5,8 +5,6 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
-#include <utility>
-
 #include "popkv_hip.h"
 
 namespace popkv {
@@ -222,32 +220,6 @@ template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, BOUND_ZERO));
 }
-// LLVM's writelane intrinsic (clang has no builtin for it here): the
-// backend sees the instruction and inserts the wait states a preceding
-// scalar-register write by a vector instruction requires.
-__device__ int popkv_llvm_writelane(int value, int lane, int old) __asm("llvm.amdgcn.writelane.i32");
-
-// x with lane L replaced by the wave-uniform value v (v_writelane_b32 with an
-// immediate lane: a vector-register write).  Collecting per-round uniform
-// values this way needs no per-lane "lane == j" masks, which the compiler
-// would otherwise hoist and keep live in scalar registers (and spill).
-template <int L>
-__device__ __forceinline__ uint32_t write_lane(uint32_t x, uint32_t v) {
-    static_assert(L >= 0 && L < kWave, "lane out of range");
-    return static_cast<uint32_t>(popkv_llvm_writelane(static_cast<int>(v), L, static_cast<int>(x)));
-}
-
-// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N-1>{}):
-// a loop whose index is a compile-time constant in the body.
-template <typename F, int... J>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int /*lane*/) {
     v += dpp_u32<0x111, 0xf, true>(v);
     v += dpp_u32<0x112, 0xf, true>(v);

@@ -156,7 +156,7 @@ __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm
                      fmaf(ql * dk, static_cast<float>(ck), dq * dk * static_cast<float>(cqk))));
 }
 
-constexpr int kScoreThreads = 256;
+constexpr int kScoreThreads = 512;  // 8 waves: 1024 tokens x one GQA group per workgroup
 constexpr int kScoreTokensPerThread = 2;
 constexpr int kMaxGroupHeads = 64;  // query heads per KV head the LDS stage holds
 
