@@ -37,10 +37,10 @@ N_BUFFERS = 8
 # HBM bytes per launch of the layer step's attention kernel at C1, from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script (KiB per
 # dispatch), each scaled by the same counter on a plain 256 MiB copy
-# (bench.py --copy-calibration): FETCH_SIZE reads 131084.5 KiB for the copy's
+# (bench.py --copy-calibration): FETCH_SIZE reads 131084.4 KiB for the copy's
 # 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).  Attention:
-# FETCH_SIZE 28020.6 KiB, WRITE_SIZE 272.0 KiB per dispatch.
-ATTN_TRAFFIC_BYTES = round(28020.6 * 1024 * (262144 / 131084.5) + 272.0 * 1024)
+# FETCH_SIZE 28700.5 KiB, WRITE_SIZE 272.0 KiB per dispatch.
+ATTN_TRAFFIC_BYTES = round(28700.5 * 1024 * (262144 / 131084.4) + 272.0 * 1024)
 
 
 def parse_args():
@@ -443,7 +443,7 @@ def main() -> int:
         "append": {"active_tokens": int(active.shape[1]), "us": round(append_ms * 1e3, 3),
                    "algorithmic_bytes": append_bytes, "GBps": round(append_bytes / (append_ms * 1e-3) / 1e9, 1)},
         "unique_kv_rows_per_step": unique_rows,
-        "roofline": {"bound": "hbm", "kernel": "attn_rank_kernel (layer step attention)",
+        "roofline": {"bound": "hbm", "kernel": "attn_list_kernel (layer step attention)",
                      "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
                      "algorithmic_bytes_per_launch": alg["attention"], "avg_launch_us": round(attn_step_ms * 1e3, 3)},

@@ -210,7 +210,10 @@ __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk,
     for (int item = threadIdx.x; item < qpk * R; item += kScoreThreads) {
         const int h = item / R, r = item % R;
         float ls = 0.0f, hs = 0.0f;
-#pragma unroll
+        // a partial unroll: fully unrolled, the compiler loads all 2G
+        // contributions before the (sequential) add chains, which alone takes
+        // 2G registers and caps the scorer's occupancy
+#pragma unroll 4
         for (int j = 0; j < G; j += 4) {
             const float4 l4 = *reinterpret_cast<const float4*>(&lo_c[h][r * G + j]);
             const float4 h4 = *reinterpret_cast<const float4*>(&hi_c[h][r * G + j]);
