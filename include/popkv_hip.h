@@ -108,11 +108,19 @@ int popkv_score(const void* queries, int32_t dtype, int64_t batch, int64_t q_hea
  * -0 < +0, NaN largest), ties at the k-th value taken in ascending token
  * order, written in ascending token order to indices[r, 0..k), and `current`
  * written to indices[r, k].  0 <= k <= tokens.  tokens <= 131072 per row.
+ * Needs popkv_topk_select_workspace_bytes(rows, tokens) bytes of 256-byte
+ * aligned workspace whose first rows * 1024 bytes (the per-row histograms)
+ * are zero when the call begins; every call leaves them zero again, so the
+ * workspace can be reused by later calls with the same row count (after a
+ * call with fewer rows, clear the larger histogram region first).  Calls
+ * sharing one workspace must be stream-ordered.
  * Replaces torch.topk(scores, k, dim=-1, sorted=False).indices followed by
  * _append_current (reference popkv.py:1094-1098, :287-291). */
+size_t popkv_topk_select_workspace_bytes(int64_t rows, int64_t tokens);
 int popkv_topk_select(const void* scores, int64_t rows, int64_t row_stride, int64_t tokens,
                       int64_t k, int64_t current, void* indices, int32_t index_dtype,
-                      int64_t index_row_stride, void* stream);
+                      int64_t index_row_stride, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /* Split sparse attention, partial pass: for query head h and split s, the
  * online-softmax state of rows indices[h, s*split .. s*split+split) of
@@ -151,9 +159,11 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
  * queries/prefix/current K/V share `dtype`; output [QH, 128] has `dtype`.
  * indices_out (int64 [QH, k+1]) may be NULL; when given, the selection is
  * also written there.  Needs popkv_layer_step_workspace_bytes() bytes of
- * workspace, 16-byte aligned and zero-filled before its first use; every call
- * leaves the workspace's histogram region zeroed again, so it can be reused
- * by later calls (calls sharing one workspace must be stream-ordered).
+ * 16-byte aligned workspace whose first q_heads * 1024 bytes (the per-head
+ * key histograms) are zero when the call begins; every call leaves them zero
+ * again, so the workspace can be reused by later calls with the same head
+ * count (after a call with fewer heads, clear the larger histogram region
+ * first).  Calls sharing one workspace must be stream-ordered.
  * Replaces the PopKV branch of LlamaSparseDecoder.decode (reference
  * popkv.py:1076-1115): query_encode, score_encoded, torch.topk +
  * _append_current, indexed_attention_split_partial and _merge. */

@@ -42,7 +42,9 @@ _SIGNATURES = {
     "popkv_score_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i32]),
     "popkv_score": (ctypes.c_int, [_vp, _c_i32, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
                                    _c_i64, _c_i32, _vp, _vp, _c_size, _vp]),
-    "popkv_topk_select": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _c_i32, _c_i64, _vp]),
+    "popkv_topk_select_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "popkv_topk_select": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _c_i32, _c_i64, _vp,
+                                         _c_size, _vp]),
     "popkv_sparse_attention_partial": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                                       _vp, _vp, _vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _c_i64,
                                                       _c_i64, _c_i32, _vp, _vp]),

@@ -207,18 +207,29 @@ int popkv_score(const void* queries, int32_t dtype, int64_t batch, int64_t q_hea
                     "popkv_score");
 }
 
+size_t popkv_topk_select_workspace_bytes(int64_t rows, int64_t tokens) {
+    if (rows < 0 || tokens < 0) return 0;
+    return popkv::topk_select_workspace_bytes(rows, tokens);
+}
+
 int popkv_topk_select(const void* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
-                      int64_t current, void* indices, int32_t index_dtype, int64_t index_row_stride, void* stream) {
-    if (!scores || !indices) return fail(POPKV_ERR_INVALID, "null pointer");
+                      int64_t current, void* indices, int32_t index_dtype, int64_t index_row_stride,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+    if (!scores || !indices || !workspace) return fail(POPKV_ERR_INVALID, "null pointer");
     if (rows < 0 || tokens < 0 || row_stride < tokens) return fail(POPKV_ERR_INVALID, "bad score shape");
     if (k < 0 || k > tokens) return fail(POPKV_ERR_INVALID, "k must satisfy 0 <= k <= tokens");
     if (index_row_stride < k + 1) return fail(POPKV_ERR_INVALID, "index row stride too small");
     if (index_dtype != POPKV_INDEX_I64 && index_dtype != POPKV_INDEX_I32)
         return fail(POPKV_ERR_INVALID, "index dtype must be int64 or int32");
     if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens per row");
-    if (rows > 0x7fffffff) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
+    if (rows > 0x7fffffff / 32) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
+    if (workspace_bytes < popkv::topk_select_workspace_bytes(rows, tokens))
+        return fail(POPKV_ERR_WORKSPACE, "top-k select needs %zu workspace bytes",
+                    popkv::topk_select_workspace_bytes(rows, tokens));
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(POPKV_ERR_INVALID, "workspace must be 256-byte aligned");
     return launched(popkv::launch_topk_select(static_cast<const uint16_t*>(scores), rows, row_stride, tokens, k,
-                                              current, indices, index_dtype, index_row_stride, as_stream(stream)),
+                                              current, indices, index_dtype, index_row_stride, workspace,
+                                              as_stream(stream)),
                     "popkv_topk_select");
 }
 
@@ -324,7 +335,7 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
     //    histograms), also written as int64 with the current token in slot k
     //    when indices_out is given
     st = launched(popkv::launch_topk_list(keys, hist, q_heads, L.score_stride, tokens, L.k, list, L.list_stride,
-                                          indices_out, L.k + 1, tokens, s),
+                                          false, indices_out, L.k + 1, tokens, s),
                   "popkv_layer_step(select)");
     if (st) return st;
     // 3. sparse attention over 256-token splits of each head's list,

@@ -41,18 +41,24 @@ hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, con
                                 int64_t batch, int q_heads, int kv_heads, int head_dim, int64_t capacity,
                                 int64_t tokens, int dim_group_size, float* scores, hipStream_t stream);
 
+// API-path top-k: fp16 scores [rows, row_stride] -> indices [rows,
+// index_row_stride] (int32 or int64), k selected tokens ascending and
+// `current` in slot k.  workspace: topk_select_workspace_bytes(rows, tokens)
+// bytes, 256-byte aligned, its first rows*1 KiB zero on entry (left zero).
+size_t topk_select_workspace_bytes(int64_t rows, int64_t tokens);
 hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens,
                               int64_t k, int64_t current, void* indices, int index_dtype,
-                              int64_t index_row_stride, hipStream_t stream);
+                              int64_t index_row_stride, void* workspace, hipStream_t stream);
 
-// Layer-step select over radix order keys with the high-byte histograms
-// ghist[row][256] the scorer built: writes each row's k selected tokens in
-// ascending order to list[row][0..k) (int32) and, with idx64 non-null, to
-// idx64[row][0..k) as int64 with `current` in slot k; re-zeroes ghist.
+// Select over radix order keys with the high-byte histograms ghist[row][256]
+// already accumulated: writes each row's k selected tokens in ascending
+// order to list[row][0..k) (int32; `current` in slot k when list_current)
+// and/or idx64[row][0..k) (int64, `current` in slot k); either may be null.
+// Re-zeroes ghist.  Key rows are padded to a multiple of 128 keys;
 // tokens <= 131072.
 hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
-                            int64_t k, int32_t* list, int64_t list_stride, int64_t* idx64, int64_t idx_stride,
-                            int64_t current, hipStream_t stream);
+                            int64_t k, int32_t* list, int64_t list_stride, bool list_current, int64_t* idx64,
+                            int64_t idx_stride, int64_t current, hipStream_t stream);
 
 hipError_t launch_attention_partial(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                     int64_t k_head_stride, int64_t k_token_stride, int64_t v_head_stride,

@@ -1,28 +1,19 @@
-// Per-query-head top-k over fp16 scores with the current token reserving the
+// Per-query-head top-k over PopKV scores with the current token reserving the
 // last slot (gfx950).
 //
 // Replaces torch.topk(scores, k, dim=-1, sorted=False).indices followed by
 // _append_current (reference popkv.py:1094-1098, :287-291).
 //
-// One 1024-thread workgroup (16 wave64s) per row.  Thread t owns the
-// contiguous segment of SEG tokens [t*SEG, t*SEG + SEG), read with 16-byte
-// loads, and keeps its keys in registers (two 16-bit keys per VGPR) for the
-// whole kernel.  The key is PyTorch's radix order of an fp16 bit pattern:
-// negatives bit-inverted, non-negatives with the sign bit set, NaN largest,
-// so -0 < +0.
-//   1. 256-bin histogram of the key's high byte -> the bin b1 holding the
-//      k-th largest key;
-//   2. 256-bin histogram of the low byte among keys with high byte b1 ->
-//      the exact k-th largest key T.
-//      Both histograms are privatized per lane (bin*64 + lane): PopKV's
-//      scores are peaked, so a shared histogram would serialize on
-//      same-address LDS atomics; with one copy per lane no two lanes of an
-//      instruction touch the same word.  The 64 copies are then summed.
-//   3. keys > T are selected; keys == T fill the remaining slots in ascending
-//      token order (PyTorch's gather-top-k tie rule).  One block scan of the
-//      packed per-thread (greater, equal) counts gives every selected token
-//      its slot in ascending token order; slots are filled in LDS and the
-//      finished list is copied out with coalesced stores.
+// Keys are PyTorch's radix order of an fp16 bit pattern: negatives
+// bit-inverted, non-negatives with the sign bit set, NaN largest, so
+// -0 < +0.  Selection = every key > T plus the lowest-index keys == T, T the
+// k-th largest key (PyTorch's gather-top-k tie rule).
+//
+// Two kernels.  key_hist_kernel (API path only; the layer step's scorer does
+// this itself) turns fp16 scores into order keys and accumulates each row's
+// 256-bin histogram of the keys' high byte; topk_list_kernel then finds T
+// from that histogram plus one low-byte histogram and writes the selected
+// tokens in ascending order.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -59,145 +50,57 @@ __device__ __forceinline__ void find_bin(const uint32_t* hist, uint32_t need, ui
     }
 }
 
-constexpr int kStageMax = 8192;  // selections staged in LDS (k <= 8192)
+// fp16 scores -> order keys in rows of key_stride (a multiple of 128 keys),
+// plus each row's high-byte histogram added into ghist[row][256].  Block
+// (row, c) covers tokens [4096 c, 4096 c + 4096), 16 per thread; VEC: the
+// rows are 16-byte aligned and read with 16-byte loads.  Peaked scores put
+// many keys in a few bins, so the block's LDS histogram takes some
+// same-address atomics; its non-zero bins are then added to ghist.
+constexpr int kKeyHistThreads = 256;
+constexpr int kKeyHistTokens = 16;  // per thread
 
-template <int SEG, bool VEC, typename IdxT>
-__global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
-    const uint16_t* __restrict__ scores, int64_t row_stride, int64_t tokens, int64_t k, int64_t current,
-    IdxT* __restrict__ out, int64_t out_stride) {
-    static_assert(SEG % 8 == 0, "segments are whole 16-byte chunks");
-    const int64_t row = blockIdx.x;
-    const uint16_t* src = scores + row * row_stride;
-    IdxT* dst = out + row * out_stride;
-    const int tid = threadIdx.x;
-
-    if (k >= tokens) {  // every cached token is selected
-        for (int64_t t = tid; t < tokens; t += kSelThreads) dst[t] = static_cast<IdxT>(t);
-        if (tid == 0) dst[tokens] = static_cast<IdxT>(current);
-        return;
-    }
-    if (k == 0) {
-        if (tid == 0) dst[0] = static_cast<IdxT>(current);
-        return;
-    }
-
-    __shared__ uint32_t hist[kBins * kWave];  // [bin][lane]
-    __shared__ uint32_t tot[kBins];
-    __shared__ uint32_t scan_sh[kSelWaves + 1];
-    __shared__ uint32_t s_bin, s_above;
-    __shared__ int32_t stage[kStageMax];
-    const int lane = tid & (kWave - 1);
-
-    // ---- load this thread's segment; absent tokens are never counted (n below)
-    const int64_t begin = static_cast<int64_t>(tid) * SEG;
-    const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(SEG, tokens - begin)));
-    uint32_t kp[SEG / 2];
-#pragma unroll
-    for (int c = 0; c < SEG / 8; ++c) {
-        if (VEC && 8 * c + 8 <= n) {
-            const uint4 u = *reinterpret_cast<const uint4*>(src + begin + 8 * c);
-            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) kp[4 * c + j] = order_key(w[j] & 0xffffu) | (order_key(w[j] >> 16) << 16);
+template <bool VEC>
+__global__ __launch_bounds__(kKeyHistThreads) void key_hist_kernel(const uint16_t* __restrict__ scores,
+                                                                   int64_t row_stride, int64_t tokens, int chunks,
+                                                                   uint16_t* __restrict__ keys, int64_t key_stride,
+                                                                   uint32_t* __restrict__ ghist) {
+    const int64_t row = blockIdx.x / chunks;
+    const int64_t t0 = (static_cast<int64_t>(blockIdx.x % chunks) * kKeyHistThreads + threadIdx.x) * kKeyHistTokens;
+    __shared__ uint32_t s_hist[kBins];
+    s_hist[threadIdx.x] = 0u;
+    __syncthreads();
+    if (t0 < tokens) {
+        const uint16_t* src = scores + row * row_stride + t0;
+        uint32_t w[kKeyHistTokens / 2];
+        if (VEC && t0 + kKeyHistTokens <= tokens) {
+            const uint4 a = reinterpret_cast<const uint4*>(src)[0];
+            const uint4 b = reinterpret_cast<const uint4*>(src)[1];
+            w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+            w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 8 * c + 2 * j;
-                const uint32_t a = e < n ? order_key(src[begin + e]) : 0u;
-                const uint32_t b = e + 1 < n ? order_key(src[begin + e + 1]) : 0u;
-                kp[4 * c + j] = a | (b << 16);
+            for (int i = 0; i < kKeyHistTokens / 2; ++i) {
+                const uint32_t lo = t0 + 2 * i < tokens ? src[2 * i] : 0u;
+                const uint32_t hi = t0 + 2 * i + 1 < tokens ? src[2 * i + 1] : 0u;
+                w[i] = lo | (hi << 16);
             }
         }
-    }
-#define POPKV_KEY(e) ((kp[(e) >> 1] >> (((e) & 1) * 16)) & 0xffffu)
-
-    // Sums the 64 per-lane copies into tot[]: thread (bin, quarter) adds 16
-    // copies, then the four quarters of a bin (adjacent lanes) combine.  The
-    // copy order is rotated by bin so a wave's 64 reads hit 64 banks.
-    auto reduce_hist = [&]() {
-        const int bin = tid >> 2, q = tid & 3;
-        uint32_t v = 0;
+        uint32_t kw[kKeyHistTokens / 2];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) v += hist[bin * kWave + q * 16 + ((c + bin) & 15)];
-        v += __shfl_xor(v, 1);
-        v += __shfl_xor(v, 2);
-        if (q == 0) tot[bin] = v;
-    };
-
-    // ---- level 1: high byte
-    for (int i = tid; i < kBins * kWave; i += kSelThreads) hist[i] = 0u;
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < SEG; ++e)
-        if (e < n) atomicAdd(&hist[(POPKV_KEY(e) >> 8) * kWave + lane], 1u);
-    __syncthreads();
-    reduce_hist();
-    __syncthreads();
-    if (tid < kWave) find_bin<kBins>(tot, static_cast<uint32_t>(k), &s_bin, &s_above);
-    __syncthreads();
-    const uint32_t b1 = s_bin;
-    const uint32_t above1 = s_above;
-
-    // ---- level 2: low byte inside bin b1
-    for (int i = tid; i < kBins * kWave; i += kSelThreads) hist[i] = 0u;
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < SEG; ++e) {
-        const uint32_t key = POPKV_KEY(e);
-        if (e < n && (key >> 8) == b1) atomicAdd(&hist[(key & 0xffu) * kWave + lane], 1u);
-    }
-    __syncthreads();
-    reduce_hist();
-    __syncthreads();
-    if (tid < kWave) find_bin<kBins>(tot, static_cast<uint32_t>(k) - above1, &s_bin, &s_above);
-    __syncthreads();
-    const uint32_t thr = (b1 << 8) | s_bin;
-    const uint32_t need_eq = static_cast<uint32_t>(k) - above1 - s_above;
-
-    // ---- ordered selection: slot of a selected token = (#greater before it)
-    //      + min(#equal before it, need_eq)
-    uint32_t n_gt = 0, n_eq = 0;
-#pragma unroll
-    for (int e = 0; e < SEG; ++e) {
-        const uint32_t key = POPKV_KEY(e);
-        if (e < n) {
-            n_gt += key > thr ? 1u : 0u;
-            n_eq += key == thr ? 1u : 0u;
+        for (int i = 0; i < kKeyHistTokens / 2; ++i) {
+            const uint32_t k0 = order_key(w[i] & 0xffffu), k1 = order_key(w[i] >> 16);
+            if (t0 + 2 * i < tokens) atomicAdd(&s_hist[k0 >> 8], 1u);
+            if (t0 + 2 * i + 1 < tokens) atomicAdd(&s_hist[k1 >> 8], 1u);
+            kw[i] = k0 | (k1 << 16);
         }
+        // t0 + 16 <= key_stride: the key rows are padded to 128 keys
+        uint4* dst = reinterpret_cast<uint4*>(keys + row * key_stride + t0);
+        dst[0] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+        dst[1] = make_uint4(kw[4], kw[5], kw[6], kw[7]);
     }
-    uint32_t total, gt_before, eq_before;
-    if (tokens <= 0xffff) {  // both prefix counts fit 16 bits: one packed scan
-        const uint32_t packed = block_excl_scan(n_gt | (n_eq << 16), scan_sh, kSelWaves, &total);
-        gt_before = packed & 0xffffu;
-        eq_before = packed >> 16;
-    } else {
-        gt_before = block_excl_scan(n_gt, scan_sh, kSelWaves, &total);
-        eq_before = block_excl_scan(n_eq, scan_sh, kSelWaves, &total);
-    }
-    const bool staged = k <= kStageMax;
-#pragma unroll
-    for (int e = 0; e < SEG; ++e) {
-        const uint32_t key = POPKV_KEY(e);
-        if (e >= n) continue;
-        uint32_t slot = 0xffffffffu;
-        if (key > thr) {
-            slot = gt_before + min(eq_before, need_eq);
-            ++gt_before;
-        } else if (key == thr) {
-            if (eq_before < need_eq) slot = gt_before + eq_before;
-            ++eq_before;
-        }
-        if (slot != 0xffffffffu) {
-            if (staged) stage[slot] = static_cast<int32_t>(begin + e);
-            else dst[slot] = static_cast<IdxT>(begin + e);
-        }
-    }
-#undef POPKV_KEY
-    if (staged) {
-        __syncthreads();
-        for (int64_t i = tid; i < k; i += kSelThreads) dst[i] = static_cast<IdxT>(stage[i]);
-    }
-    if (tid == 0) dst[k] = static_cast<IdxT>(current);
+    __syncthreads();
+    const uint32_t c = s_hist[threadIdx.x];
+    if (c != 0u) atomicAdd(&ghist[row * kBins + threadIdx.x], c);
 }
 
 // Layer-step select, list form.  The input rows hold radix order keys and
@@ -219,24 +122,25 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
 //   5. the thread writes its selected tokens (set bits of its mask, in
 //      ascending order) to list[rank...].
 // The VALU work per key is a few instructions, which matters: the kernel
-// runs on one CU per row.  The list row receives the k selected tokens in
-// ascending order (int32); with idx64 non-null the same tokens are written
-// as int64 followed by `current` in slot k (the reference's _append_current
+// runs on one CU per row.  With list non-null, its row receives the k
+// selected tokens in ascending order (int32), followed by `current` in slot
+// k when list_current; with idx64 non-null the same tokens are written as
+// int64 followed by `current` in slot k (the reference's _append_current
 // layout).  Absent tokens (past `tokens`) get key 0, below every real key
 // (real keys are >= 0x03ff; NaN patterns map to 0xffff).  ghist is
 // re-zeroed for the next call.
 template <int SEG>
 __global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
     const uint16_t* __restrict__ keys, uint32_t* __restrict__ ghist, int64_t row_stride, int ntok, int k,
-    int32_t* __restrict__ list, int64_t list_stride, int64_t* __restrict__ idx64, int64_t idx_stride,
-    int64_t current) {
+    int32_t* __restrict__ list, int64_t list_stride, bool list_current, int64_t* __restrict__ idx64,
+    int64_t idx_stride, int64_t current) {
     static_assert(SEG % 8 == 0 && SEG <= 128, "whole 16-byte chunks, at most four 32-bit masks");
     constexpr int NM = (SEG + 31) / 32;   // 32-bit masks per thread
     constexpr int MB = SEG < 32 ? SEG : 32;  // bits per mask
     const int64_t row = blockIdx.x;
     const uint16_t* src = keys + row * row_stride;
     uint32_t* gh = ghist + row * kBins;
-    int32_t* lrow = list + row * list_stride;
+    int32_t* lrow = list != nullptr ? list + row * list_stride : nullptr;
     int64_t* irow = idx64 != nullptr ? idx64 + row * idx_stride : nullptr;
     const int tid = threadIdx.x;
 
@@ -248,13 +152,16 @@ __global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
         gh[tid] = 0u;
         hist2[tid] = 0u;
     }
-    if (irow != nullptr && tid == 0) irow[k] = current;
+    if (tid == 0) {
+        if (irow != nullptr) irow[k] = current;
+        if (lrow != nullptr && list_current) lrow[k] = static_cast<int32_t>(current);
+    }
     // mode 0: nothing selected (k == 0); 1: every token (k >= ntok); 2: threshold
     const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);
     if (mode != 2) {
         if (mode == 1) {
             for (int t = tid; t < ntok; t += kSelThreads) {
-                lrow[t] = t;
+                if (lrow != nullptr) lrow[t] = t;
                 if (irow != nullptr) irow[t] = t;
             }
         }
@@ -372,7 +279,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
         for (uint32_t m = m_gt[i] | ties; m != 0u; m &= m - 1u) {
             const int32_t t = begin + 32 * i + __builtin_ctz(m);
             if (pos < static_cast<uint32_t>(k)) {
-                lrow[pos] = t;
+                if (lrow != nullptr) lrow[pos] = t;
                 if (irow != nullptr) irow[pos] = t;
             }
             ++pos;
@@ -380,43 +287,18 @@ __global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
     }
 }
 
-template <int SEG, typename IdxT>
-void launch_seg(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
-                int64_t current, IdxT* out, int64_t out_stride, bool vec, hipStream_t stream) {
-    dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
-    if (vec)
-        hipLaunchKernelGGL((topk_select_kernel<SEG, true, IdxT>), grid, block, 0, stream, scores, row_stride, tokens,
-                           k, current, out, out_stride);
-    else
-        hipLaunchKernelGGL((topk_select_kernel<SEG, false, IdxT>), grid, block, 0, stream, scores, row_stride,
-                           tokens, k, current, out, out_stride);
-}
-
-template <typename IdxT>
-hipError_t launch_select_t(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
-                           int64_t current, IdxT* out, int64_t out_stride, hipStream_t stream) {
-    const int64_t per = (tokens + kSelThreads - 1) / kSelThreads;
-    const bool vec = reinterpret_cast<uintptr_t>(scores) % 16 == 0 && row_stride % 8 == 0;
-    if (per <= 8) launch_seg<8>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
-    else if (per <= 16) launch_seg<16>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
-    else if (per <= 32) launch_seg<32>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
-    else if (per <= 64) launch_seg<64>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
-    else launch_seg<128>(scores, rows, row_stride, tokens, k, current, out, out_stride, vec, stream);
-    return hipGetLastError();
-}
-
 }  // namespace
 
 hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
-                            int64_t k, int32_t* list, int64_t list_stride, int64_t* idx64, int64_t idx_stride,
-                            int64_t current, hipStream_t stream) {
+                            int64_t k, int32_t* list, int64_t list_stride, bool list_current, int64_t* idx64,
+                            int64_t idx_stride, int64_t current, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     const int64_t per = (tokens + kSelThreads - 1) / kSelThreads;
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k < tokens ? k : tokens);
     dim3 grid(static_cast<unsigned>(rows)), block(kSelThreads);
 #define POPKV_LIST(SEG)                                                                                          \
     hipLaunchKernelGGL((topk_list_kernel<SEG>), grid, block, 0, stream, keys, ghist, row_stride, nt, kk, list, \
-                       list_stride, idx64, idx_stride, current)
+                       list_stride, list_current, idx64, idx_stride, current)
     if (per <= 8) POPKV_LIST(8);
     else if (per <= 16) POPKV_LIST(16);
     else if (per <= 32) POPKV_LIST(32);
@@ -426,15 +308,38 @@ hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows,
     return hipGetLastError();
 }
 
+size_t topk_select_workspace_bytes(int64_t rows, int64_t tokens) {
+    const int64_t key_stride = (tokens + 127) / 128 * 128;
+    const size_t hist = (static_cast<size_t>(rows) * kBins * 4 + 255) / 256 * 256;
+    return hist + static_cast<size_t>(rows) * static_cast<size_t>(key_stride > 0 ? key_stride : 128) * 2;
+}
+
 hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_stride, int64_t tokens, int64_t k,
                               int64_t current, void* indices, int index_dtype, int64_t index_row_stride,
-                              hipStream_t stream) {
+                              void* workspace, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    if (index_dtype == POPKV_INDEX_I32)
-        return launch_select_t(scores, rows, row_stride, tokens, k, current, static_cast<int32_t*>(indices),
-                               index_row_stride, stream);
-    return launch_select_t(scores, rows, row_stride, tokens, k, current, static_cast<int64_t*>(indices),
-                           index_row_stride, stream);
+    const int64_t key_stride = (tokens + 127) / 128 * 128;
+    uint32_t* ghist = static_cast<uint32_t*>(workspace);
+    uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) +
+                                                 (static_cast<size_t>(rows) * kBins * 4 + 255) / 256 * 256);
+    if (tokens > 0) {
+        const int chunks = static_cast<int>((tokens + kKeyHistThreads * kKeyHistTokens - 1) /
+                                            (kKeyHistThreads * kKeyHistTokens));
+        const bool vec = reinterpret_cast<uintptr_t>(scores) % 16 == 0 && row_stride % 8 == 0;
+        dim3 grid(static_cast<unsigned>(rows * chunks)), block(kKeyHistThreads);
+        if (vec)
+            hipLaunchKernelGGL((key_hist_kernel<true>), grid, block, 0, stream, scores, row_stride, tokens, chunks,
+                               keys, key_stride, ghist);
+        else
+            hipLaunchKernelGGL((key_hist_kernel<false>), grid, block, 0, stream, scores, row_stride, tokens, chunks,
+                               keys, key_stride, ghist);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const bool i32 = index_dtype == POPKV_INDEX_I32;
+    return launch_topk_list(keys, ghist, rows, key_stride, tokens, k, i32 ? static_cast<int32_t*>(indices) : nullptr,
+                            index_row_stride, true, i32 ? nullptr : static_cast<int64_t*>(indices), index_row_stride,
+                            current, stream);
 }
 
 }  // namespace popkv

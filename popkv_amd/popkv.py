@@ -261,15 +261,22 @@ def popkv_retrieval_step(
 class LayerStepWorkspace:
     """Reusable device workspace for ``popkv_layer_step`` (grown on demand).
 
-    The C ABI requires the workspace to be zero-filled before its first use
-    (each step leaves it reusable), so new buffers are allocated zeroed."""
+    The C ABI keeps per-head key histograms at the start of the workspace
+    (1 KiB per query head) and needs them zero when a call begins; every call
+    leaves them zero.  New buffers are allocated zeroed, and when the head
+    count changes the new histogram region is cleared, because it may cover
+    data a call with fewer heads left behind."""
 
     def __init__(self) -> None:
         self.buffer: torch.Tensor | None = None
+        self.rows = 0
 
-    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+    def get(self, nbytes: int, device: torch.device, rows: int = 0) -> torch.Tensor:
         if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
             self.buffer = torch.zeros(max(nbytes, 1), device=device, dtype=torch.uint8)
+        elif rows != self.rows:
+            self.buffer[: min(self.buffer.numel(), rows * 1024)].zero_()
+        self.rows = rows
         return self.buffer
 
 
@@ -309,7 +316,7 @@ def popkv_layer_step(
     if isinstance(workspace, torch.Tensor):
         ws = workspace  # caller-owned: zero-filled before its first use
     else:
-        ws = (workspace or LayerStepWorkspace()).get(nbytes, dev)
+        ws = (workspace or LayerStepWorkspace()).get(nbytes, dev, q_heads)
     output = torch.empty_like(qc) if out is None else out
     kk = min(budget - 1, tokens)
     idx = torch.empty((q_heads, kk + 1), device=dev, dtype=torch.int64) if return_indices else None

@@ -19,12 +19,34 @@ from . import _native as nat
 MAX_SELECT_TOKENS = 131072
 
 
+# Reusable workspaces, one per (device, stream): the native select keeps
+# per-row histograms at the start of the workspace (1 KiB per row), needs
+# them zero when a call begins and leaves them zero, so a buffer is allocated
+# zeroed and only its histogram region is cleared when the row count changes
+# (the new region may cover keys a call with fewer rows left there).
+_WORKSPACES: dict[tuple[int, int], tuple[torch.Tensor, int]] = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int, rows: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    buf, last_rows = _WORKSPACES.get(key, (None, 0))
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 256), device=device, dtype=torch.uint8)
+    elif rows != last_rows:
+        buf[: min(buf.numel(), rows * 1024)].zero_()
+    _WORKSPACES[key] = (buf, rows)
+    return buf
+
+
 def _launch(scores2d: torch.Tensor, k: int, current: int, out: torch.Tensor) -> None:
     rows, tokens = (int(x) for x in scores2d.shape)
     with torch.cuda.device(scores2d.device):
+        stream = nat.stream_of(scores2d.device)
+        nbytes = int(nat.lib().popkv_topk_select_workspace_bytes(rows, tokens))
+        ws = _workspace(scores2d.device, int(stream or 0), nbytes, rows)
         nat.call("popkv_topk_select", scores2d.data_ptr(), rows, scores2d.stride(0), tokens, int(k), int(current),
                  out.data_ptr(), nat.INDEX_I64 if out.dtype == torch.int64 else nat.INDEX_I32, out.stride(0),
-                 nat.stream_of(scores2d.device))
+                 ws.data_ptr(), ws.numel(), stream)
 
 
 def _rows(scores: torch.Tensor) -> torch.Tensor:

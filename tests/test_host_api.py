@@ -267,9 +267,15 @@ def test_library_host_only_entry_points():
     fake = 0x1000
     st = lib.popkv_pack(fake, 2, 8, 10, 128, 1280, fake, fake, fake, fake, 12, 3, 64, 64, None)
     assert st == -2 and "capacity exceeded" in lib.popkv_last_error().decode()
-    st = lib.popkv_topk_select(fake, 4, 10, 10, 11, 10, fake, 0, 12, None)
+    ws_bytes = lib.popkv_topk_select_workspace_bytes(4, 100)
+    assert ws_bytes >= 4 * 256 * 4 + 4 * 128 * 2
+    st = lib.popkv_topk_select(fake, 4, 10, 10, 11, 10, fake, 0, 12, fake, ws_bytes, None)
     assert st == -1
-    st = lib.popkv_topk_select(fake, 4, 200000, 200000, 11, 10, fake, 0, 12, None)
+    st = lib.popkv_topk_select(fake, 4, 200000, 200000, 11, 10, fake, 0, 12, fake, 1 << 30, None)
     assert st == -4
+    st = lib.popkv_topk_select(fake, 4, 100, 100, 11, 10, fake, 0, 12, None, ws_bytes, None)
+    assert st == -1 and "null" in lib.popkv_last_error().decode()
+    st = lib.popkv_topk_select(fake, 4, 100, 100, 11, 10, fake, 0, 12, fake, ws_bytes - 1, None)
+    assert st == -6 and "workspace" in lib.popkv_last_error().decode()
     with pytest.raises(RuntimeError, match="capacity exceeded"):
         _native.check(lib.popkv_pack(fake, 2, 8, 10, 128, 1280, fake, fake, fake, fake, 12, 3, 64, 64, None))
