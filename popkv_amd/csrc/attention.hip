@@ -573,6 +573,93 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_current_kernel(
                     q + static_cast<int64_t>(h) * D, cur_k + kvh * D, cur_v + kvh * D, scale);
 }
 
+// API-path partial attention, fast form (head_dim 128, contiguous K/V rows,
+// the reference's 256-row splits, 16-byte aligned index rows): as in
+// attn_list_kernel, row slot q owns the split's entries [16q, 16q + 16) and
+// reads them with 16-byte loads, but the rows come from the caller's index
+// tensor (int32 or int64) with its validity mask and the current-token
+// convention of sparse_kernels.py:267-286 (an index equal to prefix_tokens
+// reads current_k / current_v; any other index is clamped into the cache).
+// Entries past `selected` are never read from the index tensor; dead or
+// masked rows re-read a clamped, in-bounds row with weight 0.
+template <typename T, typename IdxT, int NB>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial128_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
+    int64_t prefix_tokens, const T* __restrict__ cur_k, const T* __restrict__ cur_v, const IdxT* __restrict__ idx,
+    int64_t idx_stride, const uint8_t* __restrict__ valid, const int64_t* __restrict__ head_to_kv, int kv_heads,
+    int64_t selected, float scale, float* __restrict__ partials, int nsplit) {
+    constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves, SPLIT = kSplitRows;
+    constexpr int RPS = SPLIT / NSLOT;                                 // entries per row slot
+    constexpr int PER = 16 / static_cast<int>(sizeof(IdxT));          // indices per 16-byte load
+    static_assert(RPS == 16 && RPS % NB == 0, "16 entries per slot, NB per pass");
+    const int h = blockIdx.y;
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int slot = wave * SLOTS + lane / LPR;
+    const int dim0 = (lane % LPR) * 8;
+    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+
+    const int n_rows = static_cast<int>(min<int64_t>(SPLIT, selected - static_cast<int64_t>(s) * SPLIT));
+    const int r0 = slot * RPS;  // this slot's first row in the split
+    const int64_t e0 = static_cast<int64_t>(h) * idx_stride + static_cast<int64_t>(s) * SPLIT + r0;
+    int64_t tk[RPS];
+#pragma unroll
+    for (int c = 0; c < RPS; c += PER) {
+        if (r0 + c + PER <= n_rows) {
+            const uint4 u = *reinterpret_cast<const uint4*>(idx + e0 + c);
+            const IdxT* v = reinterpret_cast<const IdxT*>(&u);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) tk[c + i] = static_cast<int64_t>(v[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) tk[c + i] = r0 + c + i < n_rows ? static_cast<int64_t>(idx[e0 + c + i]) : 0;
+        }
+    }
+    uint32_t live = 0;  // bit j: row r0 + j exists and is not masked out
+#pragma unroll
+    for (int j = 0; j < RPS; ++j) live |= (r0 + j < n_rows ? 1u : 0u) << j;
+    if (valid != nullptr && live != 0u) {
+        if (r0 + RPS <= n_rows) {
+            const uint4 u = *reinterpret_cast<const uint4*>(valid + e0);
+            const uint8_t* b = reinterpret_cast<const uint8_t*>(&u);
+#pragma unroll
+            for (int j = 0; j < RPS; ++j) live &= ~((b[j] == 0 ? 1u : 0u) << j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < RPS; ++j)
+                if (r0 + j < n_rows && valid[e0 + j] == 0) live &= ~(1u << j);
+        }
+    }
+    Raw8<T> qr;
+    qr.load(q + static_cast<int64_t>(h) * D + dim0);
+    const T* kb = kc + kvh * k_hs + dim0;
+    const T* vb = vc + kvh * v_hs + dim0;
+    const T* ckp = cur_k + kvh * D + dim0;
+    const T* cvp = cur_v + kvh * D + dim0;
+
+    SoftmaxState st;
+    init_state(st);
+#pragma unroll
+    for (int p = 0; p < RPS / NB; ++p) {
+        Raw8<T> kr[NB], vr[NB];
+        bool lv[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int j = p * NB + b;
+            lv[b] = (live >> j) & 1u;
+            const int64_t t = tk[j];
+            const bool is_cur = lv[b] && t == prefix_tokens;
+            const int64_t tc = min(max(t, static_cast<int64_t>(0)), prefix_tokens - 1);
+            kr[b].load(is_cur ? ckp : kb + tc * D);
+            vr[b].load(is_cur ? cvp : vb + tc * D);
+        }
+        fold_rows<T, NB>(st, qr, kr, vr, lv, scale);
+    }
+    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
+}
+
 // Typed arguments of one partial-attention launch.
 template <typename T, typename IdxT>
 struct PartialArgs {
@@ -600,8 +687,29 @@ hipError_t launch_partial_lpr(const PartialArgs<T, IdxT>& a, hipStream_t stream)
     return hipGetLastError();
 }
 
+// The fast form's preconditions: head_dim 128, contiguous rows, 256-row
+// splits, 16-byte aligned q / K / V / current rows, index and mask rows.
+template <typename T, typename IdxT>
+bool partial128_ok(const PartialArgs<T, IdxT>& a) {
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    return a.d == 128 && a.k_ts == 128 && a.v_ts == 128 && a.split == kSplitRows && al(a.q) && al(a.kc) &&
+           al(a.vc) && al(a.ck) && al(a.cv) && (a.k_hs * static_cast<int64_t>(sizeof(T))) % 16 == 0 &&
+           (a.v_hs * static_cast<int64_t>(sizeof(T))) % 16 == 0 && al(a.idx) &&
+           (a.idx_stride * static_cast<int64_t>(sizeof(IdxT))) % 16 == 0 &&
+           (a.valid == nullptr || (al(a.valid) && a.idx_stride % 16 == 0));
+}
+
 template <typename T, typename IdxT>
 hipError_t launch_partial_t(const PartialArgs<T, IdxT>& a, hipStream_t stream) {
+    if (partial128_ok(a)) {
+        const int nsplit = static_cast<int>((a.selected + a.split - 1) / a.split);
+        const float scale = static_cast<float>(1.0 / sqrt(128.0));
+        dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(a.qh));
+        hipLaunchKernelGGL((attn_partial128_kernel<T, IdxT, 8>), grid, dim3(kAttnThreads), 0, stream, a.q, a.kc, a.vc,
+                           a.k_hs, a.v_hs, a.prefix_tokens, a.ck, a.cv, a.idx, a.idx_stride, a.valid, a.h2k, a.kvh,
+                           a.selected, scale, a.partials, nsplit);
+        return hipGetLastError();
+    }
     if (a.d <= 64) return launch_partial_lpr<8>(a, stream);
     if (a.d <= 128) return launch_partial_lpr<16>(a, stream);
     return launch_partial_lpr<32>(a, stream);

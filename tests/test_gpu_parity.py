@@ -483,3 +483,33 @@ def test_c1_full_size_parity():
     start = L - (L % 64)
     for a, b in zip(cache.packed, want_tail):
         assert np.array_equal(bits(a)[:, start:L + 1], b)
+
+
+def test_topk_workspace_reused_across_row_counts():
+    """The select keeps per-row histograms at the start of its workspace; a
+    call with more rows than the last one must not see the keys a smaller
+    call left there (the Python wrapper clears the larger region)."""
+    for rows, tokens, seed in ((32, 5000, 1), (8, 3000, 2), (32, 5000, 3), (40, 700, 4)):
+        s = _scores("random", rows, tokens, seed=seed)
+        for k in (1, 257, tokens - 1):
+            ours = topk.topk_indices(s, k).cpu().numpy()
+            ref = torch.topk(s, k, dim=-1, sorted=False).indices.cpu().numpy()
+            for r in range(rows):
+                assert set(ours[r].tolist()) == set(ref[r].tolist()), (rows, tokens, k, r)
+
+
+def test_layer_step_workspace_reused_across_head_counts():
+    """One LayerStepWorkspace serving steps with 8 and then 32 query heads
+    (and back) gives each step the oracle's indices and output."""
+    ws = popkv.LayerStepWorkspace()
+    for q_heads, kv_heads, context, seed in ((8, 2, 3000, 21), (32, 8, 3000, 22), (8, 2, 5000, 23)):
+        base = workloads.scaled(workloads.C1, context=context, budget=700)
+        w = workloads.Workload(base.name, base.method, q_heads, kv_heads, 128, context, 700, base.token_group,
+                               base.dim_group, torch.bfloat16, seed, True)
+        layer, mapping, cache = _layer_setup(w)
+        sc, idx, out = _oracle_step(w, layer, mapping, cache)
+        o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                        layer.current_v(), mapping, budget=w.budget, workspace=ws,
+                                        return_indices=True)
+        assert np.array_equal(got.cpu().numpy(), idx), (q_heads, context)
+        np.testing.assert_allclose(f32(o), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
