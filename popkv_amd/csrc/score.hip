@@ -80,11 +80,23 @@ __global__ __launch_bounds__(kWave) void query_encode_kernel(
         float ls = 0.0f, hs = 0.0f;
         int ln = 0, hn = 0;
         if constexpr (ORDER == POPKV_ENCODE_FOLD) {
-            for (int i = start; i < end; ++i) {
-                const float x = s_q[i];
+            // Branch-free ascending fold: every dimension adds |x| to its
+            // bucket and +0 to the other, which leaves that sum unchanged
+            // (the sums start at +0 and only grow), so the result is the
+            // reference's sequential fold.  Unrolled by 8 so the LDS reads of
+            // a batch are in flight together.
+#pragma unroll 8
+            for (int j = 0; j < G; ++j) {
+                const int i = start + j;
+                const bool in = i < end;
+                const float x = in ? s_q[min(i, 255)] : 0.0f;
                 const bool sg = x >= 0.0f;
-                const bool mg = sg ? x > pos : x < neg;
-                if (mg) { hs += fabsf(x); ++hn; } else { ls += fabsf(x); ++ln; }
+                const bool mg = in && (sg ? x > pos : x < neg);
+                const float a = fabsf(x);
+                ls = ls + ((in && !mg) ? a : 0.0f);
+                hs = hs + (mg ? a : 0.0f);
+                ln += (in && !mg) ? 1 : 0;
+                hn += mg ? 1 : 0;
             }
         } else {
             float xl[G], xh[G];
@@ -349,42 +361,58 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
         for (int r = 0; r < R; ++r) pk[it][r] = rep_popc<G>(km[it], r);
     }
     for (int h = 0; h < qpk; ++h) {
-        // The group state is uniform: readfirstlane keeps it in SGPRs, read
-        // once per head.
+        // The group state is uniform but stays in vector registers (plain LDS
+        // broadcast reads): a three-operand bit op on the two query planes
+        // and a key plane may read only one scalar register, so scalar
+        // copies would cost a move per use.
         uint32_t qs[4], qm[4];
         float ql[R], dq[R];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            qs[w] = __builtin_amdgcn_readfirstlane(st.qs[h][w]);
-            qm[w] = __builtin_amdgcn_readfirstlane(st.qm[h][w]);
+            qs[w] = st.qs[h][w];
+            qm[w] = st.qm[h][w];
         }
         int pq[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            ql[r] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.ql[h][r])));
-            dq[r] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, st.qd[h][r])));
+            ql[r] = st.ql[h][r];
+            dq[r] = st.qd[h][r];
             pq[r] = rep_popc<G>(qm, r);
+        }
+        uint16_t* srow = scores + (qrow0 + h) * out_stride;
+        // every token's score first, without a branch (a token past the end
+        // scores the clamped last row and is not stored), so the tokens'
+        // independent chains interleave
+        float scs[TPT];
+#pragma unroll
+        for (int it = 0; it < TPT; ++it) {
+            float total = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) total = total + rep_term<G>(qs, qm, ks[it], km[it], r, pq[r], pk[it][r], ql[r], dq[r],
+                                                           kl[it][r], dk[it][r]);
+            scs[it] = total * 0x1.6a09e6p-4f;  // fp32(1/sqrt(128)) = 0x3DB504F3
         }
 #pragma unroll
         for (int it = 0; it < TPT; ++it) {
             const int64_t t = tok[it];
             if (t >= tokens) break;
-            float total = 0.0f;
-#pragma unroll
-            for (int r = 0; r < R; ++r) total = total + rep_term<G>(qs, qm, ks[it], km[it], r, pq[r], pk[it][r], ql[r], dq[r],
-                                                           kl[it][r], dk[it][r]);
-            const float sc = total * 0x1.6a09e6p-4f;  // fp32(1/sqrt(128)) = 0x3DB504F3
+            const float sc = scs[it];
             const uint16_t bits = f16_rne(sc);
+            const uint32_t off = static_cast<uint32_t>(t);  // tokens < 2^31
             if constexpr (STEP) {
-                // order_key(bits), with the NaN test done on the fp32 value
-                // (an fp32 NaN is exactly an fp16 NaN after the conversion)
+                // order_key(bits): bits 0..14 flip with the sign (s = 0 or
+                // all ones), bit 15 always flips; the bits above 15 are left
+                // as garbage (the store keeps 16 bits, the histogram takes
+                // bits 8..15).  The NaN test is done on the fp32 value (an
+                // fp32 NaN is exactly an fp16 NaN after the conversion).
                 const uint32_t b = bits;
-                const uint32_t flip = (static_cast<uint32_t>(static_cast<int32_t>(b << 16) >> 31) & 0xffffu) | 0x8000u;
-                const uint32_t key = sc != sc ? 0xffffu : (b ^ flip);
-                scores[(qrow0 + h) * out_stride + t] = static_cast<uint16_t>(key);
-                atomicAdd(&s_hist[h][key >> 8], 1u);
+                const uint32_t sgn = static_cast<uint32_t>(static_cast<int32_t>(b << 16) >> 31);
+                const uint32_t flipped = ((b ^ sgn) & 0x7fffu) | (~b & ~0x7fffu);
+                const uint32_t key = sc != sc ? 0xffffu : flipped;
+                srow[off] = static_cast<uint16_t>(key);
+                atomicAdd(&s_hist[h][(key >> 8) & 0xffu], 1u);
             } else {
-                scores[(qrow0 + h) * out_stride + t] = bits;
+                srow[off] = bits;
             }
         }
     }
