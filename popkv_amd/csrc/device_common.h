@@ -129,6 +129,32 @@ __device__ __forceinline__ uint32_t order_key(uint32_t h) {
     return nan ? 0xffffu : k;
 }
 
+// Raw storage of 8 consecutive elements: one 16-byte packet for 16-bit types,
+// two for float32.  Rows stay packed in registers until they are consumed.
+template <typename T> struct Raw8 {
+    uint4 u;
+    __device__ __forceinline__ void load(const T* p) { u = *reinterpret_cast<const uint4*>(p); }
+    __device__ __forceinline__ void zero() { u = make_uint4(0u, 0u, 0u, 0u); }
+    __device__ __forceinline__ float get(int i) const {
+        const uint32_t w = i < 2 ? u.x : i < 4 ? u.y : i < 6 ? u.z : u.w;
+        const uint32_t h = (i & 1) ? (w >> 16) : (w & 0xffffu);
+        return Elem<T>::kDtype == POPKV_DTYPE_BF16 ? bits_bf16(h) : bits_f16(h);
+    }
+};
+template <> struct Raw8<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = reinterpret_cast<const float4*>(p)[0];
+        b = reinterpret_cast<const float4*>(p)[1];
+    }
+    __device__ __forceinline__ void zero() { a = make_float4(0.f, 0.f, 0.f, 0.f); b = a; }
+    __device__ __forceinline__ float get(int i) const {
+        const float4& x = i < 4 ? a : b;
+        const int j = i & 3;
+        return j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
+    }
+};
+
 // ---- wave / block reductions --------------------------------------------
 
 // Wave-wide max / min / sum, the result in every lane.  max and min are

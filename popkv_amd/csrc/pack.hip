@@ -21,6 +21,8 @@
 // :376-500 (fused G16/G64, head_dim 128), :283-374 (generic G16/G64), with
 // output rows token_offset + t (the in-place append of :1075-1092,
 // :1177-1206).
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -258,6 +260,83 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     // bucket.  G64 adds dims j and j+32 (its two plane words) before the
     // halving tree; G32 / G16 reduce within one word.
     const int c0 = wave * CH;
+    if constexpr (G == 64) {
+        // G64: wave w owns rep w (dims c0 .. c0+63, plane words 2w, 2w+1).
+        // The production tree pairs dim j with j+32 and then halves, so its
+        // first level pairs (i, i+32) with (i+16, i+48); iteration i takes
+        // those four dimensions and leaves z[i] = (x[i] + x[i+32]) +
+        // (x[i+16] + x[i+48]) -- the same additions as the plain order, with
+        // 16 partial sums live instead of 64 contributions.  Bits are placed
+        // at their positions directly.  The row stays packed (8 x 16 bytes).
+        for (int t = lane; t < n; t += kWave) {
+            const T* row = base + static_cast<int64_t>(t) * D + c0;
+            const int64_t orow = kvh * cap + offset + gs + t;
+            Raw8<T> raw[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) raw[c].load(row + 8 * c);
+            uint32_t sw0 = 0, mw0 = 0, sw1 = 0, mw1 = 0;
+            // z(i): dims i, i+16, i+32, i+48 -> (low, high) level-16 sums;
+            // i is a compile-time constant (the row registers are indexed
+            // statically)
+            auto z = [&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                float xl[4], xh[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int dm = i + 16 * q;
+                    // the empty asm ties the thresholds to the bit words:
+                    // read one dimension at a time, not all hoisted
+                    float hi = s_hi[c0 + dm], nlo = s_nlo[c0 + dm];
+                    asm volatile("" : "+v"(hi), "+v"(nlo), "+v"(sw0), "+v"(sw1));
+                    const float v = raw[dm / 8].get(dm % 8);
+                    const float a = fabsf(v);
+                    const bool sg = v >= 0.0f;
+                    const bool mg = a > (sg ? hi : nlo);  // as in the plain path below
+                    const int bit = dm & 31;
+                    if (q < 2) {
+                        sw0 |= static_cast<uint32_t>(sg) << bit;
+                        mw0 |= static_cast<uint32_t>(mg) << bit;
+                    } else {
+                        sw1 |= static_cast<uint32_t>(sg) << bit;
+                        mw1 |= static_cast<uint32_t>(mg) << bit;
+                    }
+                    xl[q] = mg ? 0.0f : a;
+                    xh[q] = mg ? a : 0.0f;
+                }
+                return make_float2((xl[0] + xl[2]) + (xl[1] + xl[3]), (xh[0] + xh[2]) + (xh[1] + xh[3]));
+            };
+            auto add2 = [](float2 u, float2 w) { return make_float2(u.x + w.x, u.y + w.y); };
+            using std::integral_constant;
+            // the halving tree over z(0..15) (levels 8, 4, 2, 1), evaluated
+            // depth-first so only a few partial sums are live
+            auto a8 = [&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                const float2 u = z(integral_constant<int, i>{});
+                return add2(u, z(integral_constant<int, i + 8>{}));
+            };
+            auto b4 = [&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                const float2 u = a8(integral_constant<int, i>{});
+                return add2(u, a8(integral_constant<int, i + 4>{}));
+            };
+            auto c2 = [&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                const float2 u = b4(integral_constant<int, i>{});
+                return add2(u, b4(integral_constant<int, i + 2>{}));
+            };
+            const float2 c0s = c2(integral_constant<int, 0>{});
+            const float2 sums = add2(c0s, c2(integral_constant<int, 1>{}));
+            const int hn = __popc(mw0) + __popc(mw1);
+            float lo, de;
+            finish_rep(sums.x, 64 - hn, sums.y, hn, lo, de);
+            const int w0 = c0 / 32;
+            *reinterpret_cast<uint2*>(k_sign + orow * 4 + w0) = make_uint2(sw0, sw1);
+            *reinterpret_cast<uint2*>(k_mag + orow * 4 + w0) = make_uint2(mw0, mw1);
+            k_low[orow * R + wave] = f16_rne(lo);
+            k_delta[orow * R + wave] = f16_rne(de);
+        }
+        return;
+    }
     for (int t = lane; t < n; t += kWave) {
         const T* row = base + static_cast<int64_t>(t) * D + c0;
         const int64_t orow = kvh * cap + offset + gs + t;
