@@ -531,20 +531,70 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_gqa_kernel(
 }
 
 // Layer-step merge: the split states of head h plus the current token
-// (logit q.cur_k * scale, value cur_v), written in the query dtype.
+// (logit q.cur_k * scale, value cur_v), written in the query dtype.  One
+// wave per head, lane l owning dims l and l + 64, and no LDS or barrier:
+// the split maxima and denominators are wave reductions (lane s holds split
+// s of each 64-split chunk), the weights reach the accumulation through
+// readlane, and every split state is loaded in batches of 8 before it is
+// used.
+constexpr int kMergeStepBatch = 8;
+
 template <typename T>
-__global__ __launch_bounds__(kMergeThreads) void attn_merge_current_kernel(
+__global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
     const T* __restrict__ cur_v, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
     T* __restrict__ out) {
-    constexpr int D = 128;
+    constexpr int D = 128, S = D + 2;
     const int h = blockIdx.x;
+    const int lane = threadIdx.x;
     // no mapping: the plain GQA grouping of the dense layers
     const int64_t kvh = head_to_kv != nullptr
                             ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
                             : h / (static_cast<int>(gridDim.x) / kv_heads);
-    merge_splits<T>(partials + static_cast<int64_t>(h) * nsplit * (D + 2), nsplit, D, out + static_cast<int64_t>(h) * D,
-                    q + static_cast<int64_t>(h) * D, cur_k + kvh * D, cur_v + kvh * D, scale);
+    const float* ps = partials + static_cast<int64_t>(h) * nsplit * S;
+    const T* qh = q + static_cast<int64_t>(h) * D;
+    const T* ck = cur_k + kvh * D;
+    const T* cv = cur_v + kvh * D;
+    const float q0 = Elem<T>::load(qh, lane), q1 = Elem<T>::load(qh, lane + 64);
+    const float k0 = Elem<T>::load(ck, lane), k1 = Elem<T>::load(ck, lane + 64);
+    const float v0 = Elem<T>::load(cv, lane), v1 = Elem<T>::load(cv, lane + 64);
+    // the splits' maxima with the current token's logit
+    const float cur_m = wave_sum(q0 * k0 + q1 * k1) * scale;
+    float mx = cur_m;
+    for (int s0 = 0; s0 < nsplit; s0 += kWave)
+        if (s0 + lane < nsplit) mx = fmaxf(mx, ps[static_cast<int64_t>(s0 + lane) * S]);
+    mx = wave_max(mx);
+    const float wc = __expf(cur_m - mx);
+    float den = 0.0f, num0 = wc * v0, num1 = wc * v1;
+    for (int s0 = 0; s0 < nsplit; s0 += kWave) {
+        float w = 0.0f;
+        if (s0 + lane < nsplit) {
+            const float m = ps[static_cast<int64_t>(s0 + lane) * S];
+            w = m == -INFINITY ? 0.0f : __expf(m - mx);
+            den += ps[static_cast<int64_t>(s0 + lane) * S + 1] * w;
+        }
+        const int n = min(kWave, nsplit - s0);
+        for (int b = 0; b < n; b += kMergeStepBatch) {
+            float a0[kMergeStepBatch], a1[kMergeStepBatch];
+#pragma unroll
+            for (int j = 0; j < kMergeStepBatch; ++j) {
+                const int64_t so = static_cast<int64_t>(s0 + min(b + j, n - 1)) * S + 2;
+                a0[j] = ps[so + lane];
+                a1[j] = ps[so + lane + 64];
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeStepBatch; ++j) {
+                if (b + j < n) {
+                    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b + j));
+                    num0 = fmaf(ws, a0[j], num0);
+                    num1 = fmaf(ws, a1[j], num1);
+                }
+            }
+        }
+    }
+    den = wave_sum(den) + wc;
+    Elem<T>::store(out + static_cast<int64_t>(h) * D, lane, num0 / den);
+    Elem<T>::store(out + static_cast<int64_t>(h) * D, lane + 64, num1 / den);
 }
 
 // API-path partial attention, fast form (head_dim 128, contiguous K/V rows,
@@ -780,7 +830,7 @@ hipError_t launch_merge_current_t(const float* partials, int nsplit, const void*
                                   const void* cur_v, const int64_t* h2k, int q_heads, int kv_heads, void* out,
                                   hipStream_t stream) {
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
-    hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kMergeThreads), 0,
+    hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kWave), 0,
                        stream, partials, nsplit, static_cast<const T*>(q), static_cast<const T*>(cur_k),
                        static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out));
     return hipGetLastError();
