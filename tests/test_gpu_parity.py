@@ -513,3 +513,33 @@ def test_layer_step_workspace_reused_across_head_counts():
                                         return_indices=True)
         assert np.array_equal(got.cpu().numpy(), idx), (q_heads, context)
         np.testing.assert_allclose(f32(o), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
+@pytest.mark.parametrize("tokens", [1000, 4095])
+def test_select_int32_output_through_the_c_abi(tokens):
+    """popkv_topk_select with int32 indices (row stride k + 3): the same
+    selection as the oracle, current token in slot k, padding untouched."""
+    s = _scores("peaked", 5, tokens, seed=31)
+    k = min(511, tokens)
+    out = torch.full((5, k + 3), -7, device=DEV, dtype=torch.int32)
+    nbytes = int(_native.lib().popkv_topk_select_workspace_bytes(5, tokens))
+    ws = torch.zeros(nbytes, device=DEV, dtype=torch.uint8)
+    with torch.cuda.device(DEV):
+        _native.call("popkv_topk_select", s.data_ptr(), 5, s.stride(0), tokens, k, 12345, out.data_ptr(),
+                     _native.INDEX_I32, out.stride(0), ws.data_ptr(), nbytes, _native.stream_of(s.device))
+    got = out.cpu().numpy()
+    want = core.select(bits(s), k, tokens)
+    assert np.array_equal(got[:, :k], want[:, :k])
+    assert (got[:, k] == 12345).all() and (got[:, k + 1:] == -7).all()
+
+
+def test_split_attention_unaligned_index_rows_take_the_general_kernel():
+    """701 int64 indices per head (rows not 16-byte aligned) use the general
+    kernel; 704 use the fast one; both match the oracle."""
+    for selected in (701, 704):
+        q, k, v, ck, cv, idx, mapping = _attn_case(q_heads=8, kv_heads=2, tokens=3000, selected=selected, seed=selected)
+        valid = torch.ones_like(idx, dtype=torch.bool)
+        valid[:, 5:9] = False
+        got = sparse_kernels.indexed_attention_split(q, k, v, ck, cv, idx, mapping, valid, split_tokens=256)
+        want = _oracle_attention(q, k, v, ck, cv, idx, mapping, valid)
+        np.testing.assert_allclose(f32(got), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
