@@ -37,18 +37,26 @@ __global__ __launch_bounds__(kWave) void query_encode_kernel(
     const int W = (d + 31) / 32;
     const int R = (d + G - 1) / G;
     __shared__ float s_q[256];
+    // fold order: each dimension's contribution to the low and to the high
+    // bucket (|q| or +0), and the magnitude words
+    __shared__ __align__(16) float s_lo[256], s_hi[256];
+    __shared__ uint32_t s_mag[8];
     const T* src = q + row * d;
 
     float mn = INFINITY, mx = -INFINITY;
     float v[4];
+    // all four loads in flight at once (a dimension past d re-reads d - 1)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) v[s] = Elem<T>::load(src, min(s * kWave + lane, d - 1));
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const int dim = s * kWave + lane;
-        v[s] = dim < d ? Elem<T>::load(src, dim) : 0.0f;
         if (dim < d) {
             s_q[dim] = v[s];
             mn = fminf(mn, v[s]);
             mx = fmaxf(mx, v[s]);
+        } else {
+            v[s] = 0.0f;
         }
     }
     mn = wave_min(mn);
@@ -62,6 +70,15 @@ __global__ __launch_bounds__(kWave) void query_encode_kernel(
         const bool mg = valid && (sg ? v[s] > pos : v[s] < neg);
         const uint64_t bs = __ballot(sg);
         const uint64_t bm = __ballot(mg);
+        if constexpr (ORDER == POPKV_ENCODE_FOLD) {
+            const float a = fabsf(v[s]);
+            s_lo[dim] = valid && !mg ? a : 0.0f;  // dims past d: +0 padding
+            s_hi[dim] = mg ? a : 0.0f;
+            if (lane == 0) {
+                s_mag[2 * s] = static_cast<uint32_t>(bm);
+                s_mag[2 * s + 1] = static_cast<uint32_t>(bm >> 32);
+            }
+        }
         if (lane == 0) {
             if (2 * s < W) {
                 q_sign[row * W + 2 * s] = static_cast<int32_t>(static_cast<uint32_t>(bs));
@@ -80,24 +97,24 @@ __global__ __launch_bounds__(kWave) void query_encode_kernel(
         float ls = 0.0f, hs = 0.0f;
         int ln = 0, hn = 0;
         if constexpr (ORDER == POPKV_ENCODE_FOLD) {
-            // Branch-free ascending fold: every dimension adds |x| to its
-            // bucket and +0 to the other, which leaves that sum unchanged
-            // (the sums start at +0 and only grow), so the result is the
-            // reference's sequential fold.  Unrolled by 8 so the LDS reads of
-            // a batch are in flight together.
-#pragma unroll 8
-            for (int j = 0; j < G; ++j) {
-                const int i = start + j;
-                const bool in = i < end;
-                const float x = in ? s_q[min(i, 255)] : 0.0f;
-                const bool sg = x >= 0.0f;
-                const bool mg = in && (sg ? x > pos : x < neg);
-                const float a = fabsf(x);
-                ls = ls + ((in && !mg) ? a : 0.0f);
-                hs = hs + (mg ? a : 0.0f);
-                ln += (in && !mg) ? 1 : 0;
-                hn += mg ? 1 : 0;
+            // the ascending fold over the contributions staged above (the
+            // other bucket's +0 leaves a sum unchanged: sums start at +0 and
+            // only grow), four values per LDS read
+            for (int j = start; j < end; j += 4) {
+                const float4 l4 = *reinterpret_cast<const float4*>(&s_lo[j]);
+                const float4 h4 = *reinterpret_cast<const float4*>(&s_hi[j]);
+                ls = ls + l4.x; ls = ls + l4.y; ls = ls + l4.z; ls = ls + l4.w;
+                hs = hs + h4.x; hs = hs + h4.y; hs = hs + h4.z; hs = hs + h4.w;
             }
+            for (int w = 0; w < 8; ++w) {  // the rep's magnitude bits
+                const int lo_bit = max(start, 32 * w), hi_bit = min(end, 32 * w + 32);
+                if (lo_bit >= hi_bit) continue;
+                const uint32_t word = s_mag[w];
+                const int nb = hi_bit - lo_bit;
+                const uint32_t sel = (nb == 32 ? 0xffffffffu : ((1u << nb) - 1u)) << (lo_bit - 32 * w);
+                hn += __popc(word & sel);
+            }
+            ln = (end - start) - hn;
         } else {
             float xl[G], xh[G];
 #pragma unroll
