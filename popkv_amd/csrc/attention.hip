@@ -628,15 +628,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial128_kernel(
     const int n_rows = static_cast<int>(min<int64_t>(SPLIT, selected - static_cast<int64_t>(s) * SPLIT));
     const int r0 = slot * RPS;  // this slot's first row in the split
     const int64_t e0 = static_cast<int64_t>(h) * idx_stride + static_cast<int64_t>(s) * SPLIT + r0;
+    // whole 16-byte packets first, all in flight before any is used; the
+    // split's ragged tail (rare) is read element by element afterwards
+    // (a packet past the split's rows re-reads the head's first packet: an
+    // index row holds a positive multiple of 16 bytes)
+    uint4 uc[RPS / PER];
+#pragma unroll
+    for (int c = 0; c < RPS; c += PER) {
+        const bool in = r0 + c + PER <= n_rows;
+        uc[c / PER] = *reinterpret_cast<const uint4*>(idx + (in ? e0 + c : static_cast<int64_t>(h) * idx_stride));
+    }
     int64_t tk[RPS];
 #pragma unroll
     for (int c = 0; c < RPS; c += PER) {
-        if (r0 + c + PER <= n_rows) {
-            const uint4 u = *reinterpret_cast<const uint4*>(idx + e0 + c);
-            const IdxT* v = reinterpret_cast<const IdxT*>(&u);
+        const IdxT* v = reinterpret_cast<const IdxT*>(&uc[c / PER]);
 #pragma unroll
-            for (int i = 0; i < PER; ++i) tk[c + i] = static_cast<int64_t>(v[i]);
-        } else {
+        for (int i = 0; i < PER; ++i) tk[c + i] = static_cast<int64_t>(v[i]);
+        if (r0 + c + PER > n_rows) {  // rows past n_rows are dead below
 #pragma unroll
             for (int i = 0; i < PER; ++i) tk[c + i] = r0 + c + i < n_rows ? static_cast<int64_t>(idx[e0 + c + i]) : 0;
         }

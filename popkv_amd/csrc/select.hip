@@ -78,12 +78,14 @@ __global__ __launch_bounds__(kKeyHistThreads) void key_hist_kernel(const uint16_
             w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
             w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
         } else {
+            // element loads, all issued before use (indices past the row's
+            // end re-read its last element and are not counted below)
+            const int64_t last = tokens - 1 - t0;
+            uint32_t e[kKeyHistTokens];
 #pragma unroll
-            for (int i = 0; i < kKeyHistTokens / 2; ++i) {
-                const uint32_t lo = t0 + 2 * i < tokens ? src[2 * i] : 0u;
-                const uint32_t hi = t0 + 2 * i + 1 < tokens ? src[2 * i + 1] : 0u;
-                w[i] = lo | (hi << 16);
-            }
+            for (int i = 0; i < kKeyHistTokens; ++i) e[i] = src[min(static_cast<int64_t>(i), last)];
+#pragma unroll
+            for (int i = 0; i < kKeyHistTokens / 2; ++i) w[i] = e[2 * i] | (e[2 * i + 1] << 16);
         }
         uint32_t kw[kKeyHistTokens / 2];
 #pragma unroll
@@ -185,11 +187,19 @@ __global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
         const uint16_t* rowp = src;
         if (RELOAD) asm volatile("" : "+s"(rowp) : "v"(after) : "memory");
         const uint16_t* seg = rowp + begin;
+        // every chunk's load is issued before any is used (a chunk past
+        // the segment's tokens re-reads the row's first chunk and is then
+        // zeroed), so the loads share one memory latency
+        uint4 uc[KW / 4];
 #pragma unroll
         for (int c = 0; c < KW / 4; ++c) {
             const int e0 = 8 * (c0 + c);
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (e0 < n) u = *reinterpret_cast<const uint4*>(seg + e0);
+            uc[c] = *reinterpret_cast<const uint4*>(e0 < n ? seg + e0 : rowp);
+        }
+#pragma unroll
+        for (int c = 0; c < KW / 4; ++c) {
+            const int e0 = 8 * (c0 + c);
+            uint4 u = uc[c];
             if (e0 + 8 > n) {  // the segment's tail: keys e >= n read as 0
                 const int v = n - e0;  // keys of this chunk that exist (may be <= 0)
                 u.x &= (v > 1 ? 0xffffffffu : 0u) | (v > 0 ? 0x0000ffffu : 0u);
