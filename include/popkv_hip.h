@@ -155,7 +155,8 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
 /* One decode step of one sparse layer (batch 1, head_dim 128): query encode,
  * popcount score over `tokens` cached tokens, per-head top-k with
  * k = min(budget-1, tokens) plus the current token (index `tokens`), and
- * 256-token split sparse attention with the log-sum-exp merge.
+ * split sparse attention with the log-sum-exp merge (the splits are token
+ * chunks of the cache, each attending over its selected tokens).
  * queries/prefix/current K/V share `dtype`; output [QH, 128] has `dtype`.
  * indices_out (int64 [QH, k+1]) may be NULL; when given, the selection is
  * also written there.  Needs popkv_layer_step_workspace_bytes() bytes of
@@ -180,10 +181,11 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* output, int64_t* indices_out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
-/* Re-runs only the sparse-attention kernel of the last popkv_layer_step that
- * used `workspace` (same shapes and budget): it reads the selection lists the
- * step left there and rewrites the split partials, touching nothing else, so
- * it can be repeated.  For timing the step's dominant kernel on its own; no
+/* Re-runs only the fused select + sparse-attention kernel of the last
+ * popkv_layer_step that used `workspace` (same shapes and budget): it reads
+ * the order keys and threshold histograms the step left there and rewrites
+ * the chunk partials (and re-zeroes the already zero key histograms), so it
+ * can be repeated.  For timing the step's dominant kernel on its own; no
  * counterpart in the reference. */
 int popkv_layer_step_attention(const void* queries, int32_t dtype,
                                const void* prefix_k, const void* prefix_v,

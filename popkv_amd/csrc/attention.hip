@@ -29,6 +29,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "select_common.h"
 
 namespace popkv {
 namespace {
@@ -345,17 +346,12 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
 
 // ---------------------------------------------------------------- layer step
 
-// Layer-step attention.  The select kernel leaves each head's k selected
-// tokens as an ascending int32 list.  Workgroup (s, h) takes list entries
-// [256s, 256s + 256) -- the reference's 256-token split -- so every
-// workgroup gathers the same number of rows.  Row slot q (16 lanes, one
-// 16-byte slice of a 256-byte row each) owns the 16 consecutive entries
-// [16q, 16q + 16) of the split and reads them with four 16-byte loads, so the
-// first gathers wait on a single short load.  The current token is not in
-// the list; the merge adds it.  Rows are contiguous (token stride = head_dim
-// = 128).  For 16-bit types the Q.K products use v_dot2 (two products
-// accumulated in fp32 per instruction).
-constexpr int kSplitRows = 256;  // selected tokens per workgroup
+// Layer-step attention.  Row slot q of a workgroup (16 lanes, one 16-byte
+// slice of a 256-byte row each) gathers batches of consecutive selected
+// rows; the current token is not among them (the merge adds it).  Rows are
+// contiguous (token stride = head_dim = 128).  For 16-bit types the Q.K
+// products use v_dot2 (two products accumulated in fp32 per instruction).
+constexpr int kSplitRows = 256;  // the reference's split: selected tokens per workgroup
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -402,6 +398,10 @@ __device__ __forceinline__ void fold_rows(SoftmaxState& st, const Raw8<T>& qr, c
         logit[b] = live[b] ? dot * scale : -INFINITY;
         bm = fmaxf(bm, logit[b]);
     }
+    // The compiler sinks the V loads into this branch, so a batch's V rows
+    // are requested only once its K rows have arrived.  A branch-free form
+    // with every K and V request in flight at once measured slower on the
+    // layer step's gathers (C1 select + attention kernel 18.6 vs 17.1 us).
     const float mnew = fmaxf(st.m, bm);
     if (mnew != -INFINITY) {
         const float alpha = __expf(st.m - mnew);  // st.m = -inf gives 0
@@ -419,62 +419,175 @@ __device__ __forceinline__ void fold_rows(SoftmaxState& st, const Raw8<T>& qr, c
     }
 }
 
-template <typename T, int NB, int SPLIT = kSplitRows>
-__global__ __launch_bounds__(kAttnThreads) void attn_list_kernel(
+// Layer step: the select's second half fused with the sparse attention.
+// Block (c, h) owns chunk c of head h's key row (kChunkThreads * KPT tokens,
+// KPT per thread):
+//   1. the threshold: from the chunk histograms of chunk_hist_kernel
+//      (thread u sums bin u over every chunk and over the chunks before c),
+//      bin t2 of the low byte -> T = b1:t2, need_eq = ties taken in the row,
+//      eq_before = ties in earlier chunks (lowest index first: PyTorch's
+//      gather-top-k rule);
+//   2. the chunk's selected tokens (every key > T, the ties whose row rank
+//      is below need_eq; with k >= tokens every token) compacted in
+//      ascending order into LDS, and into idx_out[h][rank] as int64 when
+//      idx_out is non-null (rank = selected tokens before it in the row);
+//   3. attention over them: 16 row slots, each taking NB consecutive
+//      entries per pass, all NB K/V gathers in flight before any is used;
+//   4. (m, l, acc[128]) to partials[h][c] (m = -inf for an empty chunk).
+// Block 0 of each head re-zeroes the scorer's histogram ghist[h] (its last
+// reader, chunk_hist_kernel, has finished).
+template <typename T, int KPT, int NB>
+__global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
-    const int32_t* __restrict__ list, int64_t list_stride, int64_t tokens, int64_t k,
-    const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials, int nsplit) {
+    const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
+    const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, uint32_t* __restrict__ ghist,
+    const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials,
+    int64_t* __restrict__ idx_out, int64_t idx_stride) {
+    static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
     constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
-    constexpr int RPS = SPLIT / NSLOT;  // list entries per row slot
-    static_assert(RPS % 4 == 0 && RPS % NB == 0, "a slot's entries are read as 16-byte packets, NB per pass");
+    constexpr int CH = kChunkThreads * KPT;
+    constexpr int PASS = NSLOT * NB;  // entries per pass
+    static_assert(NB % 8 == 0, "a slot's entries of one pass are whole 16-byte LDS reads");
+    const int c = blockIdx.x;
     const int h = blockIdx.y;
-    const int s = blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
     const int slot = wave * SLOTS + lane / LPR;
     const int dim0 = (lane % LPR) * 8;
-    const int64_t kvh = min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);  // none / every token / threshold
 
-    // this slot's list entries first (the gathers depend on them), then the
-    // query slice
-    const int n_rows = static_cast<int>(min<int64_t>(SPLIT, k - static_cast<int64_t>(s) * SPLIT));
-    const int32_t* lrow = list + static_cast<int64_t>(h) * list_stride + static_cast<int64_t>(s) * SPLIT + slot * RPS;
-    int32_t tk[RPS];
-#pragma unroll
-    for (int i = 0; i < RPS; i += 4) {
-        const int4 v = *reinterpret_cast<const int4*>(lrow + i);
-        tk[i] = v.x;
-        tk[i + 1] = v.y;
-        tk[i + 2] = v.z;
-        tk[i + 3] = v.w;
-    }
+    // 0. loads, all issued before any is used: this thread's keys, the query
+    //    slice, the head's KV mapping and the threshold state.  The mapping
+    //    and the record are read with vector loads at a lane-opaque zero
+    //    offset: as scalar loads they would be waited for together with the
+    //    kernel arguments, before the chunk histograms are even issued.
+    int z = 0;
+    asm volatile("" : "+v"(z));
+    const int begin = c * CH + tid * KPT;
+    const int n = max(0, min(KPT, ntok - begin));
+    ChunkKeys<KPT> kk;
+    load_chunk_keys<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, n, kk);
     Raw8<T> qr;
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
+    const int64_t map = head_to_kv[h + z];
+    __shared__ uint32_t s_g2[256], s_p2[256];
+    __shared__ uint32_t s_scan[kAttnWaves];
+    __shared__ __align__(16) uint16_t s_list[CH];
+    uint32_t thr = 0, need_eq = 0, eq_before = 0, rank0 = 0;
+    if (mode == 2) {
+        const uint32_t b1 = rec[4 * h + z], above1 = rec[4 * h + 1 + z];
+        const uint16_t* hr = h2 + static_cast<int64_t>(h) * nchunks * 256 + tid;
+        uint32_t g2 = 0, p2 = 0;  // bin tid over every chunk / over chunks before c
+        for (int c0 = 0; c0 < nchunks; c0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = hr[static_cast<int64_t>(min(c0 + j, nchunks - 1)) * 256];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t x = c0 + j < nchunks ? v[j] : 0u;
+                g2 += x;
+                p2 += c0 + j < c ? x : 0u;
+            }
+        }
+        uint32_t gt1_before = 0;  // keys above bin b1 in earlier chunks
+        if (idx_out != nullptr) {
+            for (int c0 = 0; c0 < c; c0 += kWave) {
+                const uint32_t x = c0 + lane < c ? gt1[static_cast<int64_t>(h) * nchunks + c0 + lane] : 0u;
+                gt1_before += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
+            }
+        }
+        s_g2[tid] = g2;
+        s_p2[tid] = p2;
+        __syncthreads();
+        uint32_t cnt[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cnt[i] = s_g2[255 - (4 * lane + i)];
+        const uint32_t need1 = static_cast<uint32_t>(k) - above1;
+        uint32_t t2, above2;
+        wave_find_bin(cnt, need1, &t2, &above2);
+        thr = (b1 << 8) | t2;  // >= 0x03ff
+        need_eq = need1 - above2;
+        eq_before = s_p2[t2];
+        if (idx_out != nullptr) {
+            // keys of bin b1 with low byte > t2 in earlier chunks
+            uint32_t x = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x += 4 * lane + i > static_cast<int>(t2) ? s_p2[4 * lane + i] : 0u;
+            const uint32_t gt2_before =
+                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
+            rank0 = gt1_before + gt2_before + min(eq_before, need_eq);
+        }
+    } else if (mode == 1) {
+        rank0 = static_cast<uint32_t>(c * CH);
+    }
+
+    // 1. the chunk's selection masks and their ranks
+    uint32_t m_gt = 0u, m_eq = 0u;
+    if (mode == 2) key_masks<KPT>(kk, thr, &m_gt, &m_eq);
+    else if (mode == 1) m_gt = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
+    const uint32_t n_eq = static_cast<uint32_t>(__popc(m_eq));
+    uint32_t total;
+    const uint32_t packed =
+        block_excl_scan_once(static_cast<uint32_t>(__popc(m_gt)) | (n_eq << 16), s_scan, kAttnWaves, &total);
+    // ties taken by earlier chunks / before this thread / by this thread
+    // (each min is formed before the subtraction that uses it, which then
+    // never wraps)
+    const uint32_t prior = min(eq_before, need_eq);
+    const uint32_t t_before = min(eq_before + (packed >> 16), need_eq);
+    const uint32_t t_end = min(eq_before + (total >> 16), need_eq);
+    uint32_t take = min(n_eq, need_eq - t_before);
+    const int n_sel = static_cast<int>((total & 0xffffu) + (t_end - prior));
+    uint32_t pos = (packed & 0xffffu) + (t_before - prior);
+    uint32_t ties = m_eq;
+    if (take < n_eq) {  // keep only the first `take` ties
+        uint32_t rest = ties;
+        for (uint32_t j = 0; j < take; ++j) rest &= rest - 1u;
+        ties &= ~rest;
+    }
+    int64_t* irow = idx_out != nullptr ? idx_out + static_cast<int64_t>(h) * idx_stride : nullptr;
+    for (uint32_t m = m_gt | ties; m != 0u; m &= m - 1u) {
+        const int e = tid * KPT + __builtin_ctz(m);
+        if (pos < static_cast<uint32_t>(CH)) s_list[pos] = static_cast<uint16_t>(e);
+        if (irow != nullptr && rank0 + pos < static_cast<uint32_t>(k)) irow[rank0 + pos] = c * CH + e;
+        ++pos;
+    }
+    if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
+    __syncthreads();
+
+    // 2. attention over s_list[0, n_sel)
+    const int64_t kvh = min(max(map, static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
     const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
     const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
-    // entries past the split's rows are never dereferenced: their slot reads
-    // token 0 with weight 0; list values are clamped into the cache
-    const uint32_t tmax = static_cast<uint32_t>(tokens - 1);
-
+    const uint32_t t0 = static_cast<uint32_t>(c * CH);
+    const uint32_t tmax = static_cast<uint32_t>(ntok - 1);  // a selected token is < ntok; clamped all the same
     SoftmaxState st;
     init_state(st);
+    for (int base = 0; base < n_sel; base += PASS) {
+        const int e0 = base + slot * NB;  // a multiple of 8: 16-byte aligned
+        uint32_t ew[NB / 2];
 #pragma unroll
-    for (int p = 0; p < RPS / NB; ++p) {
+        for (int j = 0; j < NB / 8; ++j) {
+            const uint4 ev = *reinterpret_cast<const uint4*>(&s_list[min(e0 + 8 * j, CH - 8)]);
+            ew[4 * j] = ev.x;
+            ew[4 * j + 1] = ev.y;
+            ew[4 * j + 2] = ev.z;
+            ew[4 * j + 3] = ev.w;
+        }
         Raw8<T> kr[NB], vr[NB];
         bool live[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const int j = p * NB + b;
-            live[b] = slot * RPS + j < n_rows;
-            const uint32_t t = live[b] ? min(static_cast<uint32_t>(tk[j]), tmax) : 0u;
+            live[b] = e0 + b < n_sel;
+            // dead rows re-read the chunk's first token with weight 0
+            const uint32_t t = min(t0 + (live[b] ? ((ew[b / 2] >> ((b & 1) * 16)) & 0xffffu) : 0u), tmax);
             const uint32_t off = t * (D * sizeof(T));
             kr[b].load(reinterpret_cast<const T*>(kb + off));
             vr[b].load(reinterpret_cast<const T*>(vb + off));
         }
         fold_rows<T, NB>(st, qr, kr, vr, live, scale);
     }
-    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nsplit + s) * (D + 2));
+    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2));
 }
 
 // Dense attention (the reference's full layers, popkv.py:1022-1038): every
@@ -543,10 +656,12 @@ template <typename T>
 __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
     const T* __restrict__ cur_v, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
-    T* __restrict__ out) {
+    T* __restrict__ out, int64_t* __restrict__ idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current) {
     constexpr int D = 128, S = D + 2;
     const int h = blockIdx.x;
     const int lane = threadIdx.x;
+    // the current token's index slot of the layer step's int64 indices
+    if (idx_out != nullptr && lane == 0) idx_out[static_cast<int64_t>(h) * idx_stride + idx_slot] = current;
     // no mapping: the plain GQA grouping of the dense layers
     const int64_t kvh = head_to_kv != nullptr
                             ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
@@ -598,9 +713,9 @@ __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
 }
 
 // API-path partial attention, fast form (head_dim 128, contiguous K/V rows,
-// the reference's 256-row splits, 16-byte aligned index rows): as in
-// attn_list_kernel, row slot q owns the split's entries [16q, 16q + 16) and
-// reads them with 16-byte loads, but the rows come from the caller's index
+// the reference's 256-row splits, 16-byte aligned index rows): row slot q
+// owns the split's entries [16q, 16q + 16) and reads them with 16-byte
+// loads; the rows come from the caller's index
 // tensor (int32 or int64) with its validity mask and the current-token
 // convention of sparse_kernels.py:267-286 (an index equal to prefix_tokens
 // reads current_k / current_v; any other index is clamped into the cache).
@@ -821,62 +936,83 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
 
 namespace {
 template <typename T>
-hipError_t launch_list_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs,
-                         const int32_t* list, int64_t list_stride, int64_t tokens, int64_t k, int nsplit,
-                         const int64_t* h2k, int q_heads, int kv_heads, float* partials, hipStream_t stream) {
-    constexpr int NB = 8;  // 8 rows in flight per lane: two passes cover a slot's 16 entries
+hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs,
+                                  const uint16_t* keys, int64_t key_stride, int64_t tokens, int64_t k,
+                                  const uint32_t* rec, const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
+                                  const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
+                                  int64_t idx_stride, hipStream_t stream) {
+    constexpr int NB = 8;
+    const StepChunks ch = step_chunks(tokens, k);
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
-    dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(q_heads));
-    hipLaunchKernelGGL((attn_list_kernel<T, NB>), grid, dim3(kAttnThreads), 0, stream, static_cast<const T*>(q),
-                       static_cast<const T*>(kc), static_cast<const T*>(vc), k_hs, v_hs, list, list_stride, tokens, k,
-                       h2k, kv_heads, scale, partials, nsplit);
+    const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
+    dim3 grid(static_cast<unsigned>(ch.count), static_cast<unsigned>(q_heads));
+    const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
+#define POPKV_SC(KPT)                                                                                           \
+    case KPT:                                                                                                   \
+        hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB>), grid, dim3(kAttnThreads), 0, stream, q_, k_, \
+                           v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, ghist, h2k, kv_heads,    \
+                           scale, partials, idx_out, idx_stride);                                               \
+        break
+    switch (ch.kpt) {
+        POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
+        default: return hipErrorInvalidValue;
+    }
+#undef POPKV_SC
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t launch_merge_current_t(const float* partials, int nsplit, const void* q, const void* cur_k,
                                   const void* cur_v, const int64_t* h2k, int q_heads, int kv_heads, void* out,
+                                  int64_t* idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current,
                                   hipStream_t stream) {
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kWave), 0,
                        stream, partials, nsplit, static_cast<const T*>(q), static_cast<const T*>(cur_k),
-                       static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out));
+                       static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out), idx_out, idx_stride,
+                       idx_slot, current);
     return hipGetLastError();
 }
 }  // namespace
 
-hipError_t launch_attention_list(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
-                                 int64_t k_head_stride, int64_t v_head_stride, const int32_t* list,
-                                 int64_t list_stride, int64_t tokens, int64_t k, int nsplit,
-                                 const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                 hipStream_t stream) {
-    if (nsplit <= 0 || q_heads <= 0) return hipSuccess;
+hipError_t launch_attention_select_chunks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                          int64_t k_head_stride, int64_t v_head_stride, const uint16_t* keys,
+                                          int64_t key_stride, int64_t tokens, int64_t k, const uint32_t* rec,
+                                          const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
+                                          const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                          int64_t* idx_out, int64_t idx_stride, hipStream_t stream) {
+    if (tokens <= 0 || q_heads <= 0) return hipSuccess;
     switch (dtype) {
         case POPKV_DTYPE_F32:
-            return launch_list_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, list, list_stride,
-                                        tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
+            return launch_select_chunks_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
+                                                 key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
+                                                 kv_heads, partials, idx_out, idx_stride, stream);
         case POPKV_DTYPE_F16:
-            return launch_list_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, list, list_stride,
-                                        tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
+            return launch_select_chunks_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
+                                                 key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
+                                                 kv_heads, partials, idx_out, idx_stride, stream);
         default:
-            return launch_list_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, list, list_stride,
-                                         tokens, k, nsplit, head_to_kv, q_heads, kv_heads, partials, stream);
+            return launch_select_chunks_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
+                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
+                                                  kv_heads, partials, idx_out, idx_stride, stream);
     }
 }
 
 hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,
                                 const void* current_k, const void* current_v, const int64_t* head_to_kv, int q_heads,
-                                int kv_heads, void* output, hipStream_t stream) {
+                                int kv_heads, void* output, int64_t* idx_out, int64_t idx_stride, int64_t idx_slot,
+                                int64_t current, hipStream_t stream) {
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_merge_current_t<float>(partials, nsplit, queries, current_k, current_v, head_to_kv, q_heads,
-                                                 kv_heads, output, stream);
+                                                 kv_heads, output, idx_out, idx_stride, idx_slot, current, stream);
         case POPKV_DTYPE_F16:
             return launch_merge_current_t<f16_t>(partials, nsplit, queries, current_k, current_v, head_to_kv, q_heads,
-                                                 kv_heads, output, stream);
+                                                 kv_heads, output, idx_out, idx_stride, idx_slot, current, stream);
         default:
             return launch_merge_current_t<bf16_t>(partials, nsplit, queries, current_k, current_v, head_to_kv,
-                                                  q_heads, kv_heads, output, stream);
+                                                  q_heads, kv_heads, output, idx_out, idx_stride, idx_slot, current,
+                                                  stream);
     }
 }
 

@@ -11,6 +11,7 @@
 
 #include "kernels.h"
 #include "popkv_hip.h"
+#include "select_common.h"
 
 namespace {
 
@@ -40,32 +41,33 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 constexpr int64_t kMaxSelectTokens = 1024 * 128;
 constexpr int64_t kMaxGroupHeads = 64;
-constexpr int kLayerSplit = 256;  // selected tokens per attention workgroup
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Workspace layout of popkv_layer_step (batch 1, head_dim 128).
 struct StepLayout {
-    size_t hist, scores, list, partials, total;
-    int64_t score_stride, list_stride, k, nsplit;
+    size_t hist, rec, h2, gt1, scores, partials, total;
+    int64_t score_stride, k, nchunks;
 };
 
-// Layer-step workspace: [QH][256] u32 key histograms | [QH][score_stride] u16
-// order keys | [QH][list_stride] i32 ascending selection lists |
-// [QH][nsplit][130] f32 split partials (256 selected tokens per split, the
-// reference's split size).
+// Layer-step workspace: [QH][256] u32 high-byte key histograms (zero between
+// calls) | [QH][4] u32 threshold records | [QH][chunks][256] u16 chunk
+// low-byte histograms | [QH][chunks] u32 chunk counts | [QH][score_stride]
+// u16 order keys | [QH][chunks][130] f32 chunk partials.
 StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     StepLayout L{};
     L.k = budget - 1 < tokens ? budget - 1 : tokens;
     L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 128) * 128;
-    L.nsplit = ceil_div(L.k, kLayerSplit);
-    L.list_stride = (L.nsplit > 0 ? L.nsplit : 1) * kLayerSplit;  // whole splits: 16-byte loads stay in the row
+    L.nchunks = popkv::step_chunks(tokens, L.k).count;
+    const size_t nc = static_cast<size_t>(L.nchunks > 0 ? L.nchunks : 1);
     size_t off = 0;
     L.hist = off; off = align_up(off + static_cast<size_t>(qh) * 256 * 4);
+    L.rec = off; off = align_up(off + static_cast<size_t>(qh) * 4 * 4);
+    L.h2 = off; off = align_up(off + static_cast<size_t>(qh) * nc * 256 * 2);
+    L.gt1 = off; off = align_up(off + static_cast<size_t>(qh) * nc * 4);
     L.scores = off; off = align_up(off + static_cast<size_t>(qh * L.score_stride) * 2);
-    L.list = off; off = align_up(off + static_cast<size_t>(qh * L.list_stride) * 4);
-    L.partials = off; off = align_up(off + static_cast<size_t>(qh * (L.nsplit > 0 ? L.nsplit : 1) * (128 + 2)) * 4);
+    L.partials = off; off = align_up(off + static_cast<size_t>(qh) * nc * (128 + 2) * 4);
     L.total = off;
     return L;
 }
@@ -317,37 +319,41 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
         return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
     char* ws = static_cast<char*>(workspace);
     uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+    uint32_t* rec = reinterpret_cast<uint32_t*>(ws + L.rec);
+    uint16_t* h2 = reinterpret_cast<uint16_t*>(ws + L.h2);
+    uint32_t* gt1 = reinterpret_cast<uint32_t*>(ws + L.gt1);
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
-    int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
     hipStream_t s = as_stream(stream);
 
     // 1. query encode + popcount score -> radix order keys of the fp16 scores
-    //    (rows padded to a multiple of 64 tokens, so every row starts 128-byte
-    //    aligned) + per-head high-byte key histograms
+    //    (rows padded to a multiple of 128 tokens, so every row starts
+    //    256-byte aligned) + per-head high-byte key histograms
     st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
                                                static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
                                                static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
                                                tokens, dim_group_size, keys, L.score_stride, hist, s),
                   "popkv_layer_step(score)");
     if (st) return st;
-    // 2. top-k as an ascending token list per head (re-zeroes the
-    //    histograms), also written as int64 with the current token in slot k
-    //    when indices_out is given
-    st = launched(popkv::launch_topk_list(keys, hist, q_heads, L.score_stride, tokens, L.k, list, L.list_stride,
-                                          false, indices_out, L.k + 1, tokens, s),
-                  "popkv_layer_step(select)");
+    // 2. per-chunk low-byte histograms of the threshold's high-byte bin
+    st = launched(popkv::launch_chunk_hist(keys, L.score_stride, q_heads, tokens, L.k, hist, rec, h2, gt1, s),
+                  "popkv_layer_step(chunk histograms)");
     if (st) return st;
-    // 3. sparse attention over 256-token splits of each head's list,
-    // 4. log-sum-exp merge of the splits and the current token
-    st = launched(popkv::launch_attention_list(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride, list,
-                                               L.list_stride, tokens, L.k, static_cast<int>(L.nsplit), head_to_kv,
-                                               static_cast<int>(q_heads), static_cast<int>(kv_heads), partials, s),
-                  "popkv_layer_step(attention)");
+    // 3. per (chunk, head): the chunk's selected tokens (also written as
+    //    int64 at their rank when indices_out is given) and the sparse
+    //    attention over them (re-zeroes the histograms),
+    // 4. log-sum-exp merge of the chunks and the current token (whose index
+    //    goes to slot k)
+    st = launched(popkv::launch_attention_select_chunks(queries, dtype, prefix_k, prefix_v, k_head_stride,
+                                                        v_head_stride, keys, L.score_stride, tokens, L.k, rec, h2,
+                                                        gt1, hist, head_to_kv, static_cast<int>(q_heads),
+                                                        static_cast<int>(kv_heads), partials, indices_out, L.k + 1, s),
+                  "popkv_layer_step(select + attention)");
     if (st) return st;
-    st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nsplit), queries, dtype, current_k,
-                                                current_v, head_to_kv, static_cast<int>(q_heads),
-                                                static_cast<int>(kv_heads), output, s),
+    st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nchunks), queries, dtype, current_k,
+                                              current_v, head_to_kv, static_cast<int>(q_heads),
+                                              static_cast<int>(kv_heads), output, indices_out, L.k + 1, L.k, tokens,
+                                              s),
                   "popkv_layer_step(merge)");
     if (st) return st;
     return POPKV_OK;
@@ -369,11 +375,13 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* p
         (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
         return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
     char* ws = static_cast<char*>(workspace);
-    return launched(popkv::launch_attention_list(queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride,
-                                                 reinterpret_cast<const int32_t*>(ws + L.list), L.list_stride, tokens,
-                                                 L.k, static_cast<int>(L.nsplit), head_to_kv,
-                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads),
-                                                 reinterpret_cast<float*>(ws + L.partials), as_stream(stream)),
+    return launched(popkv::launch_attention_select_chunks(
+                        queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride,
+                        reinterpret_cast<const uint16_t*>(ws + L.scores), L.score_stride, tokens, L.k,
+                        reinterpret_cast<const uint32_t*>(ws + L.rec), reinterpret_cast<const uint16_t*>(ws + L.h2),
+                        reinterpret_cast<const uint32_t*>(ws + L.gt1), reinterpret_cast<uint32_t*>(ws + L.hist),
+                        head_to_kv, static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                        reinterpret_cast<float*>(ws + L.partials), nullptr, 0, as_stream(stream)),
                     "popkv_layer_step_attention");
 }
 
@@ -414,7 +422,8 @@ int popkv_dense_attention(const void* queries, int32_t dtype, const void* prefix
         if (st) return st;
     }
     return launched(popkv::launch_merge_current(partials, ns, queries, dtype, current_k, current_v, nullptr,
-                                                static_cast<int>(q_heads), static_cast<int>(kv_heads), output, s),
+                                                static_cast<int>(q_heads), static_cast<int>(kv_heads), output,
+                                                nullptr, 0, 0, 0, s),
                     "popkv_dense_attention(merge)");
 }
 

@@ -71,16 +71,25 @@ hipError_t launch_attention_partial(const void* queries, int dtype, const void* 
 hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t splits, int head_dim,
                                   void* output, int out_dtype, hipStream_t stream);
 
-// Layer-step attention (head_dim 128, contiguous rows): workgroup (s, h)
-// attends over entries [256s, 256s + 256) of head h's ascending selection
-// list (rows of list_stride >= 256 * nsplit int32 entries, 16-byte aligned;
-// entries past k are never dereferenced) and writes partials[h][s][130].
-hipError_t launch_attention_list(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
-                                 int64_t k_head_stride, int64_t v_head_stride, const int32_t* list,
-                                 int64_t list_stride, int64_t tokens, int64_t k, int nsplit,
-                                 const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                 hipStream_t stream);
-
+// Layer-step chunked select + attention (head_dim 128, contiguous rows).
+// Key rows hold radix order keys (rows padded to 128 keys, tokens <=
+// 131072) and ghist[row][256] their high-byte histograms; the rows are cut
+// into step_chunks(tokens, k) chunks.  launch_chunk_hist (for 0 < k <
+// tokens only) writes rec[row][4] (threshold bin, count above it),
+// h2[row][chunk][256] (uint16 low-byte histograms of the threshold bin) and
+// gt1[row][chunk] (counts above the bin).  launch_attention_select_chunks
+// then selects, per (chunk, head), the chunk's tokens among the row's k
+// largest keys (lowest index first among ties), attends over them into
+// partials[head][chunk][130], writes them as int64 to idx_out[head][rank]
+// when idx_out is non-null, and re-zeroes ghist.
+hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t rows, int64_t tokens, int64_t k,
+                             const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, hipStream_t stream);
+hipError_t launch_attention_select_chunks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
+                                          int64_t k_head_stride, int64_t v_head_stride, const uint16_t* keys,
+                                          int64_t key_stride, int64_t tokens, int64_t k, const uint32_t* rec,
+                                          const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
+                                          const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                          int64_t* idx_out, int64_t idx_stride, hipStream_t stream);
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
 // Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one
@@ -90,9 +99,11 @@ hipError_t launch_attention_dense(const void* queries, int dtype, const void* pr
                                   int64_t k_head_stride, int64_t v_head_stride, int64_t tokens, int q_heads,
                                   int kv_heads, float* partials, hipStream_t stream);
 
-// Layer-step merge of the split partials plus the current token (head_dim 128).
+// Layer-step merge of the split partials plus the current token (head_dim
+// 128); with idx_out non-null, also writes `current` to idx_out[h][idx_slot].
 hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,
                                 const void* current_k, const void* current_v, const int64_t* head_to_kv, int q_heads,
-                                int kv_heads, void* output, hipStream_t stream);
+                                int kv_heads, void* output, int64_t* idx_out, int64_t idx_stride, int64_t idx_slot,
+                                int64_t current, hipStream_t stream);
 
 }  // namespace popkv

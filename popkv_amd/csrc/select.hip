@@ -9,13 +9,20 @@
 // -0 < +0.  Selection = every key > T plus the lowest-index keys == T, T the
 // k-th largest key (PyTorch's gather-top-k tie rule).
 //
-// Two kernels.  key_hist_kernel (API path only; the layer step's scorer does
-// this itself) turns fp16 scores into order keys and accumulates each row's
-// 256-bin histogram of the keys' high byte; topk_list_kernel then finds T
-// from that histogram plus one low-byte histogram and writes the selected
-// tokens in ascending order.
+// API path: key_hist_kernel turns fp16 scores into order keys and
+// accumulates each row's 256-bin histogram of the keys' high byte;
+// topk_list_kernel then finds T from that histogram plus one low-byte
+// histogram and writes the selected tokens in ascending order (one
+// workgroup per row).
+//
+// Layer step (whose scorer writes the order keys and the high-byte
+// histograms itself): chunk_hist_kernel, one workgroup per (chunk, row),
+// writes each chunk's low-byte histogram of the threshold's high-byte bin;
+// the fused select + attention kernel (attention.hip) then derives T per
+// chunk and selects and attends in the same workgroup.
 #include "device_common.h"
 #include "kernels.h"
+#include "select_common.h"
 
 namespace popkv {
 namespace {
@@ -297,6 +304,61 @@ __global__ __launch_bounds__(kSelThreads) void topk_list_kernel(
     }
 }
 
+
+// Layer step, first half of the chunked select (the second half is the
+// fused select + attention kernel).  Block (c, h) covers chunk c of row h
+// (kChunkThreads * KPT tokens): it finds the high-byte bin b1 of the k-th
+// largest key from the scorer's histogram ghist[h], then writes
+//   h2[h][c][256]: the chunk's histogram of the low byte of its keys with
+//                  high byte b1 (uint16; a chunk holds <= 8192 tokens),
+//   gt1[h][c]:     the chunk's count of keys with high byte > b1,
+//   rec[h][0..1]:  b1 and the row's count of keys above bin b1 (block 0).
+// Only for 0 < k < tokens.
+template <int KPT>
+__global__ __launch_bounds__(kChunkThreads) void chunk_hist_kernel(const uint16_t* __restrict__ keys,
+                                                                   int64_t key_stride, int ntok, int k,
+                                                                   const uint32_t* __restrict__ ghist,
+                                                                   uint32_t* __restrict__ rec,
+                                                                   uint16_t* __restrict__ h2,
+                                                                   uint32_t* __restrict__ gt1, int nchunks) {
+    constexpr int CH = kChunkThreads * KPT;
+    const int c = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int begin = c * CH + tid * KPT;
+    ChunkKeys<KPT> kk;
+    load_chunk_keys<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, max(0, min(KPT, ntok - begin)), kk);
+    uint32_t cnt[4];
+    load_rank4(ghist + static_cast<int64_t>(h) * kBins, cnt);
+    __shared__ uint32_t s_h2[kBins];
+    __shared__ uint32_t s_gt;
+    s_h2[tid] = 0u;
+    if (tid == 0) s_gt = 0u;
+    uint32_t b1, above1;
+    wave_find_bin(cnt, static_cast<uint32_t>(k), &b1, &above1);
+    __syncthreads();
+    uint32_t n_gt = 0;
+#pragma unroll
+    for (int e = 0; e < KPT; ++e) {
+        const uint32_t key = kk.key(e);
+        const uint32_t hb = key >> 8;
+        n_gt += hb > b1 ? 1u : 0u;
+        if (hb == b1) atomicAdd(&s_h2[key & 0xffu], 1u);
+    }
+    n_gt = wave_incl_scan(n_gt, lane);
+    if (lane == kWave - 1 && n_gt != 0u) atomicAdd(&s_gt, n_gt);
+    __syncthreads();
+    const int64_t cell = static_cast<int64_t>(h) * nchunks + c;
+    h2[cell * kBins + tid] = static_cast<uint16_t>(s_h2[tid]);
+    if (tid == 0) {
+        gt1[cell] = s_gt;
+        if (c == 0) {
+            rec[4 * h] = b1;
+            rec[4 * h + 1] = above1;
+        }
+    }
+}
 }  // namespace
 
 hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
@@ -315,6 +377,25 @@ hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows,
     else if (per <= 64) POPKV_LIST(64);
     else POPKV_LIST(128);
 #undef POPKV_LIST
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t rows, int64_t tokens, int64_t k,
+                             const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, hipStream_t stream) {
+    if (rows <= 0 || k <= 0 || k >= tokens) return hipSuccess;
+    const StepChunks ch = step_chunks(tokens, k);
+    const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
+    dim3 grid(static_cast<unsigned>(ch.count), static_cast<unsigned>(rows)), block(kChunkThreads);
+#define POPKV_CH(KPT)                                                                                          \
+    case KPT:                                                                                                  \
+        hipLaunchKernelGGL((chunk_hist_kernel<KPT>), grid, block, 0, stream, keys, key_stride, nt, kk, ghist, \
+                           rec, h2, gt1, nc);                                                                  \
+        break
+    switch (ch.kpt) {
+        POPKV_CH(1); POPKV_CH(2); POPKV_CH(4); POPKV_CH(6); POPKV_CH(8); POPKV_CH(12); POPKV_CH(16); POPKV_CH(24); POPKV_CH(32);
+        default: return hipErrorInvalidValue;
+    }
+#undef POPKV_CH
     return hipGetLastError();
 }
 

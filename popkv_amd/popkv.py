@@ -333,10 +333,11 @@ def popkv_layer_step(
 def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor,
                                head_to_kv: torch.Tensor, *, budget: int,
                                workspace: LayerStepWorkspace | torch.Tensor) -> None:
-    """Re-run only the sparse-attention kernel of the last ``popkv_layer_step``
-    that used ``workspace`` (same shapes and budget); rewrites the split
-    partials inside the workspace.  A timing aid for the step's dominant
-    kernel."""
+    """Re-run only the fused select + sparse-attention kernel of the last
+    ``popkv_layer_step`` that used ``workspace`` (same shapes and budget); it
+    reads the keys and threshold histograms the step left there and rewrites
+    the chunk partials inside the workspace.  A timing aid for the step's
+    dominant kernel."""
     dev = q.device
     ws = workspace if isinstance(workspace, torch.Tensor) else workspace.buffer
     if ws is None:
