@@ -419,6 +419,28 @@ __device__ __forceinline__ void fold_rows(SoftmaxState& st, const Raw8<T>& qr, c
     }
 }
 
+// Block -> (chunk, head) of the layer step's select + attention grid
+// (nchunks * QH blocks).  With kv_groups (KV heads a multiple of 8, query
+// head h in GQA group h / qpk), block i serves group
+// 8 * (i / (8 * nchunks * qpk)) + i mod 8, chunk-major within the group:
+// the dispatcher hands blocks to the eight XCDs round-robin, so the query
+// heads of a group -- which gather overlapping K/V rows -- share one L2
+// (measured at C1: 1.0 us faster than chunk-major over all heads).
+// Otherwise block i is chunk i mod nchunks of head i / nchunks.  Either way
+// a bijection; the mapping only affects locality, never results.
+__device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk, bool kv_groups, int* c, int* h) {
+    if (kv_groups) {
+        const int per = nchunks * qpk;
+        const int j = id >> 3;
+        const int g = j / per, within = j - g * per;
+        *c = within / qpk;
+        *h = ((g << 3) + (id & 7)) * qpk + (within - *c * qpk);
+    } else {
+        *c = id % nchunks;
+        *h = id / nchunks;
+    }
+}
+
 // Layer step: the select's second half fused with the sparse attention.
 // Block (c, h) owns chunk c of head h's key row (kChunkThreads * KPT tokens,
 // KPT per thread):
@@ -435,21 +457,22 @@ __device__ __forceinline__ void fold_rows(SoftmaxState& st, const Raw8<T>& qr, c
 //      entries per pass, all NB K/V gathers in flight before any is used;
 //   4. (m, l, acc[128]) to partials[h][c] (m = -inf for an empty chunk).
 // Block 0 of each head re-zeroes the scorer's histogram ghist[h] (its last
-// reader, chunk_hist_kernel, has finished).
+// reader, chunk_hist_kernel, has finished).  The grid is one-dimensional
+// (chunk_head_of_block).
 template <typename T, int KPT, int NB>
 __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
-    const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, uint32_t* __restrict__ ghist,
-    const int64_t* __restrict__ head_to_kv, int kv_heads, float scale, float* __restrict__ partials,
-    int64_t* __restrict__ idx_out, int64_t idx_stride) {
+    const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
+    uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
+    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
     constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
     constexpr int CH = kChunkThreads * KPT;
     constexpr int PASS = NSLOT * NB;  // entries per pass
     static_assert(NB % 8 == 0, "a slot's entries of one pass are whole 16-byte LDS reads");
-    const int c = blockIdx.x;
-    const int h = blockIdx.y;
+    int c, h;
+    chunk_head_of_block(static_cast<int>(blockIdx.x), nchunks, qpk, kv_groups, &c, &h);
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -945,13 +968,15 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
     const StepChunks ch = step_chunks(tokens, k);
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
-    dim3 grid(static_cast<unsigned>(ch.count), static_cast<unsigned>(q_heads));
+    const bool groups = kv_heads % 8 == 0 && q_heads % kv_heads == 0;
+    const int qpk = groups ? q_heads / kv_heads : 1;
+    const dim3 grid(static_cast<unsigned>(ch.count * q_heads));
     const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
 #define POPKV_SC(KPT)                                                                                           \
     case KPT:                                                                                                   \
         hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB>), grid, dim3(kAttnThreads), 0, stream, q_, k_, \
-                           v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, ghist, h2k, kv_heads,    \
-                           scale, partials, idx_out, idx_stride);                                               \
+                           v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups, ghist, h2k, \
+                           kv_heads, scale, partials, idx_out, idx_stride);                                     \
         break
     switch (ch.kpt) {
         POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
