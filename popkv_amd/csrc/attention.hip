@@ -470,7 +470,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
     constexpr int CH = kChunkThreads * KPT;
     constexpr int PASS = NSLOT * NB;  // entries per pass
-    static_assert(NB % 8 == 0, "a slot's entries of one pass are whole 16-byte LDS reads");
+    static_assert(NB % 2 == 0, "a slot's entries of one pass are whole 32-bit LDS words");
     int c, h;
     chunk_head_of_block(static_cast<int>(blockIdx.x), nchunks, qpk, kv_groups, &c, &h);
     const int tid = threadIdx.x;
@@ -587,15 +587,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     SoftmaxState st;
     init_state(st);
     for (int base = 0; base < n_sel; base += PASS) {
-        const int e0 = base + slot * NB;  // a multiple of 8: 16-byte aligned
+        const int e0 = base + slot * NB;  // a multiple of NB: the widest LDS read that divides 2*NB bytes is aligned
         uint32_t ew[NB / 2];
+        if constexpr (NB % 8 == 0) {
 #pragma unroll
-        for (int j = 0; j < NB / 8; ++j) {
-            const uint4 ev = *reinterpret_cast<const uint4*>(&s_list[min(e0 + 8 * j, CH - 8)]);
-            ew[4 * j] = ev.x;
-            ew[4 * j + 1] = ev.y;
-            ew[4 * j + 2] = ev.z;
-            ew[4 * j + 3] = ev.w;
+            for (int j = 0; j < NB / 8; ++j) {
+                const uint4 ev = *reinterpret_cast<const uint4*>(&s_list[min(e0 + 8 * j, CH - 8)]);
+                ew[4 * j] = ev.x;
+                ew[4 * j + 1] = ev.y;
+                ew[4 * j + 2] = ev.z;
+                ew[4 * j + 3] = ev.w;
+            }
+        } else if constexpr (NB % 4 == 0) {
+#pragma unroll
+            for (int j = 0; j < NB / 4; ++j) {
+                const uint2 ev = *reinterpret_cast<const uint2*>(&s_list[min(e0 + 4 * j, CH - 4)]);
+                ew[2 * j] = ev.x;
+                ew[2 * j + 1] = ev.y;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NB / 2; ++j) ew[j] = *reinterpret_cast<const uint32_t*>(&s_list[min(e0 + 2 * j, CH - 2)]);
         }
         Raw8<T> kr[NB], vr[NB];
         bool live[NB];
@@ -964,7 +976,11 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
                                   const uint32_t* rec, const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                   const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
                                   int64_t idx_stride, hipStream_t stream) {
-    constexpr int NB = 8;
+    // 10 rows per slot and pass: 160 per pass, so a chunk holding up to 320
+    // selected tokens (C1: 204-294 in chunks of 2048) is gathered in two
+    // passes.  Measured at C1, select + attention: 8 rows 16.5 us (three
+    // passes above 256), 10 rows 15.5 us, 12 rows 16.4 us.
+    constexpr int NB = 10;
     const StepChunks ch = step_chunks(tokens, k);
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
