@@ -682,10 +682,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_gqa_kernel(
 // (logit q.cur_k * scale, value cur_v), written in the query dtype.  One
 // wave per head, lane l owning dims l and l + 64, and no LDS or barrier:
 // the split maxima and denominators are wave reductions (lane s holds split
-// s of each 64-split chunk), the weights reach the accumulation through
-// readlane, and every split state is loaded in batches of 8 before it is
-// used.
-constexpr int kMergeStepBatch = 8;
+// s of each 64-split group), and the weights reach the accumulation through
+// readlane.  q, cur_k, cur_v, the first group's maxima and denominators and
+// the first kMergeFirst splits' accumulators are loaded in one burst, so a
+// layer step's merge (at most 64 chunks, 16 at C1) pays one memory latency
+// for all of them; further splits (dense layers) follow in batches of
+// kMergeFirst.  Accumulation order: the current token, then the splits in
+// ascending order.
+constexpr int kMergeFirst = 16;
 
 template <typename T>
 __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
@@ -705,39 +709,68 @@ __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     const T* qh = q + static_cast<int64_t>(h) * D;
     const T* ck = cur_k + kvh * D;
     const T* cv = cur_v + kvh * D;
+    // the burst (with nsplit == 0 the accumulator loads read split 0's slot,
+    // which every workspace holds, and are not used)
     const float q0 = Elem<T>::load(qh, lane), q1 = Elem<T>::load(qh, lane + 64);
     const float k0 = Elem<T>::load(ck, lane), k1 = Elem<T>::load(ck, lane + 64);
     const float v0 = Elem<T>::load(cv, lane), v1 = Elem<T>::load(cv, lane + 64);
-    // the splits' maxima with the current token's logit
-    const float cur_m = wave_sum(q0 * k0 + q1 * k1) * scale;
-    float mx = cur_m;
-    for (int s0 = 0; s0 < nsplit; s0 += kWave)
+    float m0 = -INFINITY, l0 = 0.0f;  // split `lane`
+    if (lane < nsplit) {
+        m0 = ps[static_cast<int64_t>(lane) * S];
+        l0 = ps[static_cast<int64_t>(lane) * S + 1];
+    }
+    const int nf = min(nsplit, kMergeFirst);
+    float a0[kMergeFirst], a1[kMergeFirst];
+#pragma unroll
+    for (int j = 0; j < kMergeFirst; ++j) {
+        const int64_t so = static_cast<int64_t>(max(min(j, nf - 1), 0)) * S + 2;
+        a0[j] = ps[so + lane];
+        a1[j] = ps[so + lane + 64];
+    }
+    // the maxima of every split and the current token's logit
+    float mx = m0;
+    for (int s0 = kWave; s0 < nsplit; s0 += kWave)
         if (s0 + lane < nsplit) mx = fmaxf(mx, ps[static_cast<int64_t>(s0 + lane) * S]);
-    mx = wave_max(mx);
+    const float cur_m = wave_sum(q0 * k0 + q1 * k1) * scale;
+    mx = fmaxf(wave_max(mx), cur_m);
     const float wc = __expf(cur_m - mx);
-    float den = 0.0f, num0 = wc * v0, num1 = wc * v1;
+    const float w0 = m0 == -INFINITY ? 0.0f : __expf(m0 - mx);
+    float den = l0 * w0, num0 = wc * v0, num1 = wc * v1;
+#pragma unroll
+    for (int j = 0; j < kMergeFirst; ++j) {
+        if (j < nf) {
+            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w0), j));
+            num0 = fmaf(ws, a0[j], num0);
+            num1 = fmaf(ws, a1[j], num1);
+        }
+    }
     for (int s0 = 0; s0 < nsplit; s0 += kWave) {
-        float w = 0.0f;
-        if (s0 + lane < nsplit) {
-            const float m = ps[static_cast<int64_t>(s0 + lane) * S];
+        float w = w0;
+        if (s0 > 0) {
+            float m = -INFINITY, l = 0.0f;
+            if (s0 + lane < nsplit) {
+                m = ps[static_cast<int64_t>(s0 + lane) * S];
+                l = ps[static_cast<int64_t>(s0 + lane) * S + 1];
+            }
             w = m == -INFINITY ? 0.0f : __expf(m - mx);
-            den += ps[static_cast<int64_t>(s0 + lane) * S + 1] * w;
+            den += l * w;
         }
         const int n = min(kWave, nsplit - s0);
-        for (int b = 0; b < n; b += kMergeStepBatch) {
-            float a0[kMergeStepBatch], a1[kMergeStepBatch];
+        for (int b = s0 == 0 ? nf : 0; b < n; b += kMergeFirst) {
+            float c0[kMergeFirst], c1[kMergeFirst];
 #pragma unroll
-            for (int j = 0; j < kMergeStepBatch; ++j) {
+            for (int j = 0; j < kMergeFirst; ++j) {
                 const int64_t so = static_cast<int64_t>(s0 + min(b + j, n - 1)) * S + 2;
-                a0[j] = ps[so + lane];
-                a1[j] = ps[so + lane + 64];
+                c0[j] = ps[so + lane];
+                c1[j] = ps[so + lane + 64];
             }
 #pragma unroll
-            for (int j = 0; j < kMergeStepBatch; ++j) {
+            for (int j = 0; j < kMergeFirst; ++j) {
                 if (b + j < n) {
-                    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b + j));
-                    num0 = fmaf(ws, a0[j], num0);
-                    num1 = fmaf(ws, a1[j], num1);
+                    const float ws =
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b + j));
+                    num0 = fmaf(ws, c0[j], num0);
+                    num1 = fmaf(ws, c1[j], num1);
                 }
             }
         }
