@@ -34,13 +34,13 @@ sys.path.insert(0, str(ROOT))
 METRIC = "µs/layer score+top-k+sparse-attn @32K ctx, B=4096; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 N_BUFFERS = 8
-# HBM bytes per launch of the layer step's attention kernel at C1, from
-# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script (KiB per
+# HBM bytes per launch of the layer step's select + attention kernel at C1,
+# from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script (KiB per
 # dispatch), each scaled by the same counter on a plain 256 MiB copy
 # (bench.py --copy-calibration): FETCH_SIZE reads 131084.4 KiB for the copy's
-# 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).  Attention:
-# FETCH_SIZE 28700.5 KiB, WRITE_SIZE 272.0 KiB per dispatch.
-ATTN_TRAFFIC_BYTES = round(28700.5 * 1024 * (262144 / 131084.4) + 272.0 * 1024)
+# 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).
+# attn_select_chunk_kernel: FETCH_SIZE 28149.1 KiB, WRITE_SIZE 292.0 KiB.
+ATTN_TRAFFIC_BYTES = round(28149.1 * 1024 * (262144 / 131084.4) + 292.0 * 1024)
 
 
 def parse_args():

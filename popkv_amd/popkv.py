@@ -9,7 +9,9 @@ static K/V cache append (popkv.py:105-111, :964-972), ``_append_current`` /
 ``LlamaSparseDecoder.decode`` (popkv.py:1076-1115) as ``popkv_retrieval_step``.
 
 ``popkv_layer_step`` is the same step as one C-ABI call (four kernels:
-encode + score, top-k, split attention, log-sum-exp merge).
+encode + score with per-head key histograms, per-chunk histograms of the
+threshold bin, per-chunk select + sparse attention, log-sum-exp merge with
+the current token).
 """
 from __future__ import annotations
 
