@@ -443,18 +443,23 @@ __device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk
 
 // Layer step: the select's second half fused with the sparse attention.
 // Block (c, h) owns chunk c of head h's key row (kChunkThreads * KPT tokens,
-// KPT per thread):
-//   1. the threshold: from the chunk histograms of chunk_hist_kernel
-//      (thread u sums bin u over every chunk and over the chunks before c),
-//      bin t2 of the low byte -> T = b1:t2, need_eq = ties taken in the row,
-//      eq_before = ties in earlier chunks (lowest index first: PyTorch's
-//      gather-top-k rule);
-//   2. the chunk's selected tokens (every key > T, the ties whose row rank
-//      is below need_eq; with k >= tokens every token) compacted in
-//      ascending order into LDS, and into idx_out[h][rank] as int64 when
-//      idx_out is non-null (rank = selected tokens before it in the row);
-//   3. attention over them: 16 row slots, each taking NB consecutive
-//      entries per pass, all NB K/V gathers in flight before any is used;
+// KPT per thread).  The selection is every key > T plus the lowest-index
+// ties at T (PyTorch's gather-top-k rule), T = b1:t2 the k-th largest key;
+// with k >= tokens every token.
+//   1. The keys above bin b1 are selected whatever t2 is, and b1 arrives
+//      with the first loads (chunk_hist_kernel's record).  The block lists
+//      them first (one block scan) and issues the first gather pass over
+//      them before it resolves T.
+//   2. While those rows are in flight: the chunk histograms of bin b1
+//      (thread u sums bin u over every chunk and over the chunks before c)
+//      give t2, need_eq = ties the row takes and eq_before = ties in
+//      earlier chunks; the keys of bin b1 above T and the chunk's share of
+//      the ties are appended to the list (a second block scan).  When
+//      idx_out is non-null every selected token is also written there as
+//      int64 at its row rank (selected tokens before it in the row).
+//   3. Attention over the list: 16 row slots, each taking NB consecutive
+//      entries per pass, all NB K/V gathers of a pass in flight before any
+//      is used.
 //   4. (m, l, acc[128]) to partials[h][c] (m = -inf for an empty chunk).
 // Block 0 of each head re-zeroes the scorer's histogram ghist[h] (its last
 // reader, chunk_hist_kernel, has finished).  The grid is one-dimensional
@@ -481,10 +486,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);  // none / every token / threshold
 
     // 0. loads, all issued before any is used: this thread's keys, the query
-    //    slice, the head's KV mapping and the threshold state.  The mapping
-    //    and the record are read with vector loads at a lane-opaque zero
-    //    offset: as scalar loads they would be waited for together with the
-    //    kernel arguments, before the chunk histograms are even issued.
+    //    slice, the head's KV mapping, the threshold record and the chunk
+    //    histograms.  The mapping and the record are read with vector loads
+    //    at a lane-opaque zero offset: as scalar loads they would be waited
+    //    for together with the kernel arguments, before the chunk histograms
+    //    are even issued.
     int z = 0;
     asm volatile("" : "+v"(z));
     const int begin = c * CH + tid * KPT;
@@ -495,13 +501,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
     const int64_t map = head_to_kv[h + z];
     __shared__ uint32_t s_g2[256], s_p2[256];
-    __shared__ uint32_t s_scan[kAttnWaves];
+    __shared__ uint32_t s_scan1[kAttnWaves], s_scan2[kAttnWaves];
     __shared__ __align__(16) uint16_t s_list[CH];
-    uint32_t thr = 0, need_eq = 0, eq_before = 0, rank0 = 0;
+    uint32_t b1 = 0, above1 = 0, rank0 = 0;
+    uint32_t g2 = 0, p2 = 0;  // bin tid of the chunk histograms over every chunk / over chunks before c
+    uint32_t gt1_before = 0;  // keys above bin b1 in earlier chunks
     if (mode == 2) {
-        const uint32_t b1 = rec[4 * h + z], above1 = rec[4 * h + 1 + z];
+        b1 = rec[4 * h + z];
+        above1 = rec[4 * h + 1 + z];
         const uint16_t* hr = h2 + static_cast<int64_t>(h) * nchunks * 256 + tid;
-        uint32_t g2 = 0, p2 = 0;  // bin tid over every chunk / over chunks before c
         for (int c0 = 0; c0 < nchunks; c0 += 16) {
             uint32_t v[16];
 #pragma unroll
@@ -513,80 +521,51 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
                 p2 += c0 + j < c ? x : 0u;
             }
         }
-        uint32_t gt1_before = 0;  // keys above bin b1 in earlier chunks
         if (idx_out != nullptr) {
             for (int c0 = 0; c0 < c; c0 += kWave) {
                 const uint32_t x = c0 + lane < c ? gt1[static_cast<int64_t>(h) * nchunks + c0 + lane] : 0u;
                 gt1_before += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
             }
         }
-        s_g2[tid] = g2;
-        s_p2[tid] = p2;
-        __syncthreads();
-        uint32_t cnt[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cnt[i] = s_g2[255 - (4 * lane + i)];
-        const uint32_t need1 = static_cast<uint32_t>(k) - above1;
-        uint32_t t2, above2;
-        wave_find_bin(cnt, need1, &t2, &above2);
-        thr = (b1 << 8) | t2;  // >= 0x03ff
-        need_eq = need1 - above2;
-        eq_before = s_p2[t2];
-        if (idx_out != nullptr) {
-            // keys of bin b1 with low byte > t2 in earlier chunks
-            uint32_t x = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x += 4 * lane + i > static_cast<int>(t2) ? s_p2[4 * lane + i] : 0u;
-            const uint32_t gt2_before =
-                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
-            rank0 = gt1_before + gt2_before + min(eq_before, need_eq);
-        }
-    } else if (mode == 1) {
-        rank0 = static_cast<uint32_t>(c * CH);
     }
 
-    // 1. the chunk's selection masks and their ranks
-    uint32_t m_gt = 0u, m_eq = 0u;
-    if (mode == 2) key_masks<KPT>(kk, thr, &m_gt, &m_eq);
-    else if (mode == 1) m_gt = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
-    const uint32_t n_eq = static_cast<uint32_t>(__popc(m_eq));
-    uint32_t total;
-    const uint32_t packed =
-        block_excl_scan_once(static_cast<uint32_t>(__popc(m_gt)) | (n_eq << 16), s_scan, kAttnWaves, &total);
-    // ties taken by earlier chunks / before this thread / by this thread
-    // (each min is formed before the subtraction that uses it, which then
-    // never wraps)
-    const uint32_t prior = min(eq_before, need_eq);
-    const uint32_t t_before = min(eq_before + (packed >> 16), need_eq);
-    const uint32_t t_end = min(eq_before + (total >> 16), need_eq);
-    uint32_t take = min(n_eq, need_eq - t_before);
-    const int n_sel = static_cast<int>((total & 0xffffu) + (t_end - prior));
-    uint32_t pos = (packed & 0xffffu) + (t_before - prior);
-    uint32_t ties = m_eq;
-    if (take < n_eq) {  // keep only the first `take` ties
-        uint32_t rest = ties;
-        for (uint32_t j = 0; j < take; ++j) rest &= rest - 1u;
-        ties &= ~rest;
+    // 1. the tokens selected whatever T is: keys above bin b1 (mode 2) or
+    //    every token (mode 1), listed first in ascending order
+    uint32_t m_def = 0u;
+    if (mode == 2) {
+        uint32_t unused;
+        key_masks<KPT>(kk, (b1 << 8) | 0xffu, &m_def, &unused);
+    } else if (mode == 1) {
+        m_def = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
     }
-    int64_t* irow = idx_out != nullptr ? idx_out + static_cast<int64_t>(h) * idx_stride : nullptr;
-    for (uint32_t m = m_gt | ties; m != 0u; m &= m - 1u) {
-        const int e = tid * KPT + __builtin_ctz(m);
-        if (pos < static_cast<uint32_t>(CH)) s_list[pos] = static_cast<uint16_t>(e);
-        if (irow != nullptr && rank0 + pos < static_cast<uint32_t>(k)) irow[rank0 + pos] = c * CH + e;
-        ++pos;
+    uint32_t n_def_total;
+    const uint32_t pos_def =
+        block_excl_scan_once(static_cast<uint32_t>(__popc(m_def)), s_scan1, kAttnWaves, &n_def_total);
+    {
+        uint32_t pos = pos_def;
+        for (uint32_t m = m_def; m != 0u; m &= m - 1u) {
+            if (pos < static_cast<uint32_t>(CH)) s_list[pos] = static_cast<uint16_t>(tid * KPT + __builtin_ctz(m));
+            ++pos;
+        }
+    }
+    if (mode == 2) {
+        s_g2[tid] = g2;
+        s_p2[tid] = p2;
     }
     if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
     __syncthreads();
 
-    // 2. attention over s_list[0, n_sel)
+    // 2. first gather pass over the listed tokens, issued now
     const int64_t kvh = min(max(map, static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
     const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
     const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
     const uint32_t t0 = static_cast<uint32_t>(c * CH);
     const uint32_t tmax = static_cast<uint32_t>(ntok - 1);  // a selected token is < ntok; clamped all the same
-    SoftmaxState st;
-    init_state(st);
-    for (int base = 0; base < n_sel; base += PASS) {
+    Raw8<T> kr[NB], vr[NB];
+    bool live[NB];
+    // rows [base + slot*NB, +NB) of the list, those below `limit` live; dead
+    // rows re-read the chunk's first token and get weight 0
+    auto issue = [&](int base, int limit) {
         const int e0 = base + slot * NB;  // a multiple of NB: the widest LDS read that divides 2*NB bytes is aligned
         uint32_t ew[NB / 2];
         if constexpr (NB % 8 == 0) {
@@ -609,17 +588,88 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
 #pragma unroll
             for (int j = 0; j < NB / 2; ++j) ew[j] = *reinterpret_cast<const uint32_t*>(&s_list[min(e0 + 2 * j, CH - 2)]);
         }
-        Raw8<T> kr[NB], vr[NB];
-        bool live[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            live[b] = e0 + b < n_sel;
-            // dead rows re-read the chunk's first token with weight 0
+            live[b] = e0 + b < limit;
             const uint32_t t = min(t0 + (live[b] ? ((ew[b / 2] >> ((b & 1) * 16)) & 0xffffu) : 0u), tmax);
             const uint32_t off = t * (D * sizeof(T));
             kr[b].load(reinterpret_cast<const T*>(kb + off));
             vr[b].load(reinterpret_cast<const T*>(vb + off));
         }
+    };
+    const int first = static_cast<int>(min(n_def_total, static_cast<uint32_t>(PASS)));
+    if (first > 0) issue(0, first);
+
+    // 3. T from the chunk histograms, the rest of the selection appended
+    uint32_t thr = 0, need_eq = 0, eq_before = 0;
+    if (mode == 2) {
+        uint32_t cnt[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cnt[i] = s_g2[255 - (4 * lane + i)];
+        const uint32_t need1 = static_cast<uint32_t>(k) - above1;
+        uint32_t t2, above2;
+        wave_find_bin(cnt, need1, &t2, &above2);
+        thr = (b1 << 8) | t2;  // >= 0x03ff
+        need_eq = need1 - above2;
+        eq_before = s_p2[t2];
+        if (idx_out != nullptr) {
+            // keys of bin b1 with low byte > t2 in earlier chunks
+            uint32_t x = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x += 4 * lane + i > static_cast<int>(t2) ? s_p2[4 * lane + i] : 0u;
+            const uint32_t gt2_before =
+                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
+            rank0 = gt1_before + gt2_before + min(eq_before, need_eq);
+        }
+    } else if (mode == 1) {
+        rank0 = static_cast<uint32_t>(c * CH);
+    }
+    uint32_t m_gt = m_def, m_eq = 0u;
+    if (mode == 2) key_masks<KPT>(kk, thr, &m_gt, &m_eq);
+    const uint32_t m_rest = m_gt & ~m_def;  // bin b1 above T
+    const uint32_t n_eq = static_cast<uint32_t>(__popc(m_eq));
+    uint32_t total2;
+    const uint32_t packed =
+        block_excl_scan_once(static_cast<uint32_t>(__popc(m_rest)) | (n_eq << 16), s_scan2, kAttnWaves, &total2);
+    // ties taken by earlier chunks / before this thread / by this thread
+    // (each min is formed before the subtraction that uses it, which then
+    // never wraps)
+    const uint32_t prior = min(eq_before, need_eq);
+    const uint32_t t_before = min(eq_before + (packed >> 16), need_eq);
+    const uint32_t t_end = min(eq_before + (total2 >> 16), need_eq);
+    const uint32_t take = min(n_eq, need_eq - t_before);
+    const int n_sel = static_cast<int>(n_def_total + (total2 & 0xffffu) + (t_end - prior));
+    uint32_t ties = m_eq;
+    if (take < n_eq) {  // keep only the first `take` ties
+        uint32_t rest = ties;
+        for (uint32_t j = 0; j < take; ++j) rest &= rest - 1u;
+        ties &= ~rest;
+    }
+    {
+        uint32_t pos = n_def_total + (packed & 0xffffu) + (t_before - prior);
+        for (uint32_t m = m_rest | ties; m != 0u; m &= m - 1u) {
+            if (pos < static_cast<uint32_t>(CH)) s_list[pos] = static_cast<uint16_t>(tid * KPT + __builtin_ctz(m));
+            ++pos;
+        }
+    }
+    if (idx_out != nullptr) {
+        // ascending row ranks: selected tokens of earlier threads (listed
+        // above b1, in b1 above T, and ties taken) come first
+        int64_t* irow = idx_out + static_cast<int64_t>(h) * idx_stride;
+        uint32_t pos = pos_def + (packed & 0xffffu) + (t_before - prior);
+        for (uint32_t m = m_gt | ties; m != 0u; m &= m - 1u) {
+            if (rank0 + pos < static_cast<uint32_t>(k)) irow[rank0 + pos] = c * CH + tid * KPT + __builtin_ctz(m);
+            ++pos;
+        }
+    }
+    __syncthreads();
+
+    // 4. attention over s_list[0, n_sel): the first pass's rows, then the rest
+    SoftmaxState st;
+    init_state(st);
+    if (first > 0) fold_rows<T, NB>(st, qr, kr, vr, live, scale);
+    for (int base = first; base < n_sel; base += PASS) {
+        issue(base, n_sel);
         fold_rows<T, NB>(st, qr, kr, vr, live, scale);
     }
     store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2));
