@@ -447,19 +447,20 @@ __device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk
 // ties at T (PyTorch's gather-top-k rule), T = b1:t2 the k-th largest key;
 // with k >= tokens every token.
 //   1. The keys above bin b1 are selected whatever t2 is, and b1 arrives
-//      with the first loads (chunk_hist_kernel's record).  The block lists
-//      them first (one block scan) and issues the first gather pass over
-//      them before it resolves T.
+//      with the first loads (chunk_hist_kernel's record).  Each wave lists
+//      its own first SLOTS * NB of them (a wave scan) and issues its slots'
+//      first gather pass over them before T is resolved.
 //   2. While those rows are in flight: the chunk histograms of bin b1
 //      (thread u sums bin u over every chunk and over the chunks before c)
 //      give t2, need_eq = ties the row takes and eq_before = ties in
-//      earlier chunks; the keys of bin b1 above T and the chunk's share of
-//      the ties are appended to the list (a second block scan).  When
-//      idx_out is non-null every selected token is also written there as
-//      int64 at its row rank (selected tokens before it in the row).
-//   3. Attention over the list: 16 row slots, each taking NB consecutive
-//      entries per pass, all NB K/V gathers of a pass in flight before any
-//      is used.
+//      earlier chunks; the block lists the tokens above b1 the waves left,
+//      the keys of bin b1 above T and the chunk's share of the ties (one
+//      block scan).  When idx_out is non-null every selected token is also
+//      written there as int64 at its row rank (selected tokens before it in
+//      the row).
+//   3. Attention over the block's list: 16 row slots, each taking NB
+//      consecutive entries per pass, all NB K/V gathers of a pass in
+//      flight before any is used.
 //   4. (m, l, acc[128]) to partials[h][c] (m = -inf for an empty chunk).
 // Block 0 of each head re-zeroes the scorer's histogram ghist[h] (its last
 // reader, chunk_hist_kernel, has finished).  The grid is one-dimensional
@@ -530,7 +531,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     }
 
     // 1. the tokens selected whatever T is: keys above bin b1 (mode 2) or
-    //    every token (mode 1), listed first in ascending order
+    //    every token (mode 1).  Each wave lists its own first WCAP of them in
+    //    ascending order (a wave scan, no block barrier) and issues its
+    //    slots' first gather pass over them at once; the others join the
+    //    block's list below.
+    constexpr int WCAP = SLOTS * NB;  // entries of one wave's slots in one pass
+    __shared__ __align__(16) uint16_t s_wlist[kAttnWaves][WCAP];
     uint32_t m_def = 0u;
     if (mode == 2) {
         uint32_t unused;
@@ -538,24 +544,25 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     } else if (mode == 1) {
         m_def = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
     }
-    uint32_t n_def_total;
-    const uint32_t pos_def =
-        block_excl_scan_once(static_cast<uint32_t>(__popc(m_def)), s_scan1, kAttnWaves, &n_def_total);
+    const uint32_t dcnt = static_cast<uint32_t>(__popc(m_def));
+    const uint32_t dincl = wave_incl_scan(dcnt, lane);
+    const int wfirst = min(__builtin_amdgcn_readlane(static_cast<int>(dincl), kWave - 1), WCAP);
+    uint32_t m_left = 0u;  // this thread's tokens above bin b1 that the wave's first pass does not take
     {
-        uint32_t pos = pos_def;
+        uint32_t pos = dincl - dcnt;
         for (uint32_t m = m_def; m != 0u; m &= m - 1u) {
-            if (pos < static_cast<uint32_t>(CH)) s_list[pos] = static_cast<uint16_t>(tid * KPT + __builtin_ctz(m));
+            const int e = __builtin_ctz(m);
+            if (pos < static_cast<uint32_t>(WCAP)) s_wlist[wave][pos] = static_cast<uint16_t>(tid * KPT + e);
+            else m_left |= 1u << e;
             ++pos;
         }
     }
-    if (mode == 2) {
-        s_g2[tid] = g2;
-        s_p2[tid] = p2;
-    }
-    if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
-    __syncthreads();
+    // the wave reads its own list next: one wave's LDS operations complete in order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // 2. first gather pass over the listed tokens, issued now
+    // 2. the first gather pass, issued now
     const int64_t kvh = min(max(map, static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
     const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
     const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
@@ -563,15 +570,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const uint32_t tmax = static_cast<uint32_t>(ntok - 1);  // a selected token is < ntok; clamped all the same
     Raw8<T> kr[NB], vr[NB];
     bool live[NB];
-    // rows [base + slot*NB, +NB) of the list, those below `limit` live; dead
-    // rows re-read the chunk's first token and get weight 0
-    auto issue = [&](int base, int limit) {
-        const int e0 = base + slot * NB;  // a multiple of NB: the widest LDS read that divides 2*NB bytes is aligned
+    // rows lst[e0 .. e0 + NB) of a list of `cap` entries, those below `limit`
+    // live; dead rows re-read the chunk's first token and get weight 0.  e0
+    // is a multiple of NB, so the widest LDS read that divides 2*NB bytes is
+    // aligned.
+    auto issue = [&](const uint16_t* lst, int e0, int limit, int cap) {
         uint32_t ew[NB / 2];
         if constexpr (NB % 8 == 0) {
 #pragma unroll
             for (int j = 0; j < NB / 8; ++j) {
-                const uint4 ev = *reinterpret_cast<const uint4*>(&s_list[min(e0 + 8 * j, CH - 8)]);
+                const uint4 ev = *reinterpret_cast<const uint4*>(&lst[min(e0 + 8 * j, cap - 8)]);
                 ew[4 * j] = ev.x;
                 ew[4 * j + 1] = ev.y;
                 ew[4 * j + 2] = ev.z;
@@ -580,13 +588,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
         } else if constexpr (NB % 4 == 0) {
 #pragma unroll
             for (int j = 0; j < NB / 4; ++j) {
-                const uint2 ev = *reinterpret_cast<const uint2*>(&s_list[min(e0 + 4 * j, CH - 4)]);
+                const uint2 ev = *reinterpret_cast<const uint2*>(&lst[min(e0 + 4 * j, cap - 4)]);
                 ew[2 * j] = ev.x;
                 ew[2 * j + 1] = ev.y;
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < NB / 2; ++j) ew[j] = *reinterpret_cast<const uint32_t*>(&s_list[min(e0 + 2 * j, CH - 2)]);
+            for (int j = 0; j < NB / 2; ++j) ew[j] = *reinterpret_cast<const uint32_t*>(&lst[min(e0 + 2 * j, cap - 2)]);
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -597,10 +605,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
             vr[b].load(reinterpret_cast<const T*>(vb + off));
         }
     };
-    const int first = static_cast<int>(min(n_def_total, static_cast<uint32_t>(PASS)));
-    if (first > 0) issue(0, first);
+    if (wfirst > 0) issue(s_wlist[wave], (slot % SLOTS) * NB, wfirst, WCAP);
+    if (mode == 2) {
+        s_g2[tid] = g2;
+        s_p2[tid] = p2;
+    }
+    if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
+    __syncthreads();
 
-    // 3. T from the chunk histograms, the rest of the selection appended
+    // 3. T from the chunk histograms; the block's list: the tokens above bin
+    //    b1 the waves' first passes left, bin b1's keys above T and the
+    //    chunk's share of the ties
     uint32_t thr = 0, need_eq = 0, eq_before = 0;
     if (mode == 2) {
         uint32_t cnt[4];
@@ -626,11 +641,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     }
     uint32_t m_gt = m_def, m_eq = 0u;
     if (mode == 2) key_masks<KPT>(kk, thr, &m_gt, &m_eq);
-    const uint32_t m_rest = m_gt & ~m_def;  // bin b1 above T
+    const uint32_t m_blk = m_left | (m_gt & ~m_def);  // listed by the block (the ties follow)
     const uint32_t n_eq = static_cast<uint32_t>(__popc(m_eq));
     uint32_t total2;
     const uint32_t packed =
-        block_excl_scan_once(static_cast<uint32_t>(__popc(m_rest)) | (n_eq << 16), s_scan2, kAttnWaves, &total2);
+        block_excl_scan_once(static_cast<uint32_t>(__popc(m_blk)) | (n_eq << 16), s_scan2, kAttnWaves, &total2);
     // ties taken by earlier chunks / before this thread / by this thread
     // (each min is formed before the subtraction that uses it, which then
     // never wraps)
@@ -638,7 +653,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const uint32_t t_before = min(eq_before + (packed >> 16), need_eq);
     const uint32_t t_end = min(eq_before + (total2 >> 16), need_eq);
     const uint32_t take = min(n_eq, need_eq - t_before);
-    const int n_sel = static_cast<int>(n_def_total + (total2 & 0xffffu) + (t_end - prior));
+    const int n_list = static_cast<int>((total2 & 0xffffu) + (t_end - prior));
     uint32_t ties = m_eq;
     if (take < n_eq) {  // keep only the first `take` ties
         uint32_t rest = ties;
@@ -646,17 +661,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
         ties &= ~rest;
     }
     {
-        uint32_t pos = n_def_total + (packed & 0xffffu) + (t_before - prior);
-        for (uint32_t m = m_rest | ties; m != 0u; m &= m - 1u) {
+        uint32_t pos = (packed & 0xffffu) + (t_before - prior);
+        for (uint32_t m = m_blk | ties; m != 0u; m &= m - 1u) {
             if (pos < static_cast<uint32_t>(CH)) s_list[pos] = static_cast<uint16_t>(tid * KPT + __builtin_ctz(m));
             ++pos;
         }
     }
     if (idx_out != nullptr) {
-        // ascending row ranks: selected tokens of earlier threads (listed
-        // above b1, in b1 above T, and ties taken) come first
+        // ascending row ranks: the selected tokens of earlier threads come first
+        uint32_t gt_total;
+        const uint32_t gt_pre =
+            block_excl_scan_once(static_cast<uint32_t>(__popc(m_gt)), s_scan1, kAttnWaves, &gt_total);
         int64_t* irow = idx_out + static_cast<int64_t>(h) * idx_stride;
-        uint32_t pos = pos_def + (packed & 0xffffu) + (t_before - prior);
+        uint32_t pos = gt_pre + (t_before - prior);
         for (uint32_t m = m_gt | ties; m != 0u; m &= m - 1u) {
             if (rank0 + pos < static_cast<uint32_t>(k)) irow[rank0 + pos] = c * CH + tid * KPT + __builtin_ctz(m);
             ++pos;
@@ -664,12 +681,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     }
     __syncthreads();
 
-    // 4. attention over s_list[0, n_sel): the first pass's rows, then the rest
+    // 4. attention: the waves' first passes, then the block's list
     SoftmaxState st;
     init_state(st);
-    if (first > 0) fold_rows<T, NB>(st, qr, kr, vr, live, scale);
-    for (int base = first; base < n_sel; base += PASS) {
-        issue(base, n_sel);
+    if (wfirst > 0) fold_rows<T, NB>(st, qr, kr, vr, live, scale);
+    for (int base = 0; base < n_list; base += PASS) {
+        issue(s_list, base + slot * NB, n_list, CH);
         fold_rows<T, NB>(st, qr, kr, vr, live, scale);
     }
     store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2));
