@@ -128,9 +128,9 @@ __device__ __forceinline__ void load_rank4(const uint32_t* __restrict__ hist, ui
 // the selection is spread evenly a chunk holds about k * chunk / tokens
 // selected tokens; the chunk is the largest one expected to hold at most
 // kChunkSelected of them.  At most 64 chunks; kpt from kChunkKpt (at most
-// 32 keys per thread).  Measured at C1 (32K tokens, k = 4095): 256 selected
-// per chunk (16 chunks of 2048) 32.1-32.4 us per layer step, 192 (22 of
-// 1536) 33.3, 384 (11 of 3072) 33.8, 512 (8 of 4096) 31.7.
+// 32 keys per thread).  Measured at C1 (32K tokens, k = 4095) with 10 rows
+// per slot and gather pass: 256 selected per chunk (16 chunks of 2048)
+// 30.5 us per layer step, 192 (22 chunks of 1536) 33.6 us.
 constexpr int kChunkSelected = 256;
 constexpr int kChunkKpt[] = {1, 2, 4, 6, 8, 12, 16, 24, 32};
 
