@@ -847,6 +847,97 @@ __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     Elem<T>::store(out + static_cast<int64_t>(h) * D, lane + 64, num1 / den);
 }
 
+// Merge for many splits (dense layers: one split per 512 tokens): four
+// waves per head, wave w folding splits [16w, 16w + 16), [64 + 16w, ...) --
+// each batch of 16 in one load burst -- into a running (m, l, acc) state;
+// wave 0 then combines the four states with the current token.  The layer
+// step's merge (at most 16 splits at C1) keeps the one-wave kernel above.
+constexpr int kMergeWaves = 4;
+
+template <typename T>
+__global__ __launch_bounds__(kWave * kMergeWaves) void attn_merge_wide_kernel(
+    const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
+    const T* __restrict__ cur_v, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
+    T* __restrict__ out, int64_t* __restrict__ idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current) {
+    constexpr int D = 128, S = D + 2;
+    const int h = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    if (idx_out != nullptr && threadIdx.x == 0) idx_out[static_cast<int64_t>(h) * idx_stride + idx_slot] = current;
+    const int64_t kvh = head_to_kv != nullptr
+                            ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
+                            : h / (static_cast<int>(gridDim.x) / kv_heads);
+    const float* ps = partials + static_cast<int64_t>(h) * nsplit * S;
+    float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
+    if (wave == 0) {  // the current token's operands, in flight during the splits
+        const T* qh = q + static_cast<int64_t>(h) * D;
+        q0 = Elem<T>::load(qh, lane);
+        q1 = Elem<T>::load(qh, lane + 64);
+        k0 = Elem<T>::load(cur_k + kvh * D, lane);
+        k1 = Elem<T>::load(cur_k + kvh * D, lane + 64);
+        v0 = Elem<T>::load(cur_v + kvh * D, lane);
+        v1 = Elem<T>::load(cur_v + kvh * D, lane + 64);
+    }
+    float wm = -INFINITY, wl = 0.0f, a0 = 0.0f, a1 = 0.0f;
+    for (int s0 = wave * kMergeFirst; s0 < nsplit; s0 += kMergeWaves * kMergeFirst) {
+        const int nb = min(kMergeFirst, nsplit - s0);
+        float m = -INFINITY, l = 0.0f;
+        if (lane < nb) {
+            m = ps[static_cast<int64_t>(s0 + lane) * S];
+            l = ps[static_cast<int64_t>(s0 + lane) * S + 1];
+        }
+        float c0[kMergeFirst], c1[kMergeFirst];
+#pragma unroll
+        for (int j = 0; j < kMergeFirst; ++j) {
+            const int64_t so = static_cast<int64_t>(s0 + min(j, nb - 1)) * S + 2;
+            c0[j] = ps[so + lane];
+            c1[j] = ps[so + lane + 64];
+        }
+        const float nm = fmaxf(wm, wave_max(m));
+        const float alpha = wm == -INFINITY ? 0.0f : __expf(wm - nm);
+        const float w = m == -INFINITY ? 0.0f : __expf(m - nm);
+        wl = wl * alpha + wave_sum(l * w);
+        a0 *= alpha;
+        a1 *= alpha;
+#pragma unroll
+        for (int j = 0; j < kMergeFirst; ++j) {
+            if (j < nb) {
+                const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+                a0 = fmaf(ws, c0[j], a0);
+                a1 = fmaf(ws, c1[j], a1);
+            }
+        }
+        wm = nm;
+    }
+    __shared__ float s_m[kMergeWaves], s_l[kMergeWaves], s_a[kMergeWaves][D];
+    if (lane == 0) {
+        s_m[wave] = wm;
+        s_l[wave] = wl;
+    }
+    s_a[wave][lane] = a0;
+    s_a[wave][lane + 64] = a1;
+    __syncthreads();
+    if (wave == 0) {
+        const float cur_m = wave_sum(q0 * k0 + q1 * k1) * scale;
+        float mx = cur_m;
+#pragma unroll
+        for (int w = 0; w < kMergeWaves; ++w) mx = fmaxf(mx, s_m[w]);
+        const float wc = __expf(cur_m - mx);
+        float den = wc, num0 = wc * v0, num1 = wc * v1;
+#pragma unroll
+        for (int w = 0; w < kMergeWaves; ++w) {
+            if (s_m[w] != -INFINITY) {
+                const float f = __expf(s_m[w] - mx);
+                den += s_l[w] * f;
+                num0 = fmaf(f, s_a[w][lane], num0);
+                num1 = fmaf(f, s_a[w][lane + 64], num1);
+            }
+        }
+        Elem<T>::store(out + static_cast<int64_t>(h) * D, lane, num0 / den);
+        Elem<T>::store(out + static_cast<int64_t>(h) * D, lane + 64, num1 / den);
+    }
+}
+
 // API-path partial attention, fast form (head_dim 128, contiguous K/V rows,
 // the reference's 256-row splits, 16-byte aligned index rows): row slot q
 // owns the split's entries [16q, 16q + 16) and reads them with 16-byte
@@ -1108,10 +1199,16 @@ hipError_t launch_merge_current_t(const float* partials, int nsplit, const void*
                                   int64_t* idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current,
                                   hipStream_t stream) {
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
-    hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kWave), 0,
-                       stream, partials, nsplit, static_cast<const T*>(q), static_cast<const T*>(cur_k),
-                       static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out), idx_out, idx_stride,
-                       idx_slot, current);
+    if (nsplit > kMergeFirst)
+        hipLaunchKernelGGL((attn_merge_wide_kernel<T>), dim3(static_cast<unsigned>(q_heads)),
+                           dim3(kWave * kMergeWaves), 0, stream, partials, nsplit, static_cast<const T*>(q),
+                           static_cast<const T*>(cur_k), static_cast<const T*>(cur_v), h2k, kv_heads, scale,
+                           static_cast<T*>(out), idx_out, idx_stride, idx_slot, current);
+    else
+        hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kWave), 0,
+                           stream, partials, nsplit, static_cast<const T*>(q), static_cast<const T*>(cur_k),
+                           static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out), idx_out,
+                           idx_stride, idx_slot, current);
     return hipGetLastError();
 }
 }  // namespace
@@ -1171,7 +1268,7 @@ hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t
     switch (q_heads / kv_heads) {
         case 1: POPKV_DENSE((sizeof(T) == 4 ? 8 : 16), 1); break;
         case 2: POPKV_DENSE(8, 2); break;
-        case 4: POPKV_DENSE(8, 4); break;
+        case 4: POPKV_DENSE(4, 4); break;  // 127 VGPRs; 8 rows: 180 (measured 0.3 us slower)
         default: POPKV_DENSE(4, 8); break;
     }
 #undef POPKV_DENSE
