@@ -429,9 +429,11 @@ def test_layer_step_batch_laid_along_heads_equals_per_sequence_steps():
 
 
 @pytest.mark.parametrize("context,dtype", [(3000, torch.bfloat16), (700, torch.float32), (1, torch.bfloat16),
-                                           (1537, torch.float16)])
+                                           (1537, torch.float16), (12000, torch.bfloat16), (40000, torch.bfloat16)])
 def test_dense_attention_matches_oracle(context, dtype):
-    """The full layers: every prefix token plus the current one."""
+    """The full layers: every prefix token plus the current one.  12000 and
+    40000 tokens give 24 and 79 splits of 512: the four-wave merge, with a
+    second batch round for 79."""
     base = workloads.scaled(workloads.C1, context=context, budget=2)
     w = workloads.Workload(base.name, base.method, base.q_heads, base.kv_heads, 128, context, 2, base.token_group,
                            base.dim_group, dtype, 5, context > 1)
