@@ -156,30 +156,60 @@ __device__ __forceinline__ int rep_popc(const uint32_t* x, int r) {
     else return __popc(x[r / 2] & rep_mask<16>(r, r / 2));
 }
 
-// Four signed agreement counts of representative r (2*popc(x & sel) -
-// popc(sel) over its G dims), combined with the fp32 chain of the reference.
-// pq = popc(query mag bits of r), pk = popc(key mag bits of r): they depend
-// on one side only and are computed once per head / token by the caller.
+// popc(x) + acc as one v_bcnt_u32_b32 (its accumulate operand).  Written
+// out because the compiler re-associates 2 * (popc(x0) + popc(x1)) - p into
+// an add-shift and a subtract instead of two accumulating counts and one
+// shift-add.
+__device__ __forceinline__ int popc_acc(uint32_t x, int acc) {
+    int r;
+    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
+    return r;
+}
+
+// -p, opaque to the compiler, so that 2 * c - p stays one shift-add
+// (v_lshl_add_u32) instead of a shift and a subtract.
+__device__ __forceinline__ int neg_opaque(int p) {
+    int r;
+    asm("v_sub_u32 %0, 0, %1" : "=v"(r) : "v"(p));
+    return r;
+}
+
+// Four signed agreement counts of representative r over its G dims,
+// combined with the fp32 chain of the reference:
+//   cs  = 2*popc(m) - G,               m = ~(qs ^ ks)
+//   cq  = 2*popc(m & qm) - popc(qm)
+//   ck  = 2*popc(m & km) - popc(km)
+//   cqk = 2*popc(m & qm & km) - popc(qm & km)
+// with popc(qm & km) - G counted as popc(~(qm & km)) down from -G, so each
+// count is one accumulating popcount per word and one shift-add.
+// npq = -popc(query mag bits of r), npk = -popc(key mag bits of r): they
+// depend on one side only and are formed once per head / token by the caller.
 template <int G>
 __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm, const uint32_t* ks,
-                                          const uint32_t* km, int r, int pq, int pk, float ql, float dq,
+                                          const uint32_t* km, int r, int npq, int npk, float ql, float dq,
                                           float kl, float dk) {
     constexpr int NW = G == 64 ? 2 : 1;
     const int w0 = G == 64 ? 2 * r : (G == 32 ? r : r / 2);
-    int a = 0, aq = 0, ak = 0, aqk = 0, b = 0;
+    int a = 0, aq = 0, ak = 0, aqk = 0, nb = -G;
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
         const int w = w0 + i;
         const uint32_t sel = G == 16 ? rep_mask<16>(r, w) : 0xffffffffu;
         const uint32_t m = ~(qs[w] ^ ks[w]) & sel;
-        const uint32_t both = qm[w] & km[w] & sel;
-        a += __popc(m);
-        aq += __popc(m & qm[w]);
-        ak += __popc(m & km[w]);
-        aqk += __popc(m & both);
-        b += __popc(both);
+        if (i == 0) {
+            a = __popc(m);
+            aq = __popc(m & qm[w]);
+            ak = __popc(m & km[w]);
+            aqk = __popc(m & qm[w] & km[w]);
+        } else {
+            a = popc_acc(m, a);
+            aq = popc_acc(m & qm[w], aq);
+            ak = popc_acc(m & km[w], ak);
+            aqk = popc_acc(m & qm[w] & km[w], aqk);
+        }
+        nb = popc_acc(~(qm[w] & km[w]) & sel, nb);  // popc(~both) - G = -popc(both)
     }
-    const int cs = 2 * a - G, cq = 2 * aq - pq, ck = 2 * ak - pk, cqk = 2 * aqk - b;
+    const int cs = 2 * a - G, cq = 2 * aq + npq, ck = 2 * ak + npk, cqk = 2 * aqk + nb;
     return fmaf(ql * kl, static_cast<float>(cs),
                 fmaf(dq * kl, static_cast<float>(cq),
                      fmaf(ql * dk, static_cast<float>(ck), dq * dk * static_cast<float>(cqk))));
@@ -360,7 +390,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     // Token-side operands, decoded once and reused for every head.
     uint32_t ks[TPT][4], km[TPT][4];
     float kl[TPT][R], dk[TPT][R];
-    int pk[TPT][R];
+    int npk[TPT][R];
 #pragma unroll
     for (int it = 0; it < TPT; ++it) {
         ks[it][0] = s4[it].x; ks[it][1] = s4[it].y; ks[it][2] = s4[it].z; ks[it][3] = s4[it].w;
@@ -380,7 +410,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
             dk[it][2 * i] = bits_f16(dws[i] & 0xffffu); dk[it][2 * i + 1] = bits_f16(dws[i] >> 16);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) pk[it][r] = rep_popc<G>(km[it], r);
+        for (int r = 0; r < R; ++r) npk[it][r] = neg_opaque(rep_popc<G>(km[it], r));
     }
     for (int h = 0; h < qpk; ++h) {
         // The group state is uniform but stays in vector registers (plain LDS
@@ -394,12 +424,12 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
             qs[w] = st.qs[h][w];
             qm[w] = st.qm[h][w];
         }
-        int pq[R];
+        int npq[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             ql[r] = st.ql[h][r];
             dq[r] = st.qd[h][r];
-            pq[r] = rep_popc<G>(qm, r);
+            npq[r] = neg_opaque(rep_popc<G>(qm, r));
         }
         uint16_t* srow = scores + (qrow0 + h) * out_stride;
         // every token's score first, without a branch (a token past the end
@@ -410,7 +440,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
         for (int it = 0; it < TPT; ++it) {
             float total = 0.0f;
 #pragma unroll
-            for (int r = 0; r < R; ++r) total = total + rep_term<G>(qs, qm, ks[it], km[it], r, pq[r], pk[it][r], ql[r], dq[r],
+            for (int r = 0; r < R; ++r) total = total + rep_term<G>(qs, qm, ks[it], km[it], r, npq[r], npk[it][r], ql[r], dq[r],
                                                            kl[it][r], dk[it][r]);
             scs[it] = total * 0x1.6a09e6p-4f;  // fp32(1/sqrt(128)) = 0x3DB504F3
         }
@@ -420,21 +450,24 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
             if (t >= tokens) break;
             const float sc = scs[it];
             const uint16_t bits = f16_rne(sc);
-            const uint32_t off = static_cast<uint32_t>(t);  // tokens < 2^31
+            // byte offset as 32 bits (tokens < 2^31): the store then takes the
+            // row base from scalar registers and this offset from one VGPR
+            const uint32_t off = 2u * static_cast<uint32_t>(t);
+            uint16_t* dst = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(srow) + off);
             if constexpr (STEP) {
-                // order_key(bits): bits 0..14 flip with the sign (s = 0 or
-                // all ones), bit 15 always flips; the bits above 15 are left
+                // order_key(bits): b ^ (s | 0x8000) with s = bit 15
+                // sign-extended -- every bit flips for a negative value, only
+                // bit 15 for a non-negative one; the bits above 15 are left
                 // as garbage (the store keeps 16 bits, the histogram takes
                 // bits 8..15).  The NaN test is done on the fp32 value (an
                 // fp32 NaN is exactly an fp16 NaN after the conversion).
                 const uint32_t b = bits;
-                const uint32_t sgn = static_cast<uint32_t>(static_cast<int32_t>(b << 16) >> 31);
-                const uint32_t flipped = ((b ^ sgn) & 0x7fffu) | (~b & ~0x7fffu);
-                const uint32_t key = sc != sc ? 0xffffu : flipped;
-                srow[off] = static_cast<uint16_t>(key);
+                const uint32_t sgn = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(b), 15, 1));
+                const uint32_t key = sc != sc ? 0xffffu : b ^ (sgn | 0x8000u);
+                *dst = static_cast<uint16_t>(key);
                 atomicAdd(&s_hist[h][(key >> 8) & 0xffu], 1u);
             } else {
-                srow[off] = bits;
+                *dst = bits;
             }
         }
     }
