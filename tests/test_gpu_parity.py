@@ -491,7 +491,8 @@ def test_topk_workspace_reused_across_row_counts():
     """The select keeps per-row histograms at the start of its workspace; a
     call with more rows than the last one must not see the keys a smaller
     call left there (the Python wrapper clears the larger region)."""
-    for rows, tokens, seed in ((32, 5000, 1), (8, 3000, 2), (32, 5000, 3), (40, 700, 4)):
+    for rows, tokens, seed in ((32, 5000, 1), (8, 3000, 2), (32, 5000, 3), (40, 700, 4), (24, 30000, 5),
+                               (40, 9000, 6)):
         s = _scores("random", rows, tokens, seed=seed)
         for k in (1, 257, tokens - 1):
             ours = topk.topk_indices(s, k).cpu().numpy()
@@ -517,7 +518,7 @@ def test_layer_step_workspace_reused_across_head_counts():
         np.testing.assert_allclose(f32(o), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
 
 
-@pytest.mark.parametrize("tokens", [1000, 4095])
+@pytest.mark.parametrize("tokens", [1000, 4095, 32767])
 def test_select_int32_output_through_the_c_abi(tokens):
     """popkv_topk_select with int32 indices (row stride k + 3): the same
     selection as the oracle, current token in slot k, padding untouched."""
