@@ -39,8 +39,8 @@ N_BUFFERS = 8
 # dispatch), each scaled by the same counter on a plain 256 MiB copy
 # (bench.py --copy-calibration): FETCH_SIZE reads 131084.4 KiB for the copy's
 # 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).
-# attn_select_chunk_kernel: FETCH_SIZE 28654.0 KiB, WRITE_SIZE 292.0 KiB.
-ATTN_TRAFFIC_BYTES = round(28654.0 * 1024 * (262144 / 131084.4) + 292.0 * 1024)
+# attn_select_chunk_kernel: FETCH_SIZE 28655.2 KiB, WRITE_SIZE 292.0 KiB.
+ATTN_TRAFFIC_BYTES = round(28655.2 * 1024 * (262144 / 131084.4) + 292.0 * 1024)
 
 
 def parse_args():
