@@ -237,11 +237,11 @@ struct GroupState {
 // query loads are issued ahead of the token loads).  Each wave forms the
 // whole-head extrema, the sign/magnitude words and, for every dimension, its
 // contribution to the low and to the high bucket (|q| or +0), staged in LDS.
-// One thread per (head, representative) then runs the two
-// ascending-dimension fp32 add chains over those contributions -- adding +0
-// for the other bucket is exact, so this is the reference's fold -- and the
-// bucket counts are popcounts of the magnitude words.  All threads of the
-// block call it.
+// Two threads per (head, representative) then run the two
+// ascending-dimension fp32 add chains over those contributions, one each --
+// adding +0 for the other bucket is exact, so this is the reference's fold --
+// and the bucket counts are popcounts of the magnitude words.  All threads of
+// the block call it.
 template <int G, int MAXW>
 __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk, GroupState<G>& st,
                                                   float (*lo_c)[128], float (*hi_c)[128]) {
@@ -271,29 +271,34 @@ __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk,
         }
     }
     __syncthreads();
-    for (int item = threadIdx.x; item < qpk * R; item += kScoreThreads) {
-        const int h = item / R, r = item % R;
-        float ls = 0.0f, hs = 0.0f;
-        // a partial unroll: fully unrolled, the compiler loads all 2G
-        // contributions before the (sequential) add chains, which alone takes
-        // 2G registers and caps the scorer's occupancy
+    // two threads per (head, rep): the even one runs the low-bucket chain,
+    // the odd one the high-bucket chain (an even item count, so a pair is
+    // always active together), then the even one finishes the rep
+    for (int item = threadIdx.x; item < 2 * qpk * R; item += kScoreThreads) {
+        const int hr = item >> 1, h = hr / R, r = hr % R;
+        const float* src = (item & 1) ? &hi_c[h][r * G] : &lo_c[h][r * G];
+        float sum = 0.0f;
+        // a partial unroll: fully unrolled, the compiler loads all G
+        // contributions before the (sequential) add chain, which takes G
+        // registers and caps the scorer's occupancy
 #pragma unroll 4
         for (int j = 0; j < G; j += 4) {
-            const float4 l4 = *reinterpret_cast<const float4*>(&lo_c[h][r * G + j]);
-            const float4 h4 = *reinterpret_cast<const float4*>(&hi_c[h][r * G + j]);
-            ls = ls + l4.x; ls = ls + l4.y; ls = ls + l4.z; ls = ls + l4.w;
-            hs = hs + h4.x; hs = hs + h4.y; hs = hs + h4.z; hs = hs + h4.w;
+            const float4 v = *reinterpret_cast<const float4*>(src + j);
+            sum = sum + v.x; sum = sum + v.y; sum = sum + v.z; sum = sum + v.w;
         }
-        // high-bucket count: popcount of the G magnitude bits at r*G
-        int hn = 0;
+        const float hs = __shfl_xor(sum, 1);
+        if ((item & 1) == 0) {
+            // high-bucket count: popcount of the G magnitude bits at r*G
+            int hn = 0;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            if ((w + 1) * 32 <= r * G || w * 32 >= (r + 1) * G) continue;
-            uint32_t bits = st.qm[h][w];
-            if constexpr (G == 16) bits = (r & 1) ? (bits >> 16) : (bits & 0xffffu);
-            hn += __popc(bits);
+            for (int w = 0; w < 4; ++w) {
+                if ((w + 1) * 32 <= r * G || w * 32 >= (r + 1) * G) continue;
+                uint32_t bits = st.qm[h][w];
+                if constexpr (G == 16) bits = (r & 1) ? (bits >> 16) : (bits & 0xffffu);
+                hn += __popc(bits);
+            }
+            finish_rep(sum, G - hn, hs, hn, st.ql[h][r], st.qd[h][r]);
         }
-        finish_rep(ls, G - hn, hs, hn, st.ql[h][r], st.qd[h][r]);
     }
     __syncthreads();
 }

@@ -20,6 +20,8 @@
 // writes each chunk's low-byte histogram of the threshold's high-byte bin;
 // the fused select + attention kernel (attention.hip) then derives T per
 // chunk and selects and attends in the same workgroup.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 #include "select_common.h"
@@ -84,6 +86,34 @@ __global__ __launch_bounds__(kKeyHistThreads) void key_hist_kernel(const uint16_
             const uint4 b = reinterpret_cast<const uint4*>(src)[1];
             w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
             w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        } else if (!VEC && t0 + kKeyHistTokens <= tokens) {
+            // a row that is not 16-byte aligned (an odd row stride): the 16-byte
+            // blocks holding the thread's 32 bytes (two when the row is aligned,
+            // else three; each holds at least one of those bytes, so none
+            // reaches past the scores' own 16-byte blocks), then the 16-bit
+            // shift and the word offset of the row's misalignment, uniform over
+            // the block
+            const uintptr_t addr = reinterpret_cast<uintptr_t>(src);
+            const uint32_t mis = static_cast<uint32_t>(addr & 15u);  // even
+            const uint4* blk = reinterpret_cast<const uint4*>(addr - mis);
+            uint32_t x[12];
+            const uint4 a = blk[0], b = blk[1];
+            const uint4 c = mis != 0u ? blk[2] : make_uint4(0u, 0u, 0u, 0u);
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+            x[8] = c.x; x[9] = c.y; x[10] = c.z; x[11] = c.w;
+            const uint32_t sh = mis & 3u;  // 0 or 2 bytes
+            auto take = [&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+#pragma unroll
+                for (int i = 0; i < kKeyHistTokens / 2; ++i) w[i] = __builtin_amdgcn_alignbyte(x[q + i + 1], x[q + i], sh);
+            };
+            switch (mis >> 2) {
+                case 0: take(std::integral_constant<int, 0>{}); break;
+                case 1: take(std::integral_constant<int, 1>{}); break;
+                case 2: take(std::integral_constant<int, 2>{}); break;
+                default: take(std::integral_constant<int, 3>{}); break;
+            }
         } else {
             // element loads, all issued before use (indices past the row's
             // end re-read its last element and are not counted below)
