@@ -745,6 +745,156 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_gqa_kernel(
     }
 }
 
+// Dense attention for GQA groups of four query heads in 16-bit types, with
+// Q.K on the matrix cores: per 16-token tile one v_mfma_f32_16x16x32 chain
+// (4 steps of 32 dims) multiplies A = the group's query rows (rows 0-3; rows
+// 4-15 zero) by B = the tile's K rows (column n = token n), so lanes 0-15
+// end with the four heads' logits of token `lane` (C layout: lane l holds
+// rows 4*(l/16) .. +3 of column l % 16; A and B: lane l holds k-elements
+// 8*(l/16) .. +7 of row / column l % 16).  The tile's softmax runs on those
+// lanes (DPP row maxima, one running max per head and wave), the weights go
+// through LDS to the four 16-lane row slots, and each slot folds 4 of the
+// tile's V rows into its accumulators (8 dims per lane) with the VALU.
+// Workgroup (split, KV head) = 4 waves of 128 tokens; tiles double-buffered
+// (the next tile's K and V loads issued before the current tile is folded).
+template <typename T> struct MfmaVec8;
+template <> struct MfmaVec8<bf16_t> { typedef __bf16 type __attribute__((ext_vector_type(8))); };
+template <> struct MfmaVec8<f16_t> { typedef _Float16 type __attribute__((ext_vector_type(8))); };
+typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ mfma_f32x4 mfma_16x16x32(uint4 a, uint4 b, mfma_f32x4 c) {
+    using V = typename MfmaVec8<T>::type;
+    if constexpr (std::is_same_v<T, bf16_t>)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(V, a), __builtin_bit_cast(V, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(V, a), __builtin_bit_cast(V, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kAttnThreads) void attn_dense_mfma_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
+    int64_t tokens, float scale, float* __restrict__ partials, int nsplit) {
+    constexpr int D = 128, QPK = 4, TILE = 16;
+    constexpr int WTOK = kDenseSplit / kAttnWaves;  // tokens per wave
+    constexpr int NT = WTOK / TILE;                  // tiles per wave
+    const int g = blockIdx.y;
+    const int s = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int col = lane & 15;  // MFMA row / column; the V dim slice 8*col
+    const int grp = lane >> 4;  // MFMA k-group; the V row slot
+    const int t0 = s * kDenseSplit;
+    const int n_rows = static_cast<int>(min<int64_t>(kDenseSplit, tokens - t0));
+    const int w0 = wave * WTOK;
+    uint4 qa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        qa[i] = col < QPK ? *reinterpret_cast<const uint4*>(q + static_cast<int64_t>(g * QPK + col) * D + 32 * i + 8 * grp)
+                          : make_uint4(0u, 0u, 0u, 0u);
+    const char* kb = reinterpret_cast<const char*>(kc + g * k_hs) + 8 * grp * sizeof(T);
+    const char* vb = reinterpret_cast<const char*>(vc + g * v_hs) + 8 * col * sizeof(T);
+    // rows past the split's end re-read the split's first row (weight 0)
+    auto load_tile = [&](int it, uint4 (&kt)[4], uint4 (&vt)[4]) {
+        const int rk = w0 + it * TILE + col;
+        const uint32_t ko = static_cast<uint32_t>(t0 + (rk < n_rows ? rk : 0)) * (D * sizeof(T));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kt[i] = *reinterpret_cast<const uint4*>(kb + ko + 32 * i * sizeof(T));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rv = w0 + it * TILE + 4 * grp + r;
+            const uint32_t vo = static_cast<uint32_t>(t0 + (rv < n_rows ? rv : 0)) * (D * sizeof(T));
+            vt[r] = *reinterpret_cast<const uint4*>(vb + vo);
+        }
+    };
+    __shared__ float4 s_p[kAttnWaves][TILE];
+    float m_run[QPK], lsum[QPK], acc[QPK][8];
+#pragma unroll
+    for (int j = 0; j < QPK; ++j) {
+        m_run[j] = -INFINITY;
+        lsum[j] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[j][d] = 0.0f;
+    }
+    auto fold_tile = [&](int it, const uint4 (&kt)[4], const uint4 (&vt)[4]) {
+        mfma_f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c = mfma_16x16x32<T>(qa[i], kt[i], c);
+        const bool live = w0 + it * TILE + col < n_rows;
+        float p[QPK], alpha[QPK];
+        bool rescale = false;
+#pragma unroll
+        for (int j = 0; j < QPK; ++j) {
+            const float sj = live ? c[j] * scale : -INFINITY;
+            float mx = fmaxf(sj, dpp_mov<0xB1>(sj));
+            mx = fmaxf(mx, dpp_mov<0x4E>(mx));
+            mx = fmaxf(mx, dpp_mov<0x141>(mx));
+            mx = fmaxf(mx, dpp_mov<0x140>(mx));
+            const float mt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 0));
+            const float mn = fmaxf(m_run[j], mt);
+            alpha[j] = mn == -INFINITY ? 1.0f : __expf(m_run[j] - mn);  // m_run = -inf gives 0
+            p[j] = mn == -INFINITY ? 0.0f : __expf(sj - mn);           // dead rows give 0
+            rescale = rescale || mn != m_run[j];
+            m_run[j] = mn;
+        }
+        if (lane < TILE) s_p[wave][col] = make_float4(p[0], p[1], p[2], p[3]);
+        // the wave reads its own weights next: one wave's LDS operations complete in order
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (rescale) {  // wave-uniform: some head's running max moved
+#pragma unroll
+            for (int j = 0; j < QPK; ++j) {
+                lsum[j] *= alpha[j];
+#pragma unroll
+                for (int d = 0; d < 8; ++d) acc[j][d] *= alpha[j];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float4 pr = s_p[wave][4 * grp + r];
+            Raw8<T> v;
+            v.u = vt[r];
+            float vf[8];
+#pragma unroll
+            for (int d = 0; d < 8; ++d) vf[d] = v.get(d);
+            const float pj[QPK] = {pr.x, pr.y, pr.z, pr.w};
+#pragma unroll
+            for (int j = 0; j < QPK; ++j) {
+                lsum[j] += pj[j];
+#pragma unroll
+                for (int d = 0; d < 8; ++d) acc[j][d] = fmaf(pj[j], vf[d], acc[j][d]);
+            }
+        }
+        // the next tile's weights overwrite s_p[wave] only after every lane has read
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // a ring of AHEAD + 1 tiles: tile it + AHEAD is issued before tile it is
+    // folded (fully unrolled, so every ring index is a constant)
+    constexpr int AHEAD = 1;
+    uint4 kt[AHEAD + 1][4], vt[AHEAD + 1][4];
+#pragma unroll
+    for (int it = 0; it < AHEAD; ++it) load_tile(it, kt[it], vt[it]);
+#pragma unroll
+    for (int it = 0; it < NT; ++it) {
+        if (it + AHEAD < NT) load_tile(it + AHEAD, kt[(it + AHEAD) % (AHEAD + 1)], vt[(it + AHEAD) % (AHEAD + 1)]);
+        fold_tile(it, kt[it % (AHEAD + 1)], vt[it % (AHEAD + 1)]);
+    }
+#pragma unroll
+    for (int j = 0; j < QPK; ++j) {
+        SoftmaxState st;
+        st.m = m_run[j];
+        st.l = lsum[j];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) st.acc[d] = acc[j][d];
+        store_partial<16>(st, lane, wave, 8 * col, D,
+                          partials + (static_cast<int64_t>(g * QPK + j) * nsplit + s) * (D + 2));
+        __syncthreads();  // store_partial's LDS is reused by the next head
+    }
+}
+
 // Layer-step merge: the split states of head h plus the current token
 // (logit q.cur_k * scale, value cur_v), written in the query dtype.  One
 // wave per head, lane l owning dims l and l + 64, and no LDS or barrier:
@@ -1265,6 +1415,13 @@ hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t
 #define POPKV_DENSE(NB, QPK)                                                                                   \
     hipLaunchKernelGGL((attn_dense_gqa_kernel<T, NB, QPK>), grid, dim3(kAttnThreads), 0, stream, q_, k_, v_, k_hs, \
                        v_hs, tokens, scale, partials, nsplit)
+    if constexpr (sizeof(T) == 2) {
+        if (q_heads == 4 * kv_heads) {
+            hipLaunchKernelGGL((attn_dense_mfma_kernel<T>), grid, dim3(kAttnThreads), 0, stream, q_, k_, v_, k_hs, v_hs,
+                               tokens, scale, partials, nsplit);
+            return hipGetLastError();
+        }
+    }
     switch (q_heads / kv_heads) {
         case 1: POPKV_DENSE((sizeof(T) == 4 ? 8 : 16), 1); break;
         case 2: POPKV_DENSE(8, 2); break;
