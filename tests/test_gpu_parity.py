@@ -447,6 +447,26 @@ def test_dense_attention_matches_oracle(context, dtype):
     np.testing.assert_allclose(f32(out), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
 
 
+@pytest.mark.parametrize("q_heads,kv_heads,dtype", [(8, 8, torch.bfloat16), (8, 4, torch.float16),
+                                                     (16, 2, torch.bfloat16), (8, 2, torch.float16),
+                                                     (16, 4, torch.float32)])
+def test_dense_attention_group_sizes(q_heads, kv_heads, dtype):
+    """Dense layers at every GQA group size the launcher distinguishes: 1, 2
+    and 8 query heads per KV head (VALU kernel), 4 in fp16 (matrix-core
+    kernel) and 4 in fp32 (VALU kernel); 2100 tokens end in a ragged split."""
+    base = workloads.scaled(workloads.C1, context=2101, budget=2)
+    w = workloads.Workload(base.name, base.method, q_heads, kv_heads, 128, 2101, 2, base.token_group,
+                           base.dim_group, dtype, 9, True)
+    lay = workloads.make_layer(w).to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    L = lay.prefix_tokens
+    out = popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v())
+    idx = np.tile(np.arange(L + 1, dtype=np.int64), (w.q_heads, 1))
+    want = core.attention(f32(lay.queries), f32(lay.prefix_k()), f32(lay.prefix_v()), f32(lay.current_k()),
+                          f32(lay.current_v()), idx, mapping.cpu().numpy())
+    np.testing.assert_allclose(f32(out), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
 def test_retrieval_step_with_torch_topk_hook():
     w = workloads.scaled(workloads.C1, context=3000, budget=512)
     layer, mapping, cache = _layer_setup(w)
