@@ -16,14 +16,19 @@ cannot hold the working set.
 Prints ONE JSON line: µs per layer step (lower is better), the achieved
 algorithmic HBM GB/s of the step, per-stage kernel times of the layer step
 (HIP events recorded between its kernels), the roofline of the dominant
-kernel (the layer step's sparse attention) and a CPU baseline (the C oracle,
-one thread, on a bounded sample of the same workload).
+kernel (the layer step's select + sparse attention), the achievable
+stream-copy bandwidth, and a CPU baseline (the torch-CPU counterpart of the
+reference's readable path on every host thread, a bounded sample of the same
+workload).  ``value`` is the median of --trials trials, each exactly --steps
+consecutive layer steps replayed from one HIP graph.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -48,6 +53,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
+    p.add_argument("--trials", type=int, default=10, help="timed trials of --steps steps (the median is reported)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     p.add_argument("--no-graph", action="store_true", help="time eager launches only")
@@ -89,29 +95,22 @@ def bench_c2(args) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     n_layers, dense_layers = 32, (0, 1)
-    layers = []
+    operands, caches, outs = [], {}, []
     for li in range(n_layers):
         w = workloads.c2_layer(li)
         lay = workloads.make_layer(w).to(dev)
-        L = lay.prefix_tokens
-        cache = None
         if li not in dense_layers:
-            cache = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
-                                            reserve_tokens=128)
-        layers.append((w, lay, cache, torch.empty_like(lay.queries), lay.current_k(), lay.current_v()))
-    w0 = layers[0][0]
-    mapping = workloads.head_to_kv(w0, dev)
-    ws, dws = popkv.LayerStepWorkspace(), popkv.LayerStepWorkspace()
+            caches[li] = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group,
+                                                 dim_group_size=w.dim_group, reserve_tokens=128)
+        operands.append((lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v()))
+        outs.append(torch.empty_like(lay.queries))
+    w0 = workloads.c2_layer(0)
+    stack = popkv.SparseDecodeStack(caches, workloads.head_to_kv(w0, dev), budget=w0.budget,
+                                    full_layers=dense_layers)
     stream = torch.cuda.current_stream(dev)
 
     def stack_step() -> None:
-        for w, lay, cache, out, ck, cv in layers:
-            if cache is None:
-                popkv.dense_attention_step(lay.queries, lay.prefix_k(), lay.prefix_v(), ck, cv, workspace=dws,
-                                           out=out)
-            else:
-                popkv.popkv_layer_step(lay.queries, cache, lay.prefix_k(), lay.prefix_v(), ck, cv, mapping,
-                                       budget=w.budget, workspace=ws, out=out)
+        stack.step(operands, outs)
 
     for _ in range(max(1, args.warmup // 8)):
         stack_step()
@@ -136,7 +135,7 @@ def bench_c2(args) -> int:
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
     L = w0.prefix_tokens
-    sparse_bytes = workloads.algorithmic_bytes(layers[2][0])["step"]
+    sparse_bytes = workloads.algorithmic_bytes(workloads.c2_layer(2))["step"]
     # dense layer: every K/V row of a KV head read once (shared by its GQA
     # group), plus q in / out per query head
     dense_bytes = w0.kv_heads * (L + 1) * w0.head_dim * 2 * 2 + w0.q_heads * w0.head_dim * 2 * 2
@@ -330,39 +329,54 @@ def main() -> int:
         torch.cuda.synchronize()
         return a.elapsed_time(b) / n
 
-    # ---- eager layer steps
+    # ---- eager layer steps (reported beside the graph figure)
     for i in range(args.warmup):
         step(i)
     eager_ms = timed(step, args.steps)
 
-    def graph_timed(fn, reps: int):
-        """Average ms per call of fn(i), captured N_BUFFERS calls to a HIP
-        graph (after a warm-up on a side stream) and replayed `reps` times."""
+    def capture(fn, n: int):
+        """fn(0) .. fn(n - 1) recorded into one HIP graph (after a warm-up
+        pass on a side stream, as torch's graph capture asks)."""
         g = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(dev)
         side.wait_stream(stream)
         with torch.cuda.stream(side):
-            for i in range(N_BUFFERS):
+            for i in range(min(n, N_BUFFERS)):
                 fn(i)
         stream.wait_stream(side)
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
-            for i in range(N_BUFFERS):
+            for i in range(n):
                 fn(i)
         for _ in range(2):
             g.replay()
+        torch.cuda.synchronize()
+        return g
+
+    def graph_timed(fn, reps: int):
+        """Average ms per call of fn(i): N_BUFFERS calls in one HIP graph,
+        replayed `reps` times, HIP events on `stream`."""
+        g = capture(fn, N_BUFFERS)
         return timed(lambda i: g.replay(), reps) / N_BUFFERS
 
-    # ---- HIP-graph replay of N_BUFFERS consecutive layer steps
+    # ---- the timed steps: exactly K consecutive layer steps (rotating the
+    #      N_BUFFERS input sets) in one HIP graph; each trial replays it once,
+    #      bracketed by synchronizations and HIP events on the step's stream;
+    #      value = the median trial / K
     graph_ms = None
+    trial_ms: list[float] = []
     reps = max(1, args.steps // N_BUFFERS)
     if not args.no_graph:
         eager_out = [o.clone() for o in outs]
-        graph_ms = graph_timed(step, reps)
+        g_steps = capture(step, args.steps)
+        for _ in range(max(10, args.trials)):
+            trial_ms.append(timed(lambda i: g_steps.replay(), 1) / args.steps)
+        graph_ms = statistics.median(trial_ms)
         torch.cuda.synchronize()
         if not all(torch.equal(a, b) for a, b in zip(outs, eager_out)):
             print("graph replay changed the layer outputs", file=sys.stderr)
             return 1
+        del g_steps
     ms_per_step = graph_ms if graph_ms is not None else eager_ms
 
     # ---- the dominant kernel alone: the layer step's fused select +
@@ -374,9 +388,11 @@ def main() -> int:
         pk, pv, _ = sets[i % N_BUFFERS]
         popkv.popkv_layer_step_attention(q, pk, pv, mapping, budget=w.budget, workspace=ws)
 
+    aux_reps = max(reps, 25)  # replays of N_BUFFERS launches for the per-kernel / per-stage figures
     for i in range(args.warmup):
         attention_only(i)
-    attn_step_ms = timed(attention_only, args.steps) if args.no_graph else graph_timed(attention_only, reps)
+    attn_step_ms = (timed(attention_only, aux_reps * N_BUFFERS) if args.no_graph
+                    else graph_timed(attention_only, aux_reps))
 
     # ---- prepack of the 32K prefix and the per-token append (re-encode of
     #      the active token group incl. the new token), pack_keys_into into a
@@ -388,7 +404,7 @@ def main() -> int:
     prepack_ms = graph_timed(lambda i: popkv_cuda.pack_keys_into(
         prefix0, scratch, token_offset=0, token_group_size=w.token_group, dim_group_size=w.dim_group), 4)
     append_ms = graph_timed(lambda i: popkv_cuda.pack_keys_into(
-        active, scratch, token_offset=sealed, token_group_size=w.token_group, dim_group_size=w.dim_group), reps)
+        active, scratch, token_offset=sealed, token_group_size=w.token_group, dim_group_size=w.dim_group), aux_reps)
     meta_row = 32 + 4 * (w.head_dim // w.dim_group)
     prepack_bytes = w.kv_heads * L * (w.head_dim * 2 + meta_row)
     append_bytes = w.kv_heads * int(active.shape[1]) * (w.head_dim * 2 + meta_row)
@@ -396,22 +412,26 @@ def main() -> int:
     # ---- reference-API stages (the entry points popkv_cuda / topk /
     #      sparse_kernels expose, same inputs), for comparison with the
     #      reference's per-stage numbers
-    stage_timer = timed if args.no_graph else graph_timed
+    def stage_timer(fn, n):
+        return timed(fn, n * N_BUFFERS) if args.no_graph else graph_timed(fn, n)
+
     enc = popkv_cuda.query_encode(q.unsqueeze(0).contiguous(), dim_group_size=w.dim_group)
     score_ms = stage_timer(lambda i: popkv_cuda.score_encoded(enc, sets[i % N_BUFFERS][2].packed, head_to_kv=mapping,
-                                                              tokens=L, dim_group_size=w.dim_group), reps)
+                                                              tokens=L, dim_group_size=w.dim_group), aux_reps)
     scores = popkv_cuda.score_encoded(enc, sets[0][2].packed, head_to_kv=mapping, tokens=L,
                                       dim_group_size=w.dim_group)
     score_bufs = [scores.clone() for _ in range(N_BUFFERS)]
-    select_ms = stage_timer(lambda i: topk.select_with_current(score_bufs[i % N_BUFFERS], kk, L + 1), reps)
+    select_ms = stage_timer(lambda i: topk.select_with_current(score_bufs[i % N_BUFFERS], kk, L + 1), aux_reps)
     indices = topk.select_with_current(scores, kk, L + 1)
     attn_ms = stage_timer(lambda i: sparse_kernels.indexed_attention_split_partial(
-        q, sets[i % N_BUFFERS][0], sets[i % N_BUFFERS][1], cur_k, cur_v, indices, mapping, split_tokens=256), reps)
+        q, sets[i % N_BUFFERS][0], sets[i % N_BUFFERS][1], cur_k, cur_v, indices, mapping, split_tokens=256),
+        aux_reps)
     encode_ms = stage_timer(lambda i: popkv_cuda.query_encode(q.unsqueeze(0).contiguous(),
-                                                              dim_group_size=w.dim_group), reps)
+                                                              dim_group_size=w.dim_group), aux_reps)
     qpk = w.q_heads // w.kv_heads
     unique_rows = int(sum(torch.unique(indices[h * qpk:(h + 1) * qpk].flatten()).numel() for h in range(w.kv_heads)))
 
+    copy_gbps = stream_copy_gbps(torch, dev, stream)
     step_gbps = alg["step"] / (ms_per_step * 1e-3) / 1e9
     # the fused select + attention kernel: the attention's bytes plus the
     # select's final pass over the key rows
@@ -437,6 +457,13 @@ def main() -> int:
                    "timing": "hip-graph replay" if graph_ms is not None else "eager"},
         "achieved_GBps": round(step_gbps, 1),
         "step_algorithmic_bytes": alg["step"],
+        "step_frac_of_peak": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "stream_copy_GBps": round(copy_gbps, 1),
+        "step_frac_of_stream_copy": round(step_gbps / copy_gbps, 4),
+        "trials": {"count": len(trial_ms), "steps_each": args.steps,
+                   "us_min": round(min(trial_ms) * 1e3, 3) if trial_ms else None,
+                   "us_median": round(statistics.median(trial_ms) * 1e3, 3) if trial_ms else None,
+                   "us_max": round(max(trial_ms) * 1e3, 3) if trial_ms else None},
         "eager_us_per_layer": round(eager_ms * 1e3, 3),
         "graph_us_per_layer": None if graph_ms is None else round(graph_ms * 1e3, 3),
         "api_stages_us": {"query_encode": round(encode_ms * 1e3, 3), "score_encoded": round(score_ms * 1e3, 3),
@@ -450,7 +477,11 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "attn_select_chunk_kernel (layer step select + attention)",
                      "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
-                     "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(attn_step_ms * 1e3, 3)},
+                     "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(attn_step_ms * 1e3, 3),
+                     # DRAM bytes per launch (PMC) over the same time: the GQA heads' shared rows are
+                     # fetched once, so this is below the per-head algorithmic figure
+                     "traffic_GBps": round(ATTN_TRAFFIC_BYTES / (attn_step_ms * 1e-3) / 1e9, 1),
+                     "traffic_frac": round(ATTN_TRAFFIC_BYTES / (attn_step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
@@ -459,38 +490,76 @@ def main() -> int:
     return 0
 
 
-def cpu_baseline(layer, w, budget_s: float) -> dict:
-    """The C oracle (oracle/popkv_oracle.c, one thread) running the same layer
-    step -- fold query encode, GQA popcount scores, top-k select, float64
-    attention over the gathered rows -- on the host, repeated until about
-    `budget_s` seconds have been spent; the median step time is reported."""
-    import numpy as np
+def stream_copy_gbps(torch, dev, stream) -> float:
+    """Achievable HBM bandwidth: a plain device-to-device copy of 1 GiB
+    (1 GiB read + 1 GiB written per copy), median of 10 event-timed copies."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    times = []
+    for _ in range(10):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        dst.copy_(src)
+        b.record(stream)
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) * 1e-3)
+    del src, dst
+    return 2 * n / statistics.median(times) / 1e9
 
-    from oracle import core
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(layer, w, budget_s: float) -> dict:
+    """The torch-CPU counterpart of the reference's readable retrieval path
+    (oracle/torch_cpu.py: dense-reconstruction scores of the prepacked
+    keys, torch.topk + the current token, fp32 attention over the gathered
+    rows) on every host thread this process may use: the same C1 layer step,
+    2 warm-up steps, then steps until about `budget_s` seconds (at least 5);
+    the median step time is reported.  The one-time prefix encode is timed
+    separately."""
+    import torch
+
+    from oracle import torch_cpu
     from popkv_amd import workloads
 
-    L = w.prefix_tokens
-    keys = layer.keys.float().numpy()
-    values = layer.values.float().numpy()
-    q = layer.queries.float().numpy()
-    h2k = workloads.head_to_kv(w).numpy()
-    packed = core.pack_keys(np.ascontiguousarray(keys[:, :L]), token_group_size=w.token_group,
-                            dim_group_size=w.dim_group)
-    pk, pv = np.ascontiguousarray(keys[:, :L]), np.ascontiguousarray(values[:, :L])
-    ck, cv = keys[:, L].copy(), values[:, L].copy()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while not times or (time.perf_counter() < t_end and len(times) < 200):
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
         t0 = time.perf_counter()
-        enc = core.query_encode(q[None], w.dim_group, order="fold")
-        sc = core.score_encoded(enc, packed, head_to_kv=h2k, tokens=L, dim_group_size=w.dim_group)[0]
-        idx = core.select(sc, w.k, L)
-        core.attention(q, pk, pv, ck, cv, idx, h2k)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": 1, "kind": "port",
-            "sample": f"{len(times)} full C1 layer steps (encode+score+select+attention) of the C oracle, "
-                      f"one thread, median; host has {os.cpu_count()} logical CPUs"}
+        cl = torch_cpu.CpuRetrievalLayer(layer.prefix_k(), layer.prefix_v(), workloads.head_to_kv(w),
+                                         token_group=w.token_group, dim_group=w.dim_group)
+        prepack_s = time.perf_counter() - t0
+        q, ck, cv = layer.queries, layer.current_k(), layer.current_v()
+        for _ in range(2):
+            cl.step(q, ck, cv, w.budget)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 500):
+            t0 = time.perf_counter()
+            cl.step(q, ck, cv, w.budget)
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    med = statistics.median(times)
+    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"{len(times)} full {w.name} layer steps (query encode + dense-reconstruction scores of "
+                      f"the prepacked prefix + torch.topk + current token + fp32 attention over the gathered "
+                      f"rows), torch-CPU on {cores} threads, median after 2 warm-ups",
+            "cpu_model": _cpu_model(), "torch": torch.__version__,
+            "host_logical_cpus": os.cpu_count(), "prefix_encode_us": round(prepack_s * 1e6, 1)}
 
 
 if __name__ == "__main__":

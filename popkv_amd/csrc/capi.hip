@@ -335,10 +335,16 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
                                                tokens, dim_group_size, keys, L.score_stride, hist, s),
                   "popkv_layer_step(score)");
     if (st) return st;
+    // From here on the scorer has added into the histogram region, which
+    // must be zero when the next call begins: a failed launch clears it.
+    auto clear_hist = [&](int status) {
+        popkv::launch_fill_u32(hist, q_heads * 256, 0u, s);
+        return status;
+    };
     // 2. per-chunk low-byte histograms of the threshold's high-byte bin
     st = launched(popkv::launch_chunk_hist(keys, L.score_stride, q_heads, tokens, L.k, hist, rec, h2, gt1, s),
                   "popkv_layer_step(chunk histograms)");
-    if (st) return st;
+    if (st) return clear_hist(st);
     // 3. per (chunk, head): the chunk's selected tokens (also written as
     //    int64 at their rank when indices_out is given) and the sparse
     //    attention over them (re-zeroes the histograms),
@@ -349,7 +355,7 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
                                                         gt1, hist, head_to_kv, static_cast<int>(q_heads),
                                                         static_cast<int>(kv_heads), partials, indices_out, L.k + 1, s),
                   "popkv_layer_step(select + attention)");
-    if (st) return st;
+    if (st) return clear_hist(st);
     st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nchunks), queries, dtype, current_k,
                                               current_v, head_to_kv, static_cast<int>(q_heads),
                                               static_cast<int>(kv_heads), output, indices_out, L.k + 1, L.k, tokens,

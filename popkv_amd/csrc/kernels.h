@@ -9,6 +9,9 @@
 
 namespace popkv {
 
+// n 32-bit words of device memory set to `value` (a fill kernel).
+hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t value, hipStream_t stream);
+
 hipError_t launch_pack(const void* keys, int dtype, int64_t kv_heads, int64_t tokens, int head_dim,
                        int64_t key_head_stride, int32_t* k_sign, int32_t* k_mag, uint16_t* k_low,
                        uint16_t* k_delta, int64_t capacity, int64_t token_offset, int token_group_size,

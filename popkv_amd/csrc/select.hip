@@ -502,7 +502,22 @@ __global__ __launch_bounds__(kChunkThreads) void topk_chunk_kernel(
         }
     }
 }
+// n 32-bit words set to `value`: clears histogram regions after a failed
+// launch (a kernel, not hipMemsetAsync, so it also records into HIP graphs).
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t value) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        p[i] = value;
+}
 }  // namespace
+
+hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t value, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(blocks < 1024 ? blocks : 1024)), dim3(256), 0,
+                       stream, p, n, value);
+    return hipGetLastError();
+}
 
 hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows, int64_t row_stride, int64_t tokens,
                             int64_t k, int32_t* list, int64_t list_stride, bool list_current, int64_t* idx64,
@@ -596,15 +611,21 @@ hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_
     const bool i32 = index_dtype == POPKV_INDEX_I32;
     int32_t* out32 = i32 ? static_cast<int32_t*>(indices) : nullptr;
     int64_t* out64 = i32 ? nullptr : static_cast<int64_t*>(indices);
-    if (tokens < kTopkChunkMinTokens)
-        return launch_topk_list(keys, ghist, rows, key_stride, tokens, k, out32, index_row_stride, true, out64,
-                                index_row_stride, current, stream);
+    if (tokens < kTopkChunkMinTokens) {
+        const hipError_t e = launch_topk_list(keys, ghist, rows, key_stride, tokens, k, out32, index_row_stride,
+                                              true, out64, index_row_stride, current, stream);
+        if (e != hipSuccess) launch_fill_u32(ghist, rows * kBins, 0u, stream);
+        return e;
+    }
     uint32_t* rec = reinterpret_cast<uint32_t*>(base + w.rec);
     uint32_t* gt1 = reinterpret_cast<uint32_t*>(base + w.gt1);
     uint16_t* h2 = reinterpret_cast<uint16_t*>(base + w.h2);
     // chunk_hist_kernel runs for 0 < k < tokens only, on step_chunks(tokens, k)
     hipError_t e = launch_chunk_hist(keys, key_stride, rows, tokens, k, ghist, rec, h2, gt1, stream);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) {
+        launch_fill_u32(ghist, rows * kBins, 0u, stream);  // the histograms stay zero between calls
+        return e;
+    }
     const StepChunks ch = step_chunks(tokens, k > 0 && k < tokens ? k : tokens);
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k < tokens ? k : tokens),
               nc = static_cast<int>(ch.count);

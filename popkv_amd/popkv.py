@@ -286,6 +286,80 @@ def layer_step_workspace_bytes(q_heads: int, tokens: int, budget: int, dim_group
     return int(nat.lib().popkv_layer_step_workspace_bytes(q_heads, tokens, budget, dim_group_size))
 
 
+def _check_step_operands(name: str, q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor,
+                         k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None) -> tuple[int, int]:
+    """Shape checks shared by the fused decode entries.
+
+    The C ABI receives raw pointers and head counts only, so every size it
+    derives addresses from is checked before any device call: q [QH, 128];
+    prefix K/V [KVH, L, 128] with contiguous rows; current k/v [KVH, 128];
+    QH a positive multiple of KVH; `out` (when given) a contiguous
+    [QH, 128] tensor.  Raises ValueError (the reference's Python-side
+    checks); dtypes and devices are checked by _check_same_device.
+    Returns (QH, KVH)."""
+    if q.ndim != 2 or int(q.shape[1]) != 128:
+        raise ValueError(f"{name} requires q [query heads, 128]")
+    if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
+        raise ValueError("prefix K/V must be [KV heads, tokens, 128]")
+    if prefix_k.stride(1) != 128 or prefix_k.stride(2) != 1 or prefix_v.stride(1) != 128 or prefix_v.stride(2) != 1:
+        raise ValueError("prefix K/V rows must be contiguous (token stride 128)")
+    q_heads, kv_heads = int(q.shape[0]), int(prefix_k.shape[0])
+    if q_heads <= 0 or kv_heads <= 0 or q_heads % kv_heads != 0:
+        raise ValueError("query heads must be a positive multiple of the KV heads")
+    for t, what in ((k, "current k"), (v, "current v")):
+        if tuple(t.shape) != (kv_heads, 128):
+            raise ValueError(f"{what} must be [KV heads, 128] = [{kv_heads}, 128], got {tuple(t.shape)}")
+    if out is not None:
+        if tuple(out.shape) != (q_heads, 128):
+            raise ValueError(f"out must be [{q_heads}, 128], got {tuple(out.shape)}")
+        if not out.is_contiguous():
+            raise ValueError("out must be contiguous")
+    return q_heads, kv_heads
+
+
+def _check_same_device(name: str, q: torch.Tensor, *tensors: torch.Tensor | None) -> None:
+    """Every operand of q's dtype and on q's CUDA device (RuntimeError, as
+    the reference's TORCH_CHECKs)."""
+    ts = (q,) + tuple(t for t in tensors if t is not None)
+    if any(t.dtype != q.dtype for t in ts):
+        raise RuntimeError("queries, current K/V, prefix K/V and out must share a dtype")
+    if any(not t.is_cuda or t.device != q.device for t in ts):
+        raise RuntimeError(f"{name}: every tensor must be on the same CUDA device")
+
+
+def _check_packed_cache(cache: PopKVCache, kv_heads: int) -> None:
+    """The packed planes the scorer reads: int32 [KVH, cap, 4] sign/mag and
+    fp16 [KVH, cap, 128/G] low/delta with the prefix's KV head count, and
+    token_count within the capacity (ValueError before any device call)."""
+    if len(cache.packed) != 4:
+        raise ValueError("packed must contain (k_sign, k_mag, k_low, k_delta)")
+    if cache.dim_group_size not in (16, 32, 64):
+        raise ValueError("dim_group_size must be one of 16, 32, 64")
+    k_sign = cache.packed[0]
+    cap = int(k_sign.shape[1]) if k_sign.ndim == 3 else -1
+    reps = 128 // cache.dim_group_size
+    for t, dt, width, what in zip(cache.packed, (torch.int32, torch.int32, torch.float16, torch.float16),
+                                  (4, 4, reps, reps), ("k_sign", "k_mag", "k_low", "k_delta")):
+        if tuple(t.shape) != (kv_heads, cap, width):
+            raise ValueError(f"packed {what} must be [{kv_heads}, capacity, {width}], got {tuple(t.shape)}")
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"packed {what} must be a contiguous {dt} tensor")
+    if not 0 < cache.token_count <= cap:
+        raise ValueError("invalid score token count")
+
+
+def _check_packed_device(cache: PopKVCache, device: torch.device) -> None:
+    if any(not t.is_cuda or t.device != device for t in cache.packed):
+        raise RuntimeError("the packed cache must be on the queries' CUDA device")
+
+
+def _check_head_mapping(head_to_kv: torch.Tensor, q_heads: int) -> None:
+    if head_to_kv.ndim != 1 or int(head_to_kv.numel()) != q_heads:
+        raise ValueError(f"head_to_kv must be a vector of {q_heads} KV head indices")
+    if head_to_kv.dtype not in (torch.int64, torch.int32):
+        raise ValueError("head_to_kv must be int64 or int32")
+
+
 def popkv_layer_step(
     q: torch.Tensor, cache: PopKVCache, prefix_k: torch.Tensor, prefix_v: torch.Tensor,
     k: torch.Tensor, v: torch.Tensor, head_to_kv: torch.Tensor, *, budget: int,
@@ -299,20 +373,18 @@ def popkv_layer_step(
     prefix_k/prefix_v: [KVH, L, 128] with unit row stride 128 (any head
     stride); q: [QH, 128]; k, v: [KVH, 128].  Returns out [QH, 128] (and the
     int64 [QH, k+1] selection when return_indices)."""
-    if q.ndim != 2 or int(q.shape[1]) != 128:
-        raise ValueError("popkv_layer_step requires q [query heads, 128]")
-    if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
-        raise ValueError("prefix K/V must be [KV heads, tokens, 128]")
-    if prefix_k.stride(1) != 128 or prefix_k.stride(2) != 1 or prefix_v.stride(1) != 128 or prefix_v.stride(2) != 1:
-        raise ValueError("prefix K/V rows must be contiguous (token stride 128)")
+    q_heads, kv_heads = _check_step_operands("popkv_layer_step", q, prefix_k, prefix_v, k, v, out)
     tokens = int(prefix_k.shape[1])
     if tokens != cache.token_count:
         raise ValueError("prefix length must equal the retrieval cache's token_count")
+    if budget <= 1:
+        raise ValueError("budget must reserve at least one retrieved and one current token")
+    _check_head_mapping(head_to_kv, q_heads)
+    _check_packed_cache(cache, kv_heads)
+    _check_same_device("popkv_layer_step", q, prefix_k, prefix_v, k, v, out)
     dev = q.device
-    q_heads, kv_heads = int(q.shape[0]), int(prefix_k.shape[0])
+    _check_packed_device(cache, dev)
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
-    if any(t.dtype != q.dtype for t in (prefix_k, prefix_v, kc, vc)):
-        raise RuntimeError("queries, current K/V and prefix K/V must share a dtype")
     mapping = head_to_kv.to(device=dev, dtype=torch.int64).contiguous()
     nbytes = layer_step_workspace_bytes(q_heads, tokens, budget, cache.dim_group_size)
     if isinstance(workspace, torch.Tensor):
@@ -361,17 +433,13 @@ def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torc
     k/v [KVH, 128] -> [QH, 128], query head h reading KV head h // (QH/KVH).
     The workspace holds split partials; do not share it with
     popkv_layer_step, whose histogram region must stay zero."""
-    if q.ndim != 2 or int(q.shape[1]) != 128:
-        raise ValueError("dense_attention_step requires q [query heads, 128]")
-    if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
-        raise ValueError("prefix K/V must be [KV heads, tokens, 128]")
-    if prefix_k.stride(1) != 128 or prefix_k.stride(2) != 1 or prefix_v.stride(1) != 128 or prefix_v.stride(2) != 1:
-        raise ValueError("prefix K/V rows must be contiguous (token stride 128)")
+    q_heads, kv_heads = _check_step_operands("dense_attention_step", q, prefix_k, prefix_v, k, v, out)
+    if q_heads // kv_heads not in (1, 2, 4, 8):
+        raise ValueError("dense attention supports 1, 2, 4 or 8 query heads per KV head")
+    _check_same_device("dense_attention_step", q, prefix_k, prefix_v, k, v, out)
     dev = q.device
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
-    if any(t.dtype != q.dtype for t in (prefix_k, prefix_v, kc, vc)):
-        raise RuntimeError("queries, current K/V and prefix K/V must share a dtype")
-    q_heads, kv_heads, tokens = int(q.shape[0]), int(prefix_k.shape[0]), int(prefix_k.shape[1])
+    tokens = int(prefix_k.shape[1])
     nbytes = int(nat.lib().popkv_dense_attention_workspace_bytes(q_heads, tokens))
     ws = (workspace or LayerStepWorkspace()).get(nbytes, dev)
     output = torch.empty_like(qc) if out is None else out
@@ -380,3 +448,46 @@ def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torc
                  prefix_k.stride(0), prefix_v.stride(0), kc.data_ptr(), vc.data_ptr(), q_heads, kv_heads, tokens,
                  output.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_of(dev))
     return output
+
+
+class SparseDecodeStack:
+    """The attention half of one ``LlamaSparseDecoder.decode`` step across a
+    layer stack (popkv.py:1022-1115): a layer listed in ``full_layers`` takes
+    dense attention over every cached token plus the current one
+    (``dense_attention_step``), every other layer the PopKV retrieval step
+    over its ``PopKVCache`` (``popkv_layer_step``).  One workspace serves the
+    sparse layers and one the dense layers, so a whole step records into one
+    HIP graph without allocating.
+
+    caches: layer -> PopKVCache for the sparse layers; head_to_kv: the GQA
+    mapping of the sparse layers (dense layers use h // (QH / KVH))."""
+
+    def __init__(self, caches: dict[int, PopKVCache], head_to_kv: torch.Tensor, *, budget: int,
+                 full_layers: Sequence[int] = (0, 1)) -> None:
+        if budget <= 1:
+            raise ValueError("budget must reserve at least one retrieved and one current token")
+        overlap = set(caches) & set(full_layers)
+        if overlap:
+            raise ValueError(f"layers {sorted(overlap)} are full layers and cannot have a retrieval cache")
+        self.caches = caches
+        self.head_to_kv = head_to_kv
+        self.budget = int(budget)
+        self.full_layers = tuple(full_layers)
+        self.sparse_workspace = LayerStepWorkspace()
+        self.dense_workspace = LayerStepWorkspace()
+
+    def layer(self, layer: int, q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor, k: torch.Tensor,
+              v: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Attention output [QH, 128] of one layer for the current token."""
+        if layer in self.full_layers:
+            return dense_attention_step(q, prefix_k, prefix_v, k, v, workspace=self.dense_workspace, out=out)
+        try:
+            cache = self.caches[layer]
+        except KeyError:
+            raise ValueError(f"layer {layer} is sparse but has no retrieval cache") from None
+        return popkv_layer_step(q, cache, prefix_k, prefix_v, k, v, self.head_to_kv, budget=self.budget,
+                                workspace=self.sparse_workspace, out=out)
+
+    def step(self, operands: Sequence[tuple], outs: Sequence[torch.Tensor] | None = None) -> list[torch.Tensor]:
+        """Every layer in order; operands[layer] = (q, prefix_k, prefix_v, k, v)."""
+        return [self.layer(i, *ops, out=None if outs is None else outs[i]) for i, ops in enumerate(operands)]

@@ -1,0 +1,237 @@
+"""GPU parity at the benchmark configurations of the north star (C0, C2, C3)
+and at every chunk plan of the layer step's select, against the CPU oracle:
+prepack bits, fp16 score bits and selected indices bit-exact, attention
+within 2e-2 max-abs / 1e-2 relative of the float64 materialized reference
+(the reference's own check: tests/test_popkv.py:275-372,
+tests/test_sparse_kernels.py:118-140).  Also pins the tie rule against
+``torch.topk`` on ROCm at the row shapes where PyTorch takes its multi-block
+radix select (the path the reference's decode loop inherits,
+popkv.py:1094-1098).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from popkv_amd import popkv, popkv_cuda, topk, workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+ATTN_ATOL, ATTN_RTOL = 2e-2, 1e-2
+
+
+def f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def _packed_np(cache):
+    return tuple(bits(t) if t.dtype != torch.int32 else t.cpu().numpy() for t in cache.packed)
+
+
+def _setup(w, seed=None):
+    layer = workloads.make_layer(w, seed=seed).to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    cache = popkv.build_popkv_cache(layer.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                    reserve_tokens=64)
+    return layer, mapping, cache
+
+
+def _oracle(w, layer, mapping, cache):
+    """fold encode -> GQA popcount scores -> select -> float64 attention."""
+    L = layer.prefix_tokens
+    enc = core.query_encode(f32(layer.queries)[None], w.dim_group, order="fold")
+    h2k = mapping.cpu().numpy()
+    sc = core.score_encoded(enc, _packed_np(cache), head_to_kv=h2k, tokens=L, dim_group_size=w.dim_group)[0]
+    idx = core.select(sc, w.k, L)
+    out = core.attention(f32(layer.queries), f32(layer.prefix_k()), f32(layer.prefix_v()), f32(layer.current_k()),
+                         f32(layer.current_v()), idx, h2k)
+    return sc, idx, out
+
+
+def _assert_attention(got: torch.Tensor, want: np.ndarray) -> None:
+    err = np.abs(f32(got) - want)
+    assert (err <= ATTN_ATOL + ATTN_RTOL * np.abs(want)).all(), float(err.max())
+
+
+def _check_full_layer(w, *, seed=None, check_prepack=True, api_path=True):
+    """Prepack (bit-exact), the reference-API path (score bits, indices) and
+    the fused layer step (indices exact, attention within tolerance)."""
+    layer, mapping, cache = _setup(w, seed)
+    L = layer.prefix_tokens
+    if check_prepack:
+        want_pack = core.pack_keys(f32(layer.prefix_k()), token_group_size=w.token_group, dim_group_size=w.dim_group)
+        for a, b in zip(_packed_np(cache), want_pack):
+            assert np.array_equal(a[:, :L], b)
+    sc, idx, out = _oracle(w, layer, mapping, cache)
+    if api_path:
+        enc = popkv_cuda.query_encode(layer.queries.unsqueeze(0).contiguous(), dim_group_size=w.dim_group)
+        scores = popkv_cuda.score_encoded(enc, cache.packed, head_to_kv=mapping, tokens=L, dim_group_size=w.dim_group)
+        assert np.array_equal(bits(scores[0]), sc)
+        assert np.array_equal(topk.select_with_current(scores, w.k, L + 1).cpu().numpy(), idx)
+        o1 = popkv.popkv_retrieval_step(layer.queries, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                        layer.current_v(), cache, mapping, budget=w.budget)
+        _assert_attention(o1, out)
+    o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(got.cpu().numpy(), idx)
+    _assert_attention(o, out)
+    return layer, mapping, cache, out
+
+
+# ------------------------------------------------------------------ C0
+
+def test_c0_exact_workload():
+    """C0 as specified: one layer, QH 8 / KVH 2, 4096 context, budget 512,
+    popkv-normal (TG 32 / G 32), fp32 K/V/Q i.i.d. N(0,1), seed 0."""
+    w = workloads.C0
+    assert (w.q_heads, w.kv_heads, w.context, w.budget, w.token_group, w.dim_group, w.dtype, w.seed) == \
+        (8, 2, 4096, 512, 32, 32, torch.float32, 0)
+    _check_full_layer(w)
+
+
+# ------------------------------------------------------------------ C2
+
+def test_c2_popkv_q_sparse_layer_full_size():
+    """A C2 sparse layer at full size: PopKV-Q (TG 128 / G 16), 32K context,
+    budget 4096, bf16, seed 42 + 2 (layer 2, the first sparse layer)."""
+    w = workloads.c2_layer(2)
+    assert (w.token_group, w.dim_group, w.context, w.budget, w.seed) == (128, 16, 32768, 4096, 44)
+    _check_full_layer(w)
+
+
+def test_c2_stack_dense_and_sparse_layers_eager_and_graph():
+    """The C2 stack path bench.py captures (SparseDecodeStack): layers 0-1
+    dense over every token, layer 2 the PopKV-Q layer step, each against its
+    own oracle; then the same step recorded into a HIP graph and replayed
+    three times, with eager work and synchronizations between the replays,
+    every replay equal to the eager result."""
+    n_layers, dense = 3, (0, 1)
+    ops, caches, wants = [], {}, []
+    for li in range(n_layers):
+        w = workloads.c2_layer(li)
+        lay = workloads.make_layer(w).to(DEV)
+        mapping = workloads.head_to_kv(w, DEV)
+        ops.append((lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v()))
+        if li in dense:
+            L = lay.prefix_tokens
+            idx = np.tile(np.arange(L + 1, dtype=np.int64), (w.q_heads, 1))
+            wants.append(core.attention(f32(lay.queries), f32(lay.prefix_k()), f32(lay.prefix_v()),
+                                        f32(lay.current_k()), f32(lay.current_v()), idx, mapping.cpu().numpy()))
+        else:
+            caches[li] = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group,
+                                                 dim_group_size=w.dim_group, reserve_tokens=128)
+            wants.append(_oracle(w, lay, mapping, caches[li])[2])
+    w0 = workloads.c2_layer(0)
+    stack = popkv.SparseDecodeStack(caches, workloads.head_to_kv(w0, DEV), budget=w0.budget, full_layers=dense)
+    outs = [torch.empty_like(o[0]) for o in ops]
+    stack.step(ops, outs)
+    torch.cuda.synchronize()
+    for got, want in zip(outs, wants):
+        _assert_attention(got, want)
+    eager = [o.clone() for o in outs]
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        stack.step(ops, outs)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stack.step(ops, outs)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, eager)):
+            assert torch.equal(a, b), (rep, i)
+        stack.step(ops)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ C3
+
+@pytest.mark.parametrize("context", [4096, 8192, 16384])
+def test_c3_context_points(context):
+    """C3's short contexts at full size (PopKV-S, budget 4096, seed 7): at
+    4096 the budget covers every cached token (k = L, select-all)."""
+    w = workloads.c3(context)
+    assert w.seed == 7 and w.budget == 4096
+    if context == 4096:
+        assert w.k == w.prefix_tokens
+    _check_full_layer(w, check_prepack=context != 16384)
+
+
+# ------------------------------------------------------------------ chunk plans
+
+def _step_kpt(tokens: int, k: int) -> int:
+    """Keys per thread of the layer step's chunked select: the plan of
+    step_chunks() in csrc/select_common.h (chunks of 256 * kpt tokens holding
+    about 256 selected tokens each, at most 64 chunks)."""
+    kpts = (1, 2, 4, 6, 8, 12, 16, 24, 32)
+    want = tokens * 256 // k if k > 0 else tokens
+    want = max(want, (tokens + 63) // 64)
+    kpt = 1
+    for x in kpts:
+        if x * 256 <= want:
+            kpt = x
+    while kpt < 32 and -(-tokens // (kpt * 256)) > 64:
+        kpt = min(x for x in kpts if x > kpt)
+    return kpt
+
+
+@pytest.mark.parametrize("context,budget,kpt", [(3001, 2001, 1), (8192, 4096, 2), (16384, 4096, 4),
+                                                (28001, 4096, 6), (32768, 2501, 12), (32768, 1101, 24)])
+def test_layer_step_every_chunk_plan(context, budget, kpt):
+    """Each keys-per-thread instantiation of the chunk-histogram and the
+    fused select + attention kernels that the other tests leave out (8, 16
+    and 32 run at C1, 64K and 128K)."""
+    w = workloads.scaled(workloads.C1, context=context, budget=budget)
+    assert _step_kpt(w.prefix_tokens, w.k) == kpt
+    _check_full_layer(w, seed=300 + kpt, check_prepack=False, api_path=False)
+
+
+# ------------------------------------------------------------------ tie rule vs torch.topk
+
+def _tie_rows(kind: str, rows: int, tokens: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    if kind == "ties":
+        x = torch.randint(-3, 4, (rows, tokens), generator=g).float()
+    elif kind == "two_values":
+        x = torch.where(torch.rand(rows, tokens, generator=g) < 0.5, 1.0, 2.0)
+    elif kind == "signed_zero":
+        x = torch.where(torch.rand(rows, tokens, generator=g) < 0.5, -0.0, 0.0)
+    else:  # peaked scores with a NaN row and a row of few distinct values
+        x = torch.randn(rows, tokens, generator=g) * 0.5
+        x[:, ::97] += 4.0
+        x[3, ::37] = float("nan")
+        x[5] = torch.randint(0, 2, (tokens,), generator=g).float()
+    return x.to(torch.float16).to(DEV)
+
+
+@pytest.mark.parametrize("tokens", [32767, 131071])
+@pytest.mark.parametrize("kind", ["ties", "two_values", "signed_zero", "nan"])
+def test_tie_rule_matches_torch_topk_multi_block(kind, tokens):
+    """32 rows of 32767 and 131071 tokens: the shapes of the reference's
+    decode loop, where torch.topk takes its multi-block radix select.  The
+    selected sets equal PyTorch's for k = 1, 100, 4095 and 16383 (fewer NaNs
+    than k and more; ties cut inside one token chunk and across chunks)."""
+    s = _tie_rows(kind, 32, tokens, seed=tokens % 1000 + len(kind))
+    for k in (1, 100, 4095, 16383):
+        ours = topk.topk_indices(s, k).cpu().numpy()
+        ref = torch.topk(s, k, dim=-1, sorted=False).indices.cpu().numpy()
+        for r in range(s.shape[0]):
+            assert set(ours[r].tolist()) == set(ref[r].tolist()), (kind, tokens, k, r)
+        want = core.select(bits(s), k, tokens)
+        assert np.array_equal(topk.select_with_current(s, k, tokens + 1).cpu().numpy(), want)

@@ -155,6 +155,78 @@ def test_build_cache_validation():
         popkv.build_popkv_cache(keys, group_size=8, dim_group_size=8, reserve_tokens=1)
 
 
+def _step_operands(q_heads=8, kv_heads=2, tokens=40, cap=64, g=64):
+    q = torch.zeros(q_heads, 128, dtype=torch.bfloat16)
+    pk = torch.zeros(kv_heads, tokens, 128, dtype=torch.bfloat16)
+    k = torch.zeros(kv_heads, 128, dtype=torch.bfloat16)
+    packed = (torch.zeros(kv_heads, cap, 4, dtype=torch.int32), torch.zeros(kv_heads, cap, 4, dtype=torch.int32),
+              torch.zeros(kv_heads, cap, 128 // g, dtype=torch.float16),
+              torch.zeros(kv_heads, cap, 128 // g, dtype=torch.float16))
+    cache = popkv.PopKVCache(64, g, tokens, 0, packed, pk[:, :0])
+    mapping = torch.arange(q_heads) // (q_heads // kv_heads)
+    return q, pk, k, cache, mapping
+
+
+def test_layer_step_rejects_every_mismatched_operand_before_the_device():
+    """The C ABI gets raw pointers and head counts only, so each size it
+    derives addresses from is checked in Python first (ValueError), then
+    dtypes and devices (RuntimeError); CPU tensors reach the device check
+    only when every shape is right."""
+    q, pk, k, cache, h2k = _step_operands()
+    step = lambda **kw: popkv.popkv_layer_step(  # noqa: E731
+        kw.get("q", q), kw.get("cache", cache), kw.get("pk", pk), kw.get("pv", pk), kw.get("k", k), kw.get("v", k),
+        kw.get("h2k", h2k), budget=kw.get("budget", 16), out=kw.get("out"))
+    cases = [
+        (dict(q=q[:, :64]), "requires q"),
+        (dict(pv=pk[:, :10]), "prefix K/V must be"),
+        (dict(q=q[:7]), "positive multiple"),
+        (dict(k=k[:1]), "current k must be"),
+        (dict(v=torch.zeros(2, 64, dtype=torch.bfloat16)), "current v must be"),
+        (dict(out=torch.zeros(8, 64, dtype=torch.bfloat16)), "out must be"),
+        (dict(out=torch.zeros(128, 8, dtype=torch.bfloat16).t()), "out must be contiguous"),
+        (dict(h2k=h2k[:4]), "head_to_kv must be a vector of 8"),
+        (dict(h2k=h2k.float()), "int64 or int32"),
+        (dict(budget=1), "budget"),
+        (dict(pk=pk[:, :39], pv=pk[:, :39]), "token_count"),
+    ]
+    for kw, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            step(**kw)
+    q4, pk4, k4, cache4, h2k4 = _step_operands(q_heads=8, kv_heads=4)
+    with pytest.raises(ValueError, match="packed k_sign must be"):  # packed for 4 KV heads, prefix for 2
+        popkv.popkv_layer_step(q, cache4, pk, pk, k, k, h2k, budget=16)
+    bad = popkv.PopKVCache(64, 64, 40, 0, (cache.packed[0], cache.packed[1], cache.packed[2][:, :, :1],
+                                           cache.packed[3]), pk[:, :0])
+    with pytest.raises(ValueError, match="packed k_low must be"):
+        popkv.popkv_layer_step(q, bad, pk, pk, k, k, h2k, budget=16)
+    bad = popkv.PopKVCache(64, 64, 40, 0, (cache.packed[0].float(),) + cache.packed[1:], pk[:, :0])
+    with pytest.raises(ValueError, match="contiguous torch.int32"):
+        popkv.popkv_layer_step(q, bad, pk, pk, k, k, h2k, budget=16)
+    big = popkv.PopKVCache(64, 64, 65, 0, cache.packed, pk[:, :0])
+    pk65 = torch.zeros(2, 65, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="invalid score token count"):
+        popkv.popkv_layer_step(q, big, pk65, pk65, k, k, h2k, budget=16)
+    with pytest.raises(RuntimeError, match="share a dtype"):
+        step(k=k.float())
+    with pytest.raises(RuntimeError, match="same CUDA device"):
+        step()
+
+
+def test_dense_step_rejects_mismatched_operands_before_the_device():
+    q, pk, k, _, _ = _step_operands()
+    dense = lambda **kw: popkv.dense_attention_step(  # noqa: E731
+        kw.get("q", q), kw.get("pk", pk), kw.get("pv", pk), kw.get("k", k), kw.get("v", k), out=kw.get("out"))
+    for kw, msg in [(dict(k=k[:1]), "current k must be"), (dict(out=q[:4]), "out must be"),
+                    (dict(q=torch.zeros(6, 128, dtype=torch.bfloat16)), "1, 2, 4 or 8"),
+                    (dict(pv=pk[:1]), "prefix K/V must be")]:
+        with pytest.raises(ValueError, match=msg):
+            dense(**kw)
+    with pytest.raises(RuntimeError, match="share a dtype"):
+        dense(out=torch.zeros(8, 128))
+    with pytest.raises(RuntimeError, match="same CUDA device"):
+        dense()
+
+
 def test_static_cache_append_and_exhaustion():
     cache = popkv.StaticKVCache([torch.zeros(1, 2, 4, 8)], [torch.zeros(1, 2, 4, 8)], length=3, capacity=4)
     popkv.append_kv(cache, [torch.ones(1, 2, 1, 8)], [torch.full((1, 2, 1, 8), 2.0)])

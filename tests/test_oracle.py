@@ -458,3 +458,52 @@ def test_attention_merge_is_the_lse_identity():
     parts2 = np.concatenate([parts, np.zeros((qh, 1, d + 2), np.float32)], 1)
     parts2[:, -1, 0] = -np.inf
     np.testing.assert_allclose(core.attention_merge(parts2), got, atol=1e-6, rtol=1e-6)
+
+
+def test_torch_cpu_baseline_matches_readable_semantics():
+    """The torch-CPU baseline bench.py times restates the readable path:
+    its key / query encodes give the numpy restatement's bits and (within
+    float rounding) representatives, its dense-reconstruction scores the
+    numpy scores, and its step equals a float64 softmax over the rows its
+    own top-k picked plus the current token."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from oracle import readable, torch_cpu
+
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(2, 150, 128, generator=g)
+    v = torch.randn(2, 150, 128, generator=g)
+    q = torch.randn(8, 128, generator=g)
+    h2k = torch.arange(8) // 4
+    for tg, gg in ((32, 32), (64, 64), (128, 16), (7, 32)):
+        ks, km, kl, kd = torch_cpu.key_encode(k, tg, gg)
+        rs, rm = readable.key_magnitude(k.numpy(), tg)
+        assert np.array_equal(ks.numpy(), rs) and np.array_equal(km.numpy(), rm)
+        lo, de = readable.representatives(k.numpy(), rm, gg)
+        np.testing.assert_allclose(kl.numpy(), lo, atol=1e-6)
+        np.testing.assert_allclose(kd.numpy(), de, atol=1e-6)
+        qs, qm, ql, qd = torch_cpu.query_encode(q, gg)
+        want = readable.reference_query_encode(q.numpy(), gg)
+        assert np.array_equal(readable.pack_bits(qs.numpy()), want[0])
+        assert np.array_equal(readable.pack_bits(qm.numpy()), want[1])
+        np.testing.assert_allclose(ql.numpy(), want[2], atol=1e-6)
+        want_s = readable.reference_scores(q[None].numpy(), k.numpy(), head_to_kv=h2k.numpy(), group_size=tg,
+                                           dim_group_size=gg)[0]
+        qhat = torch_cpu.reconstruct(qs, qm, ql, qd, gg)
+        khat = torch_cpu.reconstruct(ks, km, kl, kd, gg)
+        got_s = torch.einsum("hd,htd->ht", qhat, khat[h2k]) / math.sqrt(128)
+        np.testing.assert_allclose(got_s.numpy(), want_s, atol=1e-5)
+    layer = torch_cpu.CpuRetrievalLayer(k[:, :-1], v[:, :-1], h2k, token_group=64, dim_group=64)
+    out = layer.step(q, k[:, -1], v[:, -1], budget=40)
+    assert out.shape == (8, 128)
+    qhat = torch_cpu.reconstruct(*torch_cpu.query_encode(q, 64), 64)
+    sc = (torch.einsum("hd,htd->ht", qhat, layer.khat[h2k]) / math.sqrt(128)).half()
+    idx = torch.topk(sc, 39, dim=-1, sorted=False).indices
+    for h in range(8):
+        rows_k = torch.cat([k[h2k[h], idx[h]], k[h2k[h], -1:]]).double()
+        rows_v = torch.cat([v[h2k[h], idx[h]], v[h2k[h], -1:]]).double()
+        p = torch.softmax(rows_k @ q[h].double() / math.sqrt(128), 0)
+        np.testing.assert_allclose(out[h].numpy(), (p @ rows_v).numpy(), atol=1e-5)
