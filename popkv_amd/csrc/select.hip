@@ -614,7 +614,7 @@ hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_
     if (tokens < kTopkChunkMinTokens) {
         const hipError_t e = launch_topk_list(keys, ghist, rows, key_stride, tokens, k, out32, index_row_stride,
                                               true, out64, index_row_stride, current, stream);
-        if (e != hipSuccess) launch_fill_u32(ghist, rows * kBins, 0u, stream);
+        if (e != hipSuccess) (void)launch_fill_u32(ghist, rows * kBins, 0u, stream);
         return e;
     }
     uint32_t* rec = reinterpret_cast<uint32_t*>(base + w.rec);
@@ -623,7 +623,7 @@ hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_
     // chunk_hist_kernel runs for 0 < k < tokens only, on step_chunks(tokens, k)
     hipError_t e = launch_chunk_hist(keys, key_stride, rows, tokens, k, ghist, rec, h2, gt1, stream);
     if (e != hipSuccess) {
-        launch_fill_u32(ghist, rows * kBins, 0u, stream);  // the histograms stay zero between calls
+        (void)launch_fill_u32(ghist, rows * kBins, 0u, stream);  // the histograms stay zero between calls
         return e;
     }
     const StepChunks ch = step_chunks(tokens, k > 0 && k < tokens ? k : tokens);
