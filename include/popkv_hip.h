@@ -181,6 +181,32 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* output, int64_t* indices_out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free form of popkv_layer_step: the same kernels and results,
+ * with the workspace taken from a library-owned device array of
+ * POPKV_LAYER_STEP_SCRATCH_BYTES per GPU (a file-scope __device__ array,
+ * held until the process ends) instead of a caller argument.  It calls no
+ * hipMalloc/hipFree and no allocating library routine; the caller passes
+ * inputs and outputs only.  Each call first clears the array's histogram
+ * region with a fill kernel (no hipMemsetAsync, so it records into HIP
+ * graphs).  A step whose workspace (popkv_layer_step_workspace_bytes) would
+ * exceed the array fails with POPKV_ERR_WORKSPACE.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams
+ * without ordering, or several host threads) race and must be serialized
+ * by the caller.  No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation). */
+#define POPKV_LAYER_STEP_SCRATCH_BYTES (16u << 20)
+size_t popkv_layer_step_scratch_bytes(void);
+int popkv_layer_step_noalloc(const void* queries, int32_t dtype,
+                             const int32_t* k_sign, const int32_t* k_mag,
+                             const void* k_low, const void* k_delta, int64_t capacity,
+                             const void* prefix_k, const void* prefix_v,
+                             int64_t k_head_stride, int64_t v_head_stride,
+                             const void* current_k, const void* current_v,
+                             const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
+                             int64_t tokens, int64_t budget, int32_t dim_group_size,
+                             void* output, int64_t* indices_out, void* stream);
+
 /* Re-runs only the fused select + sparse-attention kernel of the last
  * popkv_layer_step that used `workspace` (same shapes and budget): it reads
  * the order keys and threshold histograms the step left there and rewrites

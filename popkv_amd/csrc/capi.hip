@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "kernels.h"
 #include "popkv_hip.h"
@@ -70,6 +71,35 @@ StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     L.partials = off; off = align_up(off + static_cast<size_t>(qh) * nc * (128 + 2) * 4);
     L.total = off;
     return L;
+}
+
+// The allocation-free layer step's workspace: one array per GPU, held until
+// the process ends.  In host code `scratch` names a host-side stand-in, not
+// the device address, so it is never passed to a kernel or a copy; its
+// address on each device comes from hipGetSymbolAddress (device_scratch).
+static __device__ __align__(256) unsigned char scratch[POPKV_LAYER_STEP_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device
+// (with that device current) and kept.
+int device_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(POPKV_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(POPKV_ERR_UNSUPPORTED, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(POPKV_ERR_LAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return POPKV_OK;
 }
 
 }  // namespace
@@ -294,12 +324,17 @@ size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t
     return step_layout(q_heads, tokens, budget).total;
 }
 
-int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
-                     const void* k_low, const void* k_delta, int64_t capacity, const void* prefix_k,
-                     const void* prefix_v, int64_t k_head_stride, int64_t v_head_stride, const void* current_k,
-                     const void* current_v, const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
-                     int64_t tokens, int64_t budget, int32_t dim_group_size, void* output, int64_t* indices_out,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// The layer step on a given workspace.  clear_first: the histogram region is
+// set to zero by a fill kernel before the scorer adds into it (for a
+// workspace whose contents are not known to be zero).
+static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                          const void* k_low, const void* k_delta, int64_t capacity, const void* prefix_k,
+                          const void* prefix_v, int64_t k_head_stride, int64_t v_head_stride, const void* current_k,
+                          const void* current_v, const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
+                          int64_t tokens, int64_t budget, int32_t dim_group_size, void* output, int64_t* indices_out,
+                          void* workspace, size_t workspace_bytes, bool clear_first, void* stream) {
     if (!queries || !k_sign || !k_mag || !k_low || !k_delta || !prefix_k || !prefix_v || !current_k || !current_v ||
         !head_to_kv || !output)
         return fail(POPKV_ERR_INVALID, "null pointer");
@@ -325,6 +360,10 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
     hipStream_t s = as_stream(stream);
+    if (clear_first) {
+        st = launched(popkv::launch_fill_u32(hist, q_heads * 256, 0u, s), "popkv_layer_step(clear histograms)");
+        if (st) return st;
+    }
 
     // 1. query encode + popcount score -> radix order keys of the fp16 scores
     //    (rows padded to a multiple of 128 tokens, so every row starts
@@ -338,7 +377,7 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
     // From here on the scorer has added into the histogram region, which
     // must be zero when the next call begins: a failed launch clears it.
     auto clear_hist = [&](int status) {
-        popkv::launch_fill_u32(hist, q_heads * 256, 0u, s);
+        (void)popkv::launch_fill_u32(hist, q_heads * 256, 0u, s);
         return status;
     };
     // 2. per-chunk low-byte histograms of the threshold's high-byte bin
@@ -363,6 +402,44 @@ int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, 
                   "popkv_layer_step(merge)");
     if (st) return st;
     return POPKV_OK;
+}
+
+extern "C" {
+
+int popkv_layer_step(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                     const void* k_low, const void* k_delta, int64_t capacity, const void* prefix_k,
+                     const void* prefix_v, int64_t k_head_stride, int64_t v_head_stride, const void* current_k,
+                     const void* current_v, const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
+                     int64_t tokens, int64_t budget, int32_t dim_group_size, void* output, int64_t* indices_out,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+    return layer_step_run(queries, dtype, k_sign, k_mag, k_low, k_delta, capacity, prefix_k, prefix_v, k_head_stride,
+                          v_head_stride, current_k, current_v, head_to_kv, q_heads, kv_heads, tokens, budget,
+                          dim_group_size, output, indices_out, workspace, workspace_bytes, false, stream);
+}
+
+size_t popkv_layer_step_scratch_bytes(void) { return POPKV_LAYER_STEP_SCRATCH_BYTES; }
+
+int popkv_layer_step_noalloc(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                             const void* k_low, const void* k_delta, int64_t capacity, const void* prefix_k,
+                             const void* prefix_v, int64_t k_head_stride, int64_t v_head_stride,
+                             const void* current_k, const void* current_v, const int64_t* head_to_kv,
+                             int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget,
+                             int32_t dim_group_size, void* output, int64_t* indices_out, void* stream) {
+    if (q_heads > 0 && tokens >= 0 && budget > 1) {
+        const size_t need = step_layout(q_heads, tokens, budget).total;
+        if (need > POPKV_LAYER_STEP_SCRATCH_BYTES)
+            return fail(POPKV_ERR_WORKSPACE,
+                        "popkv_layer_step_noalloc: this step needs %zu bytes of scratch, more than the "
+                        "library's %zu-byte array; call popkv_layer_step with a workspace instead",
+                        need, static_cast<size_t>(POPKV_LAYER_STEP_SCRATCH_BYTES));
+    }
+    void* scratch_ptr = nullptr;
+    const int st = device_scratch(&scratch_ptr);
+    if (st) return st;
+    return layer_step_run(queries, dtype, k_sign, k_mag, k_low, k_delta, capacity, prefix_k, prefix_v, k_head_stride,
+                          v_head_stride, current_k, current_v, head_to_kv, q_heads, kv_heads, tokens, budget,
+                          dim_group_size, output, indices_out, scratch_ptr, POPKV_LAYER_STEP_SCRATCH_BYTES, true,
+                          stream);
 }
 
 int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
