@@ -181,6 +181,69 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* output, int64_t* indices_out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Batched decode step of one sparse layer over B independent sequences of
+ * different lengths, head_dim 128, in one call (the same four kernels as
+ * popkv_layer_step, every row at its own sequence's shape).  Layouts, all
+ * contiguous:
+ *   queries, output        [B, QH, 128]       (dtype)
+ *   k_sign/k_mag           [B, KVH, capacity, 4]    int32
+ *   k_low/k_delta          [B, KVH, capacity, 128/G] fp16
+ *   key_cache/value_cache  [B, KVH, cache_rows, 128] (dtype; the static
+ *                          K/V caches, read in place)
+ *   current_k/current_v    [B, KVH, 128]      (dtype)
+ *   head_to_kv             [QH] int64: one sequence's GQA mapping
+ *   token_counts           [B] int64 IN DEVICE MEMORY: sequence b has
+ *                          token_counts[b] cached tokens (rows 0 .. count-1
+ *                          of its caches); the current token is index count.
+ * max_tokens (host) bounds every count (1 <= max_tokens <= capacity,
+ * cache_rows, 131072) and sizes the launch; a count above it is treated as
+ * max_tokens.  Sequence b selects k_b = min(budget - 1, count_b) tokens;
+ * indices_out (optional) [B, QH, index_row_stride] int64 receives them in
+ * ascending order with the current token at slot k_b (entries past k_b are
+ * left untouched).  Workspace: popkv_layer_step_batched_workspace_bytes()
+ * bytes, 16-byte aligned, first B*QH*1024 bytes zero on entry (left zero),
+ * as for popkv_layer_step.  Because the counts are read on the device, one
+ * HIP graph of a decode step stays valid while the sequences grow.
+ * Replaces the PopKV branch of LlamaSparseDecoder.decode (reference
+ * popkv.py:1076-1115) for a batch: the reference's packed caches have no
+ * batch dimension (popkv_ext.cu:769-806; popkv.py:763-1129 decodes one
+ * sequence). */
+size_t popkv_layer_step_batched_workspace_bytes(int64_t batch, int64_t q_heads, int64_t max_tokens,
+                                                int64_t budget, int32_t dim_group_size);
+int popkv_layer_step_batched(const void* queries, int32_t dtype,
+                             const int32_t* k_sign, const int32_t* k_mag,
+                             const void* k_low, const void* k_delta, int64_t capacity,
+                             const void* key_cache, const void* value_cache, int64_t cache_rows,
+                             const void* current_k, const void* current_v,
+                             const int64_t* head_to_kv, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                             const int64_t* token_counts, int64_t max_tokens, int64_t budget,
+                             int32_t dim_group_size, void* output, int64_t* indices_out,
+                             int64_t index_row_stride, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* Fused per-token append, head_dim 128, one call per layer for a batch of
+ * B sequences (B = 1 for a single one): writes the new token's K/V rows
+ * new_k/new_v [B, KVH, 128] to row token_counts[b] of the static caches
+ * key_cache/value_cache [B, KVH, cache_rows, 128], and re-encodes each
+ * sequence's active token group -- rows s .. token_counts[b], s =
+ * token_counts[b] rounded down to a multiple of token_group_size, the older
+ * ones read in place from key_cache -- into the packed planes
+ * [B, KVH, capacity, .] (a group seals when it reaches token_group_size
+ * tokens: the next append starts a new one).  token_counts (device int64
+ * [B]) is read, not advanced: the caller adds 1 after every layer of the
+ * step has appended.  A count outside [0, min(cache_rows, capacity))
+ * writes nothing for that sequence and sets *status = 1 (device int32,
+ * may be NULL) -- the reference's "Pop-KV cache reserve exhausted".
+ * Replaces append_popkv / append_retrieval_caches (reference popkv.py:
+ * 438-459, :883-942: torch.cat staging of the active keys, then
+ * pack_keys_into, popkv_cuda.py:72-87, popkv_ext.cu:1075-1092) together
+ * with the static cache row write of popkv.py:964-972. */
+int popkv_append(const void* new_k, const void* new_v, int32_t dtype,
+                 void* key_cache, void* value_cache, int64_t cache_rows,
+                 int32_t* k_sign, int32_t* k_mag, void* k_low, void* k_delta, int64_t capacity,
+                 const int64_t* token_counts, int64_t batch, int64_t kv_heads,
+                 int32_t token_group_size, int32_t dim_group_size, int32_t* status, void* stream);
+
 /* Allocation-free form of popkv_layer_step: the same kernels and results,
  * with the workspace taken from a library-owned device array of
  * POPKV_LAYER_STEP_SCRATCH_BYTES per GPU (a file-scope __device__ array,

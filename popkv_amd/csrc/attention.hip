@@ -465,13 +465,13 @@ __device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk
 // Block 0 of each head re-zeroes the scorer's histogram ghist[h] (its last
 // reader, chunk_hist_kernel, has finished).  The grid is one-dimensional
 // (chunk_head_of_block).
-template <typename T, int KPT, int NB>
+template <typename T, int KPT, int NB, bool SEQ>
 __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
     const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
     uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
-    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride) {
+    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
     constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
     constexpr int CH = kChunkThreads * KPT;
@@ -484,7 +484,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const int wave = tid / kWave;
     const int slot = wave * SLOTS + lane / LPR;
     const int dim0 = (lane % LPR) * 8;
-    const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);  // none / every token / threshold
+    // SEQ (a batched step): row h is query head hl of sequence b, whose own
+    // token count and k arrive with the first loads; every load below is
+    // addressed within the launch's bounds (ntok tokens, nchunks chunks) and
+    // masked to the row's own shape afterwards.
+    int64_t b = 0;
+    int hl = h;
+    if constexpr (SEQ) {
+        b = h / seq.q_heads;
+        hl = h - static_cast<int>(b) * seq.q_heads;
+    }
 
     // 0. loads, all issued before any is used: this thread's keys, the query
     //    slice, the head's KV mapping, the threshold record and the chunk
@@ -495,19 +504,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     int z = 0;
     asm volatile("" : "+v"(z));
     const int begin = c * CH + tid * KPT;
-    const int n = max(0, min(KPT, ntok - begin));
     ChunkKeys<KPT> kk;
-    load_chunk_keys<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, n, kk);
+    load_chunk_keys_raw<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, max(0, min(KPT, ntok - begin)), kk);
     Raw8<T> qr;
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
-    const int64_t map = head_to_kv[h + z];
+    const int64_t map = head_to_kv[hl + z];
+    int nch = nchunks;  // this row's chunks
+    if constexpr (SEQ) {
+        ntok = static_cast<int>(seq_tokens_of(seq, b, ntok));
+        k = min(seq.budget - 1, ntok);
+        nch = (ntok + CH - 1) / CH;
+    }
+    const int n = max(0, min(KPT, ntok - begin));
+    mask_chunk_keys<KPT>(n, kk);
+    const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);  // none / every token / threshold
     __shared__ uint32_t s_g2[256], s_p2[256];
     __shared__ uint32_t s_scan1[kAttnWaves], s_scan2[kAttnWaves];
     __shared__ __align__(16) uint16_t s_list[CH];
     uint32_t b1 = 0, above1 = 0, rank0 = 0;
     uint32_t g2 = 0, p2 = 0;  // bin tid of the chunk histograms over every chunk / over chunks before c
     uint32_t gt1_before = 0;  // keys above bin b1 in earlier chunks
-    if (mode == 2) {
+    if (SEQ || mode == 2) {
         b1 = rec[4 * h + z];
         above1 = rec[4 * h + 1 + z];
         const uint16_t* hr = h2 + static_cast<int64_t>(h) * nchunks * 256 + tid;
@@ -517,7 +534,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
             for (int j = 0; j < 16; ++j) v[j] = hr[static_cast<int64_t>(min(c0 + j, nchunks - 1)) * 256];
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const uint32_t x = c0 + j < nchunks ? v[j] : 0u;
+                const uint32_t x = c0 + j < nch ? v[j] : 0u;
                 g2 += x;
                 p2 += c0 + j < c ? x : 0u;
             }
@@ -527,6 +544,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
                 const uint32_t x = c0 + lane < c ? gt1[static_cast<int64_t>(h) * nchunks + c0 + lane] : 0u;
                 gt1_before += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
             }
+        }
+    }
+    if constexpr (SEQ) {
+        if (c >= nch) {  // past this sequence's tokens: an empty state (the merge weighs it 0)
+            if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
+            float* dst = partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2);
+            if (tid < D + 2) dst[tid] = tid == 0 ? -INFINITY : 0.0f;
+            return;
         }
     }
 
@@ -564,8 +589,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
 
     // 2. the first gather pass, issued now
     const int64_t kvh = min(max(map, static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
-    const char* kb = reinterpret_cast<const char*>(kc + kvh * k_hs) + dim0 * sizeof(T);
-    const char* vb = reinterpret_cast<const char*>(vc + kvh * v_hs) + dim0 * sizeof(T);
+    const char* kb = reinterpret_cast<const char*>(kc + b * seq.k_bstride + kvh * k_hs) + dim0 * sizeof(T);
+    const char* vb = reinterpret_cast<const char*>(vc + b * seq.v_bstride + kvh * v_hs) + dim0 * sizeof(T);
     const uint32_t t0 = static_cast<uint32_t>(c * CH);
     const uint32_t tmax = static_cast<uint32_t>(ntok - 1);  // a selected token is < ntok; clamped all the same
     Raw8<T> kr[NB], vr[NB];
@@ -908,20 +933,38 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_mfma_kernel(
 // ascending order.
 constexpr int kMergeFirst = 16;
 
+// Row of current_k / current_v for merge block h, and (for a batched step)
+// the row's current-token index and its slot k in the indices: sequence b =
+// h / q_heads has min(tokens[b], bound) cached tokens (*current holds the
+// launch bound on entry).  Unbatched: KV head head_to_kv[h] (clamped), or
+// h / (QH / KVH) without a mapping (the dense layers).
+__device__ __forceinline__ int64_t merge_kv_row(const SeqTable& seq, const int64_t* __restrict__ head_to_kv, int h,
+                                                int kv_heads, int64_t* idx_slot, int64_t* current) {
+    if (seq.tokens != nullptr) {
+        const int64_t b = h / seq.q_heads;
+        *current = seq_tokens_of(seq, b, *current);
+        *idx_slot = min(static_cast<int64_t>(seq.budget) - 1, *current);
+        return b * seq.kv_heads +
+               min(max(head_to_kv[h - b * seq.q_heads], static_cast<int64_t>(0)), static_cast<int64_t>(seq.kv_heads - 1));
+    }
+    return head_to_kv != nullptr ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
+                                 : h / (static_cast<int>(gridDim.x) / kv_heads);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
     const T* __restrict__ cur_v, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
-    T* __restrict__ out, int64_t* __restrict__ idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current) {
+    T* __restrict__ out, int64_t* __restrict__ idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current,
+    SeqTable seq) {
     constexpr int D = 128, S = D + 2;
     const int h = blockIdx.x;
     const int lane = threadIdx.x;
-    // the current token's index slot of the layer step's int64 indices
+    // the current token's index slot of the layer step's int64 indices, and
+    // the KV row of its current k/v (no mapping: the plain GQA grouping of
+    // the dense layers)
+    const int64_t kvh = merge_kv_row(seq, head_to_kv, h, kv_heads, &idx_slot, &current);
     if (idx_out != nullptr && lane == 0) idx_out[static_cast<int64_t>(h) * idx_stride + idx_slot] = current;
-    // no mapping: the plain GQA grouping of the dense layers
-    const int64_t kvh = head_to_kv != nullptr
-                            ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
-                            : h / (static_cast<int>(gridDim.x) / kv_heads);
     const float* ps = partials + static_cast<int64_t>(h) * nsplit * S;
     const T* qh = q + static_cast<int64_t>(h) * D;
     const T* ck = cur_k + kvh * D;
@@ -1008,15 +1051,14 @@ template <typename T>
 __global__ __launch_bounds__(kWave * kMergeWaves) void attn_merge_wide_kernel(
     const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
     const T* __restrict__ cur_v, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
-    T* __restrict__ out, int64_t* __restrict__ idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current) {
+    T* __restrict__ out, int64_t* __restrict__ idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current,
+    SeqTable seq) {
     constexpr int D = 128, S = D + 2;
     const int h = blockIdx.x;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
+    const int64_t kvh = merge_kv_row(seq, head_to_kv, h, kv_heads, &idx_slot, &current);
     if (idx_out != nullptr && threadIdx.x == 0) idx_out[static_cast<int64_t>(h) * idx_stride + idx_slot] = current;
-    const int64_t kvh = head_to_kv != nullptr
-                            ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
-                            : h / (static_cast<int>(gridDim.x) / kv_heads);
     const float* ps = partials + static_cast<int64_t>(h) * nsplit * S;
     float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
     if (wave == 0) {  // the current token's operands, in flight during the splits
@@ -1316,7 +1358,7 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
                                   const uint16_t* keys, int64_t key_stride, int64_t tokens, int64_t k,
                                   const uint32_t* rec, const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                   const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
-                                  int64_t idx_stride, hipStream_t stream) {
+                                  int64_t idx_stride, const SeqTable& seq, hipStream_t stream) {
     // 10 rows per slot and pass: 160 per pass, so a chunk holding up to 320
     // selected tokens (C1: 204-294 in chunks of 2048) is gathered in two
     // passes.  Measured at C1, select + attention: 8 rows 16.5 us (three
@@ -1325,15 +1367,26 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
     const StepChunks ch = step_chunks(tokens, k);
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
-    const bool groups = kv_heads % 8 == 0 && q_heads % kv_heads == 0;
-    const int qpk = groups ? q_heads / kv_heads : 1;
+    // q_heads: rows of the step (a batched step: B * QH); the placement
+    // groups rows by GQA group (a batched step's groups are b * KVH + j)
+    const bool batched = seq.tokens != nullptr;
+    const int qpk_all = batched ? seq.q_heads / seq.kv_heads : (kv_heads > 0 ? q_heads / kv_heads : 1);
+    const int kv_all = batched ? q_heads / qpk_all : kv_heads;
+    const bool groups = kv_all % 8 == 0 && (batched || q_heads % kv_heads == 0);
+    const int qpk = groups ? qpk_all : 1;
+    const int kv_clamp = batched ? seq.kv_heads : kv_heads;
     const dim3 grid(static_cast<unsigned>(ch.count * q_heads));
     const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
-#define POPKV_SC(KPT)                                                                                           \
-    case KPT:                                                                                                   \
-        hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB>), grid, dim3(kAttnThreads), 0, stream, q_, k_, \
-                           v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups, ghist, h2k, \
-                           kv_heads, scale, partials, idx_out, idx_stride);                                     \
+#define POPKV_SC(KPT)                                                                                            \
+    case KPT:                                                                                                    \
+        if (batched)                                                                                             \
+            hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, true>), grid, dim3(kAttnThreads), 0, stream, \
+                               q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
+                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq);                  \
+        else                                                                                                     \
+            hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, false>), grid, dim3(kAttnThreads), 0, stream, \
+                               q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
+                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq);                  \
         break
     switch (ch.kpt) {
         POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
@@ -1347,18 +1400,18 @@ template <typename T>
 hipError_t launch_merge_current_t(const float* partials, int nsplit, const void* q, const void* cur_k,
                                   const void* cur_v, const int64_t* h2k, int q_heads, int kv_heads, void* out,
                                   int64_t* idx_out, int64_t idx_stride, int64_t idx_slot, int64_t current,
-                                  hipStream_t stream) {
+                                  const SeqTable& seq, hipStream_t stream) {
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     if (nsplit > kMergeFirst)
         hipLaunchKernelGGL((attn_merge_wide_kernel<T>), dim3(static_cast<unsigned>(q_heads)),
                            dim3(kWave * kMergeWaves), 0, stream, partials, nsplit, static_cast<const T*>(q),
                            static_cast<const T*>(cur_k), static_cast<const T*>(cur_v), h2k, kv_heads, scale,
-                           static_cast<T*>(out), idx_out, idx_stride, idx_slot, current);
+                           static_cast<T*>(out), idx_out, idx_stride, idx_slot, current, seq);
     else
         hipLaunchKernelGGL((attn_merge_current_kernel<T>), dim3(static_cast<unsigned>(q_heads)), dim3(kWave), 0,
                            stream, partials, nsplit, static_cast<const T*>(q), static_cast<const T*>(cur_k),
                            static_cast<const T*>(cur_v), h2k, kv_heads, scale, static_cast<T*>(out), idx_out,
-                           idx_stride, idx_slot, current);
+                           idx_stride, idx_slot, current, seq);
     return hipGetLastError();
 }
 }  // namespace
@@ -1368,39 +1421,42 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           int64_t key_stride, int64_t tokens, int64_t k, const uint32_t* rec,
                                           const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                          int64_t* idx_out, int64_t idx_stride, hipStream_t stream) {
+                                          int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
+                                          hipStream_t stream) {
     if (tokens <= 0 || q_heads <= 0) return hipSuccess;
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_select_chunks_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
-                                                 kv_heads, partials, idx_out, idx_stride, stream);
+                                                 kv_heads, partials, idx_out, idx_stride, seq, stream);
         case POPKV_DTYPE_F16:
             return launch_select_chunks_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
-                                                 kv_heads, partials, idx_out, idx_stride, stream);
+                                                 kv_heads, partials, idx_out, idx_stride, seq, stream);
         default:
             return launch_select_chunks_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                   key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
-                                                  kv_heads, partials, idx_out, idx_stride, stream);
+                                                  kv_heads, partials, idx_out, idx_stride, seq, stream);
     }
 }
 
 hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,
                                 const void* current_k, const void* current_v, const int64_t* head_to_kv, int q_heads,
                                 int kv_heads, void* output, int64_t* idx_out, int64_t idx_stride, int64_t idx_slot,
-                                int64_t current, hipStream_t stream) {
+                                int64_t current, const SeqTable& seq, hipStream_t stream) {
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_merge_current_t<float>(partials, nsplit, queries, current_k, current_v, head_to_kv, q_heads,
-                                                 kv_heads, output, idx_out, idx_stride, idx_slot, current, stream);
+                                                 kv_heads, output, idx_out, idx_stride, idx_slot, current, seq,
+                                                 stream);
         case POPKV_DTYPE_F16:
             return launch_merge_current_t<f16_t>(partials, nsplit, queries, current_k, current_v, head_to_kv, q_heads,
-                                                 kv_heads, output, idx_out, idx_stride, idx_slot, current, stream);
+                                                 kv_heads, output, idx_out, idx_stride, idx_slot, current, seq,
+                                                 stream);
         default:
             return launch_merge_current_t<bf16_t>(partials, nsplit, queries, current_k, current_v, head_to_kv,
                                                   q_heads, kv_heads, output, idx_out, idx_stride, idx_slot, current,
-                                                  stream);
+                                                  seq, stream);
     }
 }
 

@@ -371,7 +371,7 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
                                                static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
                                                static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
-                                               tokens, dim_group_size, keys, L.score_stride, hist, s),
+                                               tokens, dim_group_size, keys, L.score_stride, hist, popkv::SeqTable{}, s),
                   "popkv_layer_step(score)");
     if (st) return st;
     // From here on the scorer has added into the histogram region, which
@@ -381,7 +381,8 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
         return status;
     };
     // 2. per-chunk low-byte histograms of the threshold's high-byte bin
-    st = launched(popkv::launch_chunk_hist(keys, L.score_stride, q_heads, tokens, L.k, hist, rec, h2, gt1, s),
+    st = launched(popkv::launch_chunk_hist(keys, L.score_stride, q_heads, tokens, L.k, hist, rec, h2, gt1,
+                                           popkv::SeqTable{}, s),
                   "popkv_layer_step(chunk histograms)");
     if (st) return clear_hist(st);
     // 3. per (chunk, head): the chunk's selected tokens (also written as
@@ -392,13 +393,14 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     st = launched(popkv::launch_attention_select_chunks(queries, dtype, prefix_k, prefix_v, k_head_stride,
                                                         v_head_stride, keys, L.score_stride, tokens, L.k, rec, h2,
                                                         gt1, hist, head_to_kv, static_cast<int>(q_heads),
-                                                        static_cast<int>(kv_heads), partials, indices_out, L.k + 1, s),
+                                                        static_cast<int>(kv_heads), partials, indices_out, L.k + 1,
+                                                        popkv::SeqTable{}, s),
                   "popkv_layer_step(select + attention)");
     if (st) return clear_hist(st);
     st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nchunks), queries, dtype, current_k,
                                               current_v, head_to_kv, static_cast<int>(q_heads),
                                               static_cast<int>(kv_heads), output, indices_out, L.k + 1, L.k, tokens,
-                                              s),
+                                              popkv::SeqTable{}, s),
                   "popkv_layer_step(merge)");
     if (st) return st;
     return POPKV_OK;
@@ -442,6 +444,110 @@ int popkv_layer_step_noalloc(const void* queries, int32_t dtype, const int32_t* 
                           stream);
 }
 
+size_t popkv_layer_step_batched_workspace_bytes(int64_t batch, int64_t q_heads, int64_t max_tokens, int64_t budget,
+                                                int32_t dim_group_size) {
+    if (batch <= 0 || q_heads <= 0 || max_tokens < 0 || budget <= 1 || !valid_group(dim_group_size)) return 0;
+    return step_layout(batch * q_heads, max_tokens, budget).total;
+}
+
+int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                             const void* k_low, const void* k_delta, int64_t capacity, const void* key_cache,
+                             const void* value_cache, int64_t cache_rows, const void* current_k,
+                             const void* current_v, const int64_t* head_to_kv, int64_t batch, int64_t q_heads,
+                             int64_t kv_heads, const int64_t* token_counts, int64_t max_tokens, int64_t budget,
+                             int32_t dim_group_size, void* output, int64_t* indices_out, int64_t index_row_stride,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    if (!queries || !k_sign || !k_mag || !k_low || !k_delta || !key_cache || !value_cache || !current_k ||
+        !current_v || !head_to_kv || !token_counts || !output)
+        return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "tensors must be fp32/fp16/bf16");
+    if (budget <= 1) return fail(POPKV_ERR_INVALID, "budget must reserve at least one retrieved and one current token");
+    if (batch <= 0) return fail(POPKV_ERR_INVALID, "empty batch");
+    int st = check_score_common(head_to_kv, batch, q_heads, kv_heads, capacity, max_tokens, dim_group_size);
+    if (st) return st;
+    if (max_tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens");
+    if (max_tokens > cache_rows) return fail(POPKV_ERR_CAPACITY, "max_tokens exceeds the static cache rows");
+    const int64_t kmax = budget - 1 < max_tokens ? budget - 1 : max_tokens;
+    if (indices_out && index_row_stride < kmax + 1) return fail(POPKV_ERR_INVALID, "index row stride too small");
+    const int64_t rows = batch * q_heads;
+    const StepLayout L = step_layout(rows, max_tokens, budget);
+    if (!workspace || workspace_bytes < L.total)
+        return fail(POPKV_ERR_WORKSPACE, "batched layer step needs %zu workspace bytes", L.total);
+    if (!aligned16(workspace)) return fail(POPKV_ERR_INVALID, "workspace must be 16-byte aligned");
+    const size_t es = elem_size(dtype);
+    if (!aligned16(k_sign) || !aligned16(k_mag) || !aligned16(k_low) || !aligned16(k_delta) || !aligned16(queries) ||
+        !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(current_k) || !aligned16(current_v) ||
+        (cache_rows * 128 * static_cast<int64_t>(es)) % 16)
+        return fail(POPKV_ERR_UNSUPPORTED, "batched layer step tensors need 16-byte alignment");
+    popkv::SeqTable seq;
+    seq.tokens = token_counts;
+    seq.cache_rows = kv_heads * capacity;
+    seq.k_bstride = seq.v_bstride = kv_heads * cache_rows * 128;
+    seq.q_heads = static_cast<int>(q_heads);
+    seq.kv_heads = static_cast<int>(kv_heads);
+    seq.budget = static_cast<int>(budget < 0x7fffffff ? budget : 0x7fffffff);
+    char* ws = static_cast<char*>(workspace);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+    uint32_t* rec = reinterpret_cast<uint32_t*>(ws + L.rec);
+    uint16_t* h2 = reinterpret_cast<uint16_t*>(ws + L.h2);
+    uint32_t* gt1 = reinterpret_cast<uint32_t*>(ws + L.gt1);
+    uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
+    float* partials = reinterpret_cast<float*>(ws + L.partials);
+    hipStream_t s = as_stream(stream);
+    // the same four kernels as popkv_layer_step, every row at its own
+    // sequence's token count (see popkv::SeqTable)
+    st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
+                                               static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
+                                               static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
+                                               max_tokens, dim_group_size, keys, L.score_stride, hist, seq, s),
+                  "popkv_layer_step_batched(score)");
+    if (st) return st;
+    auto clear_hist = [&](int status) {
+        (void)popkv::launch_fill_u32(hist, rows * 256, 0u, s);
+        return status;
+    };
+    st = launched(popkv::launch_chunk_hist(keys, L.score_stride, rows, max_tokens, L.k, hist, rec, h2, gt1, seq, s),
+                  "popkv_layer_step_batched(chunk histograms)");
+    if (st) return clear_hist(st);
+    st = launched(popkv::launch_attention_select_chunks(queries, dtype, key_cache, value_cache, cache_rows * 128,
+                                                        cache_rows * 128, keys, L.score_stride, max_tokens, L.k, rec,
+                                                        h2, gt1, hist, head_to_kv, static_cast<int>(rows),
+                                                        static_cast<int>(kv_heads), partials, indices_out,
+                                                        index_row_stride, seq, s),
+                  "popkv_layer_step_batched(select + attention)");
+    if (st) return clear_hist(st);
+    return launched(popkv::launch_merge_current(partials, static_cast<int>(L.nchunks), queries, dtype, current_k,
+                                                current_v, head_to_kv, static_cast<int>(rows),
+                                                static_cast<int>(kv_heads), output, indices_out, index_row_stride,
+                                                L.k, max_tokens, seq, s),
+                    "popkv_layer_step_batched(merge)");
+}
+
+int popkv_append(const void* new_k, const void* new_v, int32_t dtype, void* key_cache, void* value_cache,
+                 int64_t cache_rows, int32_t* k_sign, int32_t* k_mag, void* k_low, void* k_delta, int64_t capacity,
+                 const int64_t* token_counts, int64_t batch, int64_t kv_heads, int32_t token_group_size,
+                 int32_t dim_group_size, int32_t* status, void* stream) {
+    if (!new_k || !new_v || !key_cache || !value_cache || !k_sign || !k_mag || !k_low || !k_delta || !token_counts)
+        return fail(POPKV_ERR_INVALID, "null pointer");
+    if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "keys must be fp32/fp16/bf16");
+    if (batch <= 0 || kv_heads <= 0 || batch * kv_heads > 0x7fffffff)
+        return fail(POPKV_ERR_INVALID, "bad batch or KV head count");
+    if (cache_rows <= 0 || capacity <= 0) return fail(POPKV_ERR_CAPACITY, "Pop-KV cache capacity exceeded");
+    if (token_group_size < 1 || token_group_size > 4096)
+        return fail(POPKV_ERR_INVALID, "token_group_size must be between 1 and 4096");
+    if (!valid_group(dim_group_size)) return fail(POPKV_ERR_INVALID, "dim_group_size must be 16, 32, or 64");
+    const size_t es = elem_size(dtype);
+    if (!aligned16(new_k) || !aligned16(new_v) || !aligned16(key_cache) || !aligned16(value_cache) ||
+        !aligned16(k_sign) || !aligned16(k_mag) || !aligned16(k_low) || !aligned16(k_delta) ||
+        (cache_rows * 128 * static_cast<int64_t>(es)) % 16)
+        return fail(POPKV_ERR_UNSUPPORTED, "append tensors need 16-byte alignment");
+    return launched(popkv::launch_append(new_k, new_v, dtype, key_cache, value_cache, cache_rows, token_counts, batch,
+                                         static_cast<int>(kv_heads), k_sign, k_mag, static_cast<uint16_t*>(k_low),
+                                         static_cast<uint16_t*>(k_delta), capacity, token_group_size, dim_group_size,
+                                         status, as_stream(stream)),
+                    "popkv_append");
+}
+
 int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
                                int64_t k_head_stride, int64_t v_head_stride, const int64_t* head_to_kv,
                                int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget, void* workspace,
@@ -464,7 +570,7 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* p
                         reinterpret_cast<const uint32_t*>(ws + L.rec), reinterpret_cast<const uint16_t*>(ws + L.h2),
                         reinterpret_cast<const uint32_t*>(ws + L.gt1), reinterpret_cast<uint32_t*>(ws + L.hist),
                         head_to_kv, static_cast<int>(q_heads), static_cast<int>(kv_heads),
-                        reinterpret_cast<float*>(ws + L.partials), nullptr, 0, as_stream(stream)),
+                        reinterpret_cast<float*>(ws + L.partials), nullptr, 0, popkv::SeqTable{}, as_stream(stream)),
                     "popkv_layer_step_attention");
 }
 
@@ -506,7 +612,7 @@ int popkv_dense_attention(const void* queries, int32_t dtype, const void* prefix
     }
     return launched(popkv::launch_merge_current(partials, ns, queries, dtype, current_k, current_v, nullptr,
                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads), output,
-                                                nullptr, 0, 0, 0, s),
+                                                nullptr, 0, 0, 0, popkv::SeqTable{}, s),
                     "popkv_dense_attention(merge)");
 }
 

@@ -9,6 +9,23 @@
 
 namespace popkv {
 
+// Per-sequence shape of a batched layer step (B independent sequences of
+// different lengths, one launch).  Row h of the step (query head h % q_heads
+// of sequence b = h / q_heads) covers min(max(tokens[b], 0), ntok) cached
+// tokens, ntok being the launch's token bound, and selects
+// min(budget - 1, that) of them.  Packed caches are [B, KVH, capacity, .]
+// (cache_rows = KVH * capacity rows per sequence), K/V storage
+// [B, KVH, rows, 128] (k_bstride / v_bstride elements per sequence), current
+// k/v [B, KVH, 128], queries and outputs [B, QH, 128]; head_to_kv maps a
+// sequence's query heads to its KV heads.  tokens == nullptr: a single
+// sequence (the unbatched entries), every row at the launch's token count.
+struct SeqTable {
+    const int64_t* tokens = nullptr;
+    int64_t cache_rows = 0;
+    int64_t k_bstride = 0, v_bstride = 0;
+    int q_heads = 0, kv_heads = 0, budget = 0;
+};
+
 // n 32-bit words of device memory set to `value` (a fill kernel).
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t value, hipStream_t stream);
 
@@ -16,6 +33,18 @@ hipError_t launch_pack(const void* keys, int dtype, int64_t kv_heads, int64_t to
                        int64_t key_head_stride, int32_t* k_sign, int32_t* k_mag, uint16_t* k_low,
                        uint16_t* k_delta, int64_t capacity, int64_t token_offset, int token_group_size,
                        int dim_group_size, hipStream_t stream);
+
+// Fused per-token append (head_dim 128): for every (sequence b, KV head j)
+// of a batch, write new_k / new_v [B*KVH, 128] to row counts[b] of the
+// static caches [B*KVH, cache_rows, 128] and re-encode the sequence's active
+// token group (rows counts[b] - counts[b] % tg .. counts[b], read in place)
+// into the packed planes [B*KVH, capacity, .].  counts: device int64 [B],
+// not modified; a count outside [0, min(cache_rows, capacity)) writes
+// nothing and sets *status = 1 (status may be null).
+hipError_t launch_append(const void* new_k, const void* new_v, int dtype, void* key_cache, void* value_cache,
+                         int64_t cache_rows, const int64_t* counts, int64_t batch, int kv_heads, int32_t* k_sign,
+                         int32_t* k_mag, uint16_t* k_low, uint16_t* k_delta, int64_t capacity,
+                         int token_group_size, int dim_group_size, int32_t* status, hipStream_t stream);
 
 hipError_t launch_query_encode(const void* queries, int dtype, int64_t rows, int head_dim,
                                int dim_group_size, int order, int32_t* q_sign, int32_t* q_mag,
@@ -36,7 +65,7 @@ hipError_t launch_score_d128_raw(const void* queries, int dtype, const int32_t* 
                                  const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
                                  int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
                                  int dim_group_size, uint16_t* keys, int64_t key_row_stride, uint32_t* ghist,
-                                 hipStream_t stream);
+                                 const SeqTable& seq, hipStream_t stream);
 
 hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, const float* q_low,
                                 const float* q_delta, const int32_t* k_sign, const int32_t* k_mag,
@@ -86,13 +115,15 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
 // partials[head][chunk][130], writes them as int64 to idx_out[head][rank]
 // when idx_out is non-null, and re-zeroes ghist.
 hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t rows, int64_t tokens, int64_t k,
-                             const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, hipStream_t stream);
+                             const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, const SeqTable& seq,
+                             hipStream_t stream);
 hipError_t launch_attention_select_chunks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                           int64_t k_head_stride, int64_t v_head_stride, const uint16_t* keys,
                                           int64_t key_stride, int64_t tokens, int64_t k, const uint32_t* rec,
                                           const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
-                                          int64_t* idx_out, int64_t idx_stride, hipStream_t stream);
+                                          int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
+                                          hipStream_t stream);
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
 // Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one
@@ -107,6 +138,6 @@ hipError_t launch_attention_dense(const void* queries, int dtype, const void* pr
 hipError_t launch_merge_current(const float* partials, int nsplit, const void* queries, int dtype,
                                 const void* current_k, const void* current_v, const int64_t* head_to_kv, int q_heads,
                                 int kv_heads, void* output, int64_t* idx_out, int64_t idx_stride, int64_t idx_slot,
-                                int64_t current, hipStream_t stream);
+                                int64_t current, const SeqTable& seq, hipStream_t stream);
 
 }  // namespace popkv

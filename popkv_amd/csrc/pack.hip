@@ -208,18 +208,80 @@ template <> __device__ __forceinline__ void load2<float>(const float* p, float& 
 // dimensions (whole plane words and whole representatives).
 template <int G> constexpr int pack128_waves() { return 128 / (G > 32 ? G : 32); }
 
-template <typename T, int G>
+// Operands of the fused append (APPEND form of pack128_kernel): block i
+// serves KV head i % kv_heads of sequence b = i / kv_heads, whose cache
+// holds counts[b] tokens.  new_k / new_v [B*KVH, 128] are the new token's
+// rows; key_cache / value_cache [B*KVH, cache_rows, 128] the static caches
+// (the new rows go to row counts[b]); the packed planes have `cap` rows per
+// (sequence, KV head).  A count outside [0, min(cache_rows, cap)) writes
+// nothing and sets *status to 1 (when status is non-null).
+template <typename T>
+struct AppendArgs {
+    const T* new_k = nullptr;
+    const T* new_v = nullptr;
+    T* key_cache = nullptr;
+    T* value_cache = nullptr;
+    int64_t cache_rows = 0;
+    const int64_t* counts = nullptr;
+    int kv_heads = 1;
+    int32_t* status = nullptr;
+};
+
+// Prefix prepack (APPEND false): block (x, y) encodes token group x of KV
+// head y, rows [x*tg, min(x*tg + tg, tokens)) of `keys`, into packed rows
+// y*cap + offset + x*tg + t.
+// Fused append (APPEND true, see AppendArgs): the new token joins its
+// sequence's active group -- rows [sealed, count) read in place from the
+// static key cache, then the new key itself, sealed = count - count % tg --
+// and the whole group is re-encoded into packed rows sealed .. count; the
+// new K/V rows are written to the static caches by the same block.
+template <typename T, int G, bool APPEND>
 __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     const T* __restrict__ keys, int64_t head_stride, int64_t tokens, int tg,
     int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
-    uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta, int64_t cap, int64_t offset) {
+    uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta, int64_t cap, int64_t offset,
+    AppendArgs<T> ap) {
     constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int64_t kvh = blockIdx.y;
-    const int64_t gs = static_cast<int64_t>(blockIdx.x) * tg;
-    const int n = static_cast<int>(min(gs + static_cast<int64_t>(tg), tokens) - gs);
-    const T* base = keys + kvh * head_stride + gs * D;
+    int n;
+    const T* base;             // row t < n (t < n - 1 in the append) is base + t * D
+    const T* last = nullptr;   // the append's new key (row n - 1)
+    int64_t orow0;             // packed row of token 0
+    if constexpr (!APPEND) {
+        const int64_t kvh = blockIdx.y;
+        const int64_t gs = static_cast<int64_t>(blockIdx.x) * tg;
+        n = static_cast<int>(min(gs + static_cast<int64_t>(tg), tokens) - gs);
+        base = keys + kvh * head_stride + gs * D;
+        orow0 = kvh * cap + offset + gs;
+    } else {
+        const int64_t bh = blockIdx.x;
+        const int64_t count = ap.counts[bh / ap.kv_heads];
+        if (count < 0 || count >= ap.cache_rows || count >= cap) {
+            if (ap.status != nullptr && threadIdx.x == 0) *ap.status = 1;
+            return;
+        }
+        // the new K and V rows into the static caches, 16 bytes per thread
+        constexpr int VEC = D * static_cast<int>(sizeof(T)) / 16;
+        static_assert(2 * VEC <= kWave * NW, "one 16-byte slice per thread");
+        const int64_t dst_row = (bh * ap.cache_rows + count) * D;
+        if (threadIdx.x < VEC) {
+            reinterpret_cast<uint4*>(ap.key_cache + dst_row)[threadIdx.x] =
+                reinterpret_cast<const uint4*>(ap.new_k + bh * D)[threadIdx.x];
+        } else if (threadIdx.x < 2 * VEC) {
+            reinterpret_cast<uint4*>(ap.value_cache + dst_row)[threadIdx.x - VEC] =
+                reinterpret_cast<const uint4*>(ap.new_v + bh * D)[threadIdx.x - VEC];
+        }
+        const int64_t sealed = count - count % tg;
+        n = static_cast<int>(count - sealed) + 1;
+        base = ap.key_cache + (bh * ap.cache_rows + sealed) * D;
+        last = ap.new_k + bh * D;
+        orow0 = bh * cap + sealed;
+    }
+    auto row_of = [&](int t) -> const T* {
+        if constexpr (APPEND) return t == n - 1 ? last : base + static_cast<int64_t>(t) * D;
+        else return base + static_cast<int64_t>(t) * D;
+    };
 
     // Phase 1: extrema of dims 2*lane, 2*lane+1; wave w takes tokens w, w+NW, ...
     float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
@@ -228,7 +290,7 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
 #pragma unroll
         for (int i = 0; i < PH1; ++i) {
             const int t = min(t0 + i * NW, n - 1);  // repeats the last row: min/max unchanged
-            load2<T>(base + static_cast<int64_t>(t) * D + 2 * lane, a[i], b[i]);
+            load2<T>(row_of(t) + 2 * lane, a[i], b[i]);
         }
 #pragma unroll
         for (int i = 0; i < PH1; ++i) {
@@ -269,8 +331,8 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
         // 16 partial sums live instead of 64 contributions.  Bits are placed
         // at their positions directly.  The row stays packed (8 x 16 bytes).
         for (int t = lane; t < n; t += kWave) {
-            const T* row = base + static_cast<int64_t>(t) * D + c0;
-            const int64_t orow = kvh * cap + offset + gs + t;
+            const T* row = row_of(t) + c0;
+            const int64_t orow = orow0 + t;
             Raw8<T> raw[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) raw[c].load(row + 8 * c);
@@ -338,8 +400,8 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
         return;
     }
     for (int t = lane; t < n; t += kWave) {
-        const T* row = base + static_cast<int64_t>(t) * D + c0;
-        const int64_t orow = kvh * cap + offset + gs + t;
+        const T* row = row_of(t) + c0;
+        const int64_t orow = orow0 + t;
         constexpr int NWD = CH / 32, NR = CH / G;
         uint32_t sw[NWD], mw[NWD];
         float lows[NR], deltas[NR];
@@ -421,8 +483,8 @@ hipError_t launch_pack_t(const T* keys, int64_t kvh, int64_t tokens, int d, int6
                       (reinterpret_cast<uintptr_t>(ks) % 16 == 0) && (reinterpret_cast<uintptr_t>(km) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(kl) % 16 == 0) && (reinterpret_cast<uintptr_t>(kd) % 16 == 0);
     if (fast)
-        hipLaunchKernelGGL((pack128_kernel<T, G>), grid, dim3(kWave * pack128_waves<G>()), 0, stream, keys,
-                           head_stride, tokens, tg, ks, km, kl, kd, cap, off);
+        hipLaunchKernelGGL((pack128_kernel<T, G, false>), grid, dim3(kWave * pack128_waves<G>()), 0, stream, keys,
+                           head_stride, tokens, tg, ks, km, kl, kd, cap, off, AppendArgs<T>{});
     else
         hipLaunchKernelGGL((pack_kernel<T, G, false>), grid, dim3(kPackThreads), 0, stream, keys, head_stride,
                            tokens, d, tg, ks, km, kl, kd, cap, off);
@@ -440,7 +502,66 @@ hipError_t launch_pack_g(const T* keys, int64_t kvh, int64_t tokens, int d, int6
     }
 }
 
+template <typename T>
+hipError_t launch_append_t(const AppendArgs<T>& ap, int64_t rows, int tg, int g, int32_t* ks, int32_t* km,
+                           uint16_t* kl, uint16_t* kd, int64_t cap, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(rows));
+    switch (g) {
+        case 16:
+            hipLaunchKernelGGL((pack128_kernel<T, 16, true>), grid, dim3(kWave * pack128_waves<16>()), 0, stream,
+                               nullptr, 0, 0, tg, ks, km, kl, kd, cap, 0, ap);
+            break;
+        case 32:
+            hipLaunchKernelGGL((pack128_kernel<T, 32, true>), grid, dim3(kWave * pack128_waves<32>()), 0, stream,
+                               nullptr, 0, 0, tg, ks, km, kl, kd, cap, 0, ap);
+            break;
+        default:
+            hipLaunchKernelGGL((pack128_kernel<T, 64, true>), grid, dim3(kWave * pack128_waves<64>()), 0, stream,
+                               nullptr, 0, 0, tg, ks, km, kl, kd, cap, 0, ap);
+            break;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_append_dt(const void* new_k, const void* new_v, void* key_cache, void* value_cache,
+                            int64_t cache_rows, const int64_t* counts, int64_t batch, int kv_heads, int32_t* k_sign,
+                            int32_t* k_mag, uint16_t* k_low, uint16_t* k_delta, int64_t capacity, int tg, int g,
+                            int32_t* status, hipStream_t stream) {
+    AppendArgs<T> ap;
+    ap.new_k = static_cast<const T*>(new_k);
+    ap.new_v = static_cast<const T*>(new_v);
+    ap.key_cache = static_cast<T*>(key_cache);
+    ap.value_cache = static_cast<T*>(value_cache);
+    ap.cache_rows = cache_rows;
+    ap.counts = counts;
+    ap.kv_heads = kv_heads;
+    ap.status = status;
+    return launch_append_t<T>(ap, batch * kv_heads, tg, g, k_sign, k_mag, k_low, k_delta, capacity, stream);
+}
+
 }  // namespace
+
+hipError_t launch_append(const void* new_k, const void* new_v, int dtype, void* key_cache, void* value_cache,
+                         int64_t cache_rows, const int64_t* counts, int64_t batch, int kv_heads, int32_t* k_sign,
+                         int32_t* k_mag, uint16_t* k_low, uint16_t* k_delta, int64_t capacity,
+                         int token_group_size, int dim_group_size, int32_t* status, hipStream_t stream) {
+    if (batch <= 0 || kv_heads <= 0) return hipSuccess;
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_append_dt<float>(new_k, new_v, key_cache, value_cache, cache_rows, counts, batch, kv_heads,
+                                           k_sign, k_mag, k_low, k_delta, capacity, token_group_size,
+                                           dim_group_size, status, stream);
+        case POPKV_DTYPE_F16:
+            return launch_append_dt<f16_t>(new_k, new_v, key_cache, value_cache, cache_rows, counts, batch, kv_heads,
+                                           k_sign, k_mag, k_low, k_delta, capacity, token_group_size,
+                                           dim_group_size, status, stream);
+        default:
+            return launch_append_dt<bf16_t>(new_k, new_v, key_cache, value_cache, cache_rows, counts, batch,
+                                            kv_heads, k_sign, k_mag, k_low, k_delta, capacity, token_group_size,
+                                            dim_group_size, status, stream);
+    }
+}
 
 hipError_t launch_pack(const void* keys, int dtype, int64_t kv_heads, int64_t tokens, int head_dim,
                        int64_t key_head_stride, int32_t* k_sign, int32_t* k_mag, uint16_t* k_low,

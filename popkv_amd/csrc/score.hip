@@ -22,6 +22,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "select_common.h"
 
 namespace popkv {
 namespace {
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const uint16_t* __restrict__ k_low, const uint16_t* __restrict__ k_delta,
     const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, int qpk_rt,
     int64_t cap, int64_t tokens, uint16_t* __restrict__ scores, int64_t out_stride,
-    uint32_t* __restrict__ ghist) {
+    uint32_t* __restrict__ ghist, SeqTable seq) {
     constexpr int R = 128 / G;
     // Layer-step mode (the kernel encodes the raw query): the output holds the
     // scores' radix order keys instead of fp16 bits, and the per-head 256-bin
@@ -346,6 +347,12 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     // A mapping outside [0, kv_heads) is clamped, never dereferenced.
     const int64_t kvh = min(max(head_to_kv[qh0], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
     const int64_t qrow0 = b * q_heads + qh0;
+    // packed rows of this KV head (a batched step gives each sequence its own
+    // cache; the reference's batch shares one), and the tokens scored: a
+    // batched step's sequences end at their own counts (the loads below stay
+    // within the launch bound `tokens`, the stores within the sequence's)
+    const int64_t cbase = b * seq.cache_rows + kvh * cap;
+    const int64_t ntok_b = seq.tokens != nullptr ? seq_tokens_of(seq, b, tokens) : tokens;
 
     // Load order matters: loads retire in issue order (vmcnt), so the raw
     // query values the encode needs are loaded first, then this thread's
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
 #pragma unroll
     for (int it = 0; it < TPT; ++it) {
         tok[it] = (static_cast<int64_t>(blockIdx.x) * TPT + it) * kScoreThreads + threadIdx.x;
-        const int64_t krow = kvh * cap + min(tok[it], tokens - 1);
+        const int64_t krow = cbase + min(tok[it], tokens - 1);
         s4[it] = k_sign[krow];
         m4[it] = k_mag[krow];
         lw[it] = reinterpret_cast<const RepWord*>(k_low)[krow];
@@ -452,7 +459,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
 #pragma unroll
         for (int it = 0; it < TPT; ++it) {
             const int64_t t = tok[it];
-            if (t >= tokens) break;
+            if (t >= ntok_b) break;
             const float sc = scs[it];
             const uint16_t bits = f16_rne(sc);
             // byte offset as 32 bits (tokens < 2^31): the store then takes the
@@ -557,7 +564,8 @@ template <int G, typename QT>
 hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float* ql, const float* qd, const QT* q_raw,
                                const int32_t* ks, const int32_t* km, const uint16_t* kl, const uint16_t* kd,
                                const int64_t* h2k, int64_t batch, int qh, int kvh, int64_t cap, int64_t tokens,
-                               uint16_t* out, int64_t out_stride, uint32_t* ghist, hipStream_t stream) {
+                               uint16_t* out, int64_t out_stride, uint32_t* ghist, const SeqTable& seq,
+                               hipStream_t stream) {
     const int qpk = qh / kvh;
     const int64_t per_block = static_cast<int64_t>(kScoreThreads) * score_tokens_per_thread<G>();
     dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block), static_cast<unsigned>(batch * kvh));
@@ -565,7 +573,7 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
     const uint4* km4 = reinterpret_cast<const uint4*>(km);
 #define POPKV_SCORE_LAUNCH(Q)                                                                                 \
     hipLaunchKernelGGL((score_d128_kernel<G, Q, QT>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd, q_raw, \
-                       ks4, km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride, ghist)
+                       ks4, km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride, ghist, seq)
     switch (qpk) {
         case 1: POPKV_SCORE_LAUNCH(1); break;
         case 2: POPKV_SCORE_LAUNCH(2); break;
@@ -582,20 +590,20 @@ hipError_t launch_score_d128_q(const int32_t* q_sign, const int32_t* q_mag, cons
                                const QT* q_raw, const int32_t* k_sign, const int32_t* k_mag, const uint16_t* k_low,
                                const uint16_t* k_delta, const int64_t* head_to_kv, int64_t batch, int q_heads,
                                int kv_heads, int64_t capacity, int64_t tokens, int dim_group_size, uint16_t* scores,
-                               int64_t score_row_stride, uint32_t* ghist, hipStream_t stream) {
+                               int64_t score_row_stride, uint32_t* ghist, const SeqTable& seq, hipStream_t stream) {
     switch (dim_group_size) {
         case 16:
             return launch_score_d128_g<16, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
-                                               score_row_stride, ghist, stream);
+                                               score_row_stride, ghist, seq, stream);
         case 32:
             return launch_score_d128_g<32, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
-                                               score_row_stride, ghist, stream);
+                                               score_row_stride, ghist, seq, stream);
         default:
             return launch_score_d128_g<64, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
-                                               score_row_stride, ghist, stream);
+                                               score_row_stride, ghist, seq, stream);
     }
 }
 
@@ -625,28 +633,30 @@ hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const 
                              int64_t score_row_stride, hipStream_t stream) {
     return launch_score_d128_q<void>(q_sign, q_mag, q_low, q_delta, nullptr, k_sign, k_mag, k_low, k_delta,
                                      head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size, scores,
-                                     score_row_stride, nullptr, stream);
+                                     score_row_stride, nullptr, SeqTable{}, stream);
 }
 
 hipError_t launch_score_d128_raw(const void* queries, int dtype, const int32_t* k_sign, const int32_t* k_mag,
                                  const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
                                  int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
                                  int dim_group_size, uint16_t* keys, int64_t key_row_stride, uint32_t* ghist,
-                                 hipStream_t stream) {
+                                 const SeqTable& seq, hipStream_t stream) {
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_score_d128_q<float>(nullptr, nullptr, nullptr, nullptr, static_cast<const float*>(queries),
                                               k_sign, k_mag, k_low, k_delta, head_to_kv, batch, q_heads, kv_heads,
-                                              capacity, tokens, dim_group_size, keys, key_row_stride, ghist, stream);
+                                              capacity, tokens, dim_group_size, keys, key_row_stride, ghist, seq,
+                                              stream);
         case POPKV_DTYPE_F16:
             return launch_score_d128_q<f16_t>(nullptr, nullptr, nullptr, nullptr, static_cast<const f16_t*>(queries),
                                               k_sign, k_mag, k_low, k_delta, head_to_kv, batch, q_heads, kv_heads,
-                                              capacity, tokens, dim_group_size, keys, key_row_stride, ghist, stream);
+                                              capacity, tokens, dim_group_size, keys, key_row_stride, ghist, seq,
+                                              stream);
         default:
             return launch_score_d128_q<bf16_t>(nullptr, nullptr, nullptr, nullptr,
                                                static_cast<const bf16_t*>(queries), k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size,
-                                               keys, key_row_stride, ghist, stream);
+                                               keys, key_row_stride, ghist, seq, stream);
     }
 }
 

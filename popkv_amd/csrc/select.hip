@@ -350,7 +350,8 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_hist_kernel(const uint16_
                                                                    const uint32_t* __restrict__ ghist,
                                                                    uint32_t* __restrict__ rec,
                                                                    uint16_t* __restrict__ h2,
-                                                                   uint32_t* __restrict__ gt1, int nchunks) {
+                                                                   uint32_t* __restrict__ gt1, int nchunks,
+                                                                   SeqTable seq) {
     constexpr int CH = kChunkThreads * KPT;
     const int c = blockIdx.x;
     const int h = blockIdx.y;
@@ -358,9 +359,15 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_hist_kernel(const uint16_
     const int lane = tid & (kWave - 1);
     const int begin = c * CH + tid * KPT;
     ChunkKeys<KPT> kk;
-    load_chunk_keys<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, max(0, min(KPT, ntok - begin)), kk);
+    load_chunk_keys_raw<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, max(0, min(KPT, ntok - begin)), kk);
     uint32_t cnt[4];
     load_rank4(ghist + static_cast<int64_t>(h) * kBins, cnt);
+    if (seq.tokens != nullptr) {  // a batched step: this row's own token count and k
+        ntok = static_cast<int>(seq_tokens_of(seq, h / seq.q_heads, ntok));
+        k = min(seq.budget - 1, ntok);
+        if (k <= 0 || k >= ntok || c * CH >= ntok) return;
+    }
+    mask_chunk_keys<KPT>(max(0, min(KPT, ntok - begin)), kk);
     __shared__ uint32_t s_h2[kBins];
     __shared__ uint32_t s_gt;
     s_h2[tid] = 0u;
@@ -539,7 +546,8 @@ hipError_t launch_topk_list(const uint16_t* keys, uint32_t* ghist, int64_t rows,
 }
 
 hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t rows, int64_t tokens, int64_t k,
-                             const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, hipStream_t stream) {
+                             const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, const SeqTable& seq,
+                             hipStream_t stream) {
     if (rows <= 0 || k <= 0 || k >= tokens) return hipSuccess;
     const StepChunks ch = step_chunks(tokens, k);
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
@@ -547,7 +555,7 @@ hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t r
 #define POPKV_CH(KPT)                                                                                          \
     case KPT:                                                                                                  \
         hipLaunchKernelGGL((chunk_hist_kernel<KPT>), grid, block, 0, stream, keys, key_stride, nt, kk, ghist, \
-                           rec, h2, gt1, nc);                                                                  \
+                           rec, h2, gt1, nc, seq);                                                             \
         break
     switch (ch.kpt) {
         POPKV_CH(1); POPKV_CH(2); POPKV_CH(4); POPKV_CH(6); POPKV_CH(8); POPKV_CH(12); POPKV_CH(16); POPKV_CH(24); POPKV_CH(32);
@@ -621,7 +629,7 @@ hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_
     uint32_t* gt1 = reinterpret_cast<uint32_t*>(base + w.gt1);
     uint16_t* h2 = reinterpret_cast<uint16_t*>(base + w.h2);
     // chunk_hist_kernel runs for 0 < k < tokens only, on step_chunks(tokens, k)
-    hipError_t e = launch_chunk_hist(keys, key_stride, rows, tokens, k, ghist, rec, h2, gt1, stream);
+    hipError_t e = launch_chunk_hist(keys, key_stride, rows, tokens, k, ghist, rec, h2, gt1, SeqTable{}, stream);
     if (e != hipSuccess) {
         (void)launch_fill_u32(ghist, rows * kBins, 0u, stream);  // the histograms stay zero between calls
         return e;

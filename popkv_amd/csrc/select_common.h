@@ -5,8 +5,15 @@
 // are >= 0x03ff), so they never reach the threshold bucket.
 #pragma once
 #include "device_common.h"
+#include "kernels.h"
 
 namespace popkv {
+
+// Cached tokens of sequence b of a batched step, clamped into [0, bound].
+__device__ __forceinline__ int64_t seq_tokens_of(const SeqTable& seq, int64_t b, int64_t bound) {
+    const int64_t t = seq.tokens[b];
+    return t < 0 ? 0 : (t > bound ? bound : t);
+}
 
 // Tokens of a chunk: one workgroup of kChunkThreads threads, KPT consecutive
 // tokens per thread, so a chunk is kChunkThreads * KPT tokens.
@@ -26,10 +33,13 @@ template <int KPT> struct ChunkKeys {
 // `row` starts 256-byte aligned and begin is a multiple of KPT, so loads of
 // the widest size that divides 2*KPT bytes are aligned.  Every load is
 // issued before any is used; a load past the row's tokens re-reads the
-// row's first keys and is zeroed.
+// row's first keys and is zeroed.  load_chunk_keys_raw issues the loads for
+// the first n keys (the rest re-read the row's start, unmasked);
+// mask_chunk_keys then zeroes every key at or past n (which may be smaller
+// than the n the loads were issued for).
 template <int KPT>
-__device__ __forceinline__ void load_chunk_keys(const uint16_t* __restrict__ row, int begin, int n,
-                                                ChunkKeys<KPT>& k) {
+__device__ __forceinline__ void load_chunk_keys_raw(const uint16_t* __restrict__ row, int begin, int n,
+                                                    ChunkKeys<KPT>& k) {
     if constexpr (KPT % 8 == 0) {
         uint4 u[KPT / 8];
 #pragma unroll
@@ -59,11 +69,22 @@ __device__ __forceinline__ void load_chunk_keys(const uint16_t* __restrict__ row
     } else {
         k.w[0] = row[n > 0 ? begin : 0];
     }
+}
+
+template <int KPT>
+__device__ __forceinline__ void mask_chunk_keys(int n, ChunkKeys<KPT>& k) {
     if (n < KPT) {  // the row's ragged end (or a thread past it)
 #pragma unroll
         for (int i = 0; i < ChunkKeys<KPT>::W; ++i)
             k.w[i] &= (2 * i + 1 < n ? 0xffff0000u : 0u) | (2 * i < n ? 0x0000ffffu : 0u);
     }
+}
+
+template <int KPT>
+__device__ __forceinline__ void load_chunk_keys(const uint16_t* __restrict__ row, int begin, int n,
+                                                ChunkKeys<KPT>& k) {
+    load_chunk_keys_raw<KPT>(row, begin, n, k);
+    mask_chunk_keys<KPT>(n, k);
 }
 
 // Bit masks of the thread's keys: bit e of *gt = key e > thr, of *eq =

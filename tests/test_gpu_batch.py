@@ -1,0 +1,264 @@
+"""Batched decode with in-place cache maintenance on the GPU, against the
+CPU oracle.
+
+  * The fused append (popkv_append) re-encodes each sequence's active token
+    group from the static K cache in place; the packed planes stay
+    bit-exact with the oracle's prefix encode of the whole sequence across
+    every token-group boundary (the reference's incremental == prefix test,
+    tests/test_popkv.py:354-372, at TG 8..128 and G 16/32/64), and the new
+    K/V rows land in the static caches.
+  * The batched layer step (popkv_layer_step_batched) serves sequences of
+    different lengths in one call; each sequence's indices equal its own
+    oracle's and its attention is within 2e-2 / 1e-2 -- before and after an
+    append, and for a decode step captured once in a HIP graph and replayed
+    while the device lengths grow.
+  * C4's shape: eight 64K sequences, two of them checked against their own
+    oracles after an append step.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from popkv_amd import batch as pb
+from popkv_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+ATTN_ATOL, ATTN_RTOL = 2e-2, 1e-2
+
+
+def f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def bits(t):
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def _packed_np(cache, b):
+    return tuple(bits(t[b]) if t.dtype != torch.int32 else t[b].cpu().numpy() for t in cache.packed)
+
+
+def _seq_data(batch, kv_heads, rows, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(batch, kv_heads, rows, 128, generator=g).to(dtype)
+    v = torch.randn(batch, kv_heads, rows, 128, generator=g).to(dtype)
+    return k, v
+
+
+@pytest.mark.parametrize("tg", [8, 16, 32, 64, 128])
+def test_fused_append_crosses_every_token_group_boundary(tg):
+    """Three sequences starting at TG-2, 3TG-1 and 2TG tokens; three
+    appends seal a group, fill one and start new ones.  After every append
+    each sequence's packed rows equal the oracle's prefix encode of its
+    whole key sequence, bit for bit, and the static caches hold the new
+    rows."""
+    starts = [tg - 2, 3 * tg - 1, 2 * tg]
+    rows = 3 * tg + 8
+    for g in (16, 32, 64):
+        keys, values = _seq_data(3, 2, rows, seed=70 + tg + g)
+        kc = torch.zeros(3, 2, rows, 128, dtype=torch.bfloat16, device=DEV)
+        vc = torch.zeros_like(kc)
+        for b, n in enumerate(starts):
+            kc[b, :, :n] = keys[b, :, :n].to(DEV)
+            vc[b, :, :n] = values[b, :, :n].to(DEV)
+        lengths = pb.SequenceLengths.create(starts, DEV)
+        cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g)
+        status = torch.zeros(1, dtype=torch.int32, device=DEV)
+        for step in range(3):
+            cur = lengths.host
+            nk = torch.stack([keys[b, :, cur[b]] for b in range(3)]).to(DEV)
+            nv = torch.stack([values[b, :, cur[b]] for b in range(3)]).to(DEV)
+            pb.append_batched(cache, lengths, nk, nv, status=status)
+            lengths.advance()
+            torch.cuda.synchronize()
+            for b in range(3):
+                n = lengths.host[b]
+                want = core.pack_keys(f32(keys[b, :, :n]), token_group_size=tg, dim_group_size=g)
+                for a, w in zip(_packed_np(cache, b), want):
+                    assert np.array_equal(a[:, :n], w), (tg, g, step, b)
+                assert torch.equal(kc[b, :, n - 1].cpu(), keys[b, :, n - 1])
+                assert torch.equal(vc[b, :, n - 1].cpu(), values[b, :, n - 1])
+        assert int(status.item()) == 0
+
+
+def test_fused_append_full_sequence_is_refused():
+    kc = torch.zeros(2, 2, 16, 128, dtype=torch.bfloat16, device=DEV)
+    lengths = pb.SequenceLengths.create([16, 3], DEV)
+    cache = pb.build_batched_popkv_cache(kc, kc.clone(), lengths, group_size=8, dim_group_size=32)
+    nk = torch.zeros(2, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="reserve exhausted"):
+        pb.append_batched(cache, lengths, nk, nk)
+    # the device check: a count the host mirror does not know about
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    lengths.host = [3, 3]
+    before = cache.key_cache.clone()
+    pb.append_batched(cache, lengths, nk + 1, nk + 1, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1
+    assert torch.equal(cache.key_cache[0], before[0])  # the full sequence is untouched
+    assert torch.equal(cache.key_cache[1, :, 3].float().cpu(), torch.ones(2, 128))
+
+
+def _oracle_seq(q, kc, vc, ck, cv, cache, b, n, mapping, budget, g):
+    """Oracle of one sequence of the batch at n cached tokens, from the
+    static rows alone (its own prefix encode, not the GPU's planes: an
+    append re-encodes the active group's earlier rows too)."""
+    h2k = mapping.cpu().numpy()
+    enc = core.query_encode(f32(q[b])[None], g, order="fold")
+    pk = core.pack_keys(f32(kc[b, :, :n]), token_group_size=cache.group_size, dim_group_size=g)
+    sc = core.score_encoded(enc, pk, head_to_kv=h2k, tokens=n, dim_group_size=g)[0]
+    kk = min(budget - 1, n)
+    idx = core.select(sc, kk, n)
+    out = core.attention(f32(q[b]), f32(kc[b, :, :n]), f32(vc[b, :, :n]), f32(ck[b]), f32(cv[b]), idx, h2k)
+    return idx, out
+
+
+def _assert_attention(got, want):
+    err = np.abs(f32(got) - want)
+    assert (err <= ATTN_ATOL + ATTN_RTOL * np.abs(want)).all(), float(err.max())
+
+
+def _check_batch(q, cache, lengths, ck, cv, mapping, budget, out, idx, check=None):
+    for b in (range(lengths.batch) if check is None else check):
+        n = lengths.host[b]
+        want_idx, want_out = _oracle_seq(q, cache.key_cache, cache.value_cache, ck, cv, cache, b, n, mapping,
+                                         budget, cache.dim_group_size)
+        kk = min(budget - 1, n)
+        assert np.array_equal(idx[b, :, :kk + 1].cpu().numpy(), want_idx), (b, n)
+        _assert_attention(out[b], want_out)
+
+
+@pytest.mark.parametrize("g,tg", [(64, 64), (16, 128), (32, 32)])
+def test_batched_layer_step_ragged_lengths(g, tg):
+    """Sequences of 5000, 3001, 700 (budget covers it: select-all), 7777 and
+    0 cached tokens in one call; then each appends a token and the step runs
+    again at the new lengths."""
+    starts = [5000, 3001, 700, 7777, 0]
+    batch, qh, kvh, rows, budget = len(starts), 32, 8, 7800, 1024
+    keys, values = _seq_data(batch, kvh, rows, seed=g + tg)
+    kc, vc = keys.to(DEV), values.to(DEV)
+    gq = torch.Generator().manual_seed(5)
+    lengths = pb.SequenceLengths.create(starts, DEV)
+    cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g)
+    mapping = torch.arange(qh, device=DEV) // (qh // kvh)
+    ws = pb.LayerStepWorkspace()
+    for step in range(2):
+        q = torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+        ck = torch.randn(batch, kvh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+        cv = torch.randn(batch, kvh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+        out, idx = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, workspace=ws,
+                                               return_indices=True)
+        _check_batch(q, cache, lengths, ck, cv, mapping, budget, out, idx)
+        out2 = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, workspace=ws)
+        assert torch.equal(out2, out)
+        pb.append_batched(cache, lengths, ck, cv)
+        lengths.advance()
+
+
+def test_batched_step_graph_replays_follow_growing_lengths():
+    """One decode step -- layer step, fused append, lengths += 1 -- captured
+    once in a HIP graph, then replayed three times with new tokens copied in
+    between: every replay's output and indices match the oracle at that
+    replay's lengths (the counts are read on the device)."""
+    starts = [3000, 1500, 2200]
+    batch, qh, kvh, rows, budget, g, tg = 3, 32, 8, 3100, 512, 64, 64
+    keys, values = _seq_data(batch, kvh, rows, seed=17)
+    kc = torch.zeros(batch, kvh, rows, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    for b, n in enumerate(starts):
+        kc[b, :, :n] = keys[b, :, :n].to(DEV)
+        vc[b, :, :n] = values[b, :, :n].to(DEV)
+    lengths = pb.SequenceLengths.create(starts, DEV)
+    cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g)
+    mapping = torch.arange(qh, device=DEV) // (qh // kvh)
+    ws = pb.LayerStepWorkspace()
+    gq = torch.Generator().manual_seed(8)
+    q = torch.empty(batch, qh, 128, dtype=torch.bfloat16, device=DEV)
+    ck = torch.empty(batch, kvh, 128, dtype=torch.bfloat16, device=DEV)
+    cv = torch.empty_like(ck)
+    out = torch.empty_like(q)
+    idx = torch.empty(batch, qh, budget, dtype=torch.int64, device=DEV)
+    bound = max(starts) + 8
+
+    def step():
+        o, i = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, max_tokens=bound,
+                                           workspace=ws, out=out, return_indices=True)
+        idx.copy_(i)
+        pb.append_batched(cache, lengths, ck, cv)
+        lengths.device.add_(1)
+
+    def next_token(r):
+        q.copy_(torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16))
+        ck.copy_(torch.stack([keys[b, :, lengths.host[b]] for b in range(batch)]))
+        cv.copy_(torch.stack([values[b, :, lengths.host[b]] for b in range(batch)]))
+
+    # warm-up on a side stream (it advances the lengths once), then capture
+    next_token(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    lengths.host = [x + 1 for x in lengths.host]
+    graph = torch.cuda.CUDAGraph()
+    next_token(0)
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    # capture ran nothing: the device lengths are still the host's
+    assert lengths.device.cpu().tolist() == lengths.host
+    for r in range(3):
+        next_token(r)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _check_batch(q, cache, lengths, ck, cv, mapping, budget, out, idx)
+        lengths.host = [x + 1 for x in lengths.host]
+        assert lengths.device.cpu().tolist() == lengths.host
+
+
+def test_c4_batch_after_an_append():
+    """C4's shape: eight sequences of 64K (PopKV-S, budget 4096, bf16, the
+    C1 distribution with seed 123 + b).  The prefixes hold 65534 tokens; the
+    append step adds token 65534 (static K/V row and metadata), then one
+    batched step with token 65535 as the current one; sequences 0 and 7 are
+    checked against their own oracles."""
+    w = workloads.C4
+    batch, rows = w.batch, w.context
+    kc = torch.empty(batch, w.kv_heads, rows, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.empty_like(kc)
+    qs, cks, cvs = [], [], []
+    for b in range(batch):
+        lay = workloads.make_layer(w, seed=w.seed + b)
+        kc[b] = lay.keys.to(DEV)
+        vc[b] = lay.values.to(DEV)
+        qs.append(lay.queries)
+        del lay
+    L = w.prefix_tokens  # 65535
+    new_k, new_v = kc[:, :, L - 1].clone(), vc[:, :, L - 1].clone()
+    cur_k, cur_v = kc[:, :, L].clone(), vc[:, :, L].clone()
+    kc[:, :, L - 1:] = 0  # the append writes row L - 1 back; row L stays outside the prefix
+    vc[:, :, L - 1:] = 0
+    lengths = pb.SequenceLengths.create([L - 1] * batch, DEV)
+    cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=w.token_group, dim_group_size=w.dim_group)
+    pb.append_batched(cache, lengths, new_k, new_v)
+    lengths.advance()
+    q = torch.stack(qs).to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    out, idx = pb.popkv_layer_step_batched(q, cache, lengths, cur_k, cur_v, mapping, budget=w.budget,
+                                           return_indices=True)
+    torch.cuda.synchronize()
+    for b in (0, 7):
+        want_pack = core.pack_keys(f32(kc[b, :, :L]), token_group_size=w.token_group, dim_group_size=w.dim_group)
+        for a, wp in zip(_packed_np(cache, b), want_pack):
+            assert np.array_equal(a[:, :L], wp), b
+    _check_batch(q, cache, lengths, cur_k, cur_v, mapping, w.budget, out, idx, check=(0, 7))

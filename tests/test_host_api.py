@@ -351,3 +351,49 @@ def test_library_host_only_entry_points():
     assert st == -6 and "workspace" in lib.popkv_last_error().decode()
     with pytest.raises(RuntimeError, match="capacity exceeded"):
         _native.check(lib.popkv_pack(fake, 2, 8, 10, 128, 1280, fake, fake, fake, fake, 12, 3, 64, 64, None))
+
+
+def test_batched_api_validation_before_the_device():
+    """popkv_amd.batch checks shapes, lengths and capacity on the host
+    before any launch (CPU tensors never reach the C ABI)."""
+    from popkv_amd import batch as pb
+
+    with pytest.raises(ValueError, match="non-negative"):
+        pb.SequenceLengths.create([3, -1], "cpu")
+    lengths = pb.SequenceLengths.create([3, 5], "cpu")
+    lengths.advance()
+    assert lengths.host == [4, 6] and lengths.device.tolist() == [4, 6]
+    kc = torch.zeros(2, 2, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="static K/V caches must be"):
+        pb.build_batched_popkv_cache(kc[..., :64], kc[..., :64], lengths, group_size=8, dim_group_size=32)
+    with pytest.raises(ValueError, match="3 lengths"):
+        pb.build_batched_popkv_cache(kc, kc, pb.SequenceLengths.create([1, 1, 1], "cpu"), group_size=8,
+                                     dim_group_size=32)
+    with pytest.raises(RuntimeError, match="capacity exceeded"):
+        pb.build_batched_popkv_cache(kc, kc, pb.SequenceLengths.create([9, 1], "cpu"), group_size=8,
+                                     dim_group_size=32)
+    with pytest.raises(ValueError, match="non-specialized"):
+        pb.build_batched_popkv_cache(kc, kc, lengths, group_size=5, dim_group_size=64)
+    planes = (torch.zeros(2, 2, 8, 4, dtype=torch.int32), torch.zeros(2, 2, 8, 4, dtype=torch.int32),
+              torch.zeros(2, 2, 8, 4, dtype=torch.float16), torch.zeros(2, 2, 8, 4, dtype=torch.float16))
+    cache = pb.BatchedPopKVCache(8, 32, planes, kc, kc.clone())
+    nk = torch.zeros(2, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="new K/V must be"):
+        pb.append_batched(cache, lengths, nk[:1], nk[:1])
+    with pytest.raises(RuntimeError, match="reserve exhausted"):
+        pb.append_batched(cache, pb.SequenceLengths.create([8, 2], "cpu"), nk, nk)
+    q = torch.zeros(2, 8, 128, dtype=torch.bfloat16)
+    h2k = torch.arange(8) // 4
+    step = pb.popkv_layer_step_batched
+    with pytest.raises(ValueError, match="q must be"):
+        step(q[:1], cache, lengths, nk, nk, h2k, budget=4)
+    with pytest.raises(ValueError, match="current k must be"):
+        step(q, cache, lengths, nk[:, :1], nk, h2k, budget=4)
+    with pytest.raises(ValueError, match="head_to_kv"):
+        step(q, cache, lengths, nk, nk, h2k[:4], budget=4)
+    with pytest.raises(ValueError, match="budget"):
+        step(q, cache, lengths, nk, nk, h2k, budget=1)
+    with pytest.raises(ValueError, match="max_tokens"):
+        step(q, cache, lengths, nk, nk, h2k, budget=4, max_tokens=5)
+    with pytest.raises(RuntimeError, match="invalid score token count"):
+        step(q, cache, lengths, nk, nk, h2k, budget=4, max_tokens=9)
