@@ -235,3 +235,31 @@ def test_tie_rule_matches_torch_topk_multi_block(kind, tokens):
             assert set(ours[r].tolist()) == set(ref[r].tolist()), (kind, tokens, k, r)
         want = core.select(bits(s), k, tokens)
         assert np.array_equal(topk.select_with_current(s, k, tokens + 1).cpu().numpy(), want)
+
+
+# ------------------------------------------------------------------ wire format
+
+def test_packed_metadata_hand_off_through_the_wire_format():
+    """Prefill -> decode hand-off: a cache prepacked on the GPU is
+    serialized (popkv_amd.wire), loaded back onto the device, and the layer
+    step over it gives the same output and selection; appends then resume
+    from the transported active keys, bit-exact with the oracle."""
+    from popkv_amd import wire
+
+    w = workloads.scaled(workloads.C1, context=5000, budget=1024)
+    layer, mapping, cache = _setup(w)
+    blob = wire.to_bytes(cache)
+    back = wire.from_bytes(blob, device=DEV)
+    args = (layer.prefix_k(), layer.prefix_v(), layer.current_k(), layer.current_v(), mapping)
+    o1, i1 = popkv.popkv_layer_step(layer.queries, cache, *args, budget=w.budget, return_indices=True)
+    o2, i2 = popkv.popkv_layer_step(layer.queries, back, *args, budget=w.budget, return_indices=True)
+    assert torch.equal(i1, i2) and torch.equal(o1, o2)
+    keys = layer.prefix_k()
+    for step in range(3):
+        new = torch.randn(w.kv_heads, 1, 128, generator=torch.Generator().manual_seed(step)).to(w.dtype).to(DEV)
+        popkv.append_popkv(back, new)
+        keys = torch.cat([keys, new], 1)
+        n = keys.shape[1]
+        want = core.pack_keys(f32(keys), token_group_size=w.token_group, dim_group_size=w.dim_group)
+        for a, b in zip(_packed_np(back), want):
+            assert np.array_equal(a[:, :n], b)

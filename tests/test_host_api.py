@@ -397,3 +397,70 @@ def test_batched_api_validation_before_the_device():
         step(q, cache, lengths, nk, nk, h2k, budget=4, max_tokens=5)
     with pytest.raises(RuntimeError, match="invalid score token count"):
         step(q, cache, lengths, nk, nk, h2k, budget=4, max_tokens=9)
+
+
+def _oracle_cache(tokens=150, tg=64, g=64, cap=256, seed=3, dtype=torch.bfloat16):
+    import numpy as np
+
+    from oracle import core
+
+    gen = torch.Generator().manual_seed(seed)
+    keys = torch.randn(2, tokens, 128, generator=gen).to(dtype)
+    ks, km, kl, kd = core.pack_keys(keys.float().numpy(), token_group_size=tg, dim_group_size=g)
+    planes = []
+    for a, dt in ((ks, torch.int32), (km, torch.int32), (kl, torch.float16), (kd, torch.float16)):
+        full = torch.zeros(2, cap, a.shape[2], dtype=dt)
+        src = torch.from_numpy(np.ascontiguousarray(a).view(np.int16 if dt == torch.float16 else np.int32))
+        full[:, :tokens] = src.view(dt)
+        planes.append(full)
+    sealed = tokens // tg * tg
+    return popkv.PopKVCache(tg, g, tokens, sealed, tuple(planes), keys[:, sealed:].clone())
+
+
+def test_packed_metadata_wire_round_trip_and_validation(tmp_path):
+    """The packed-metadata format (popkv_amd.wire): a cache encoded by the
+    oracle survives to_bytes / from_bytes and save / load bit for bit (rows
+    past token_count come back zero); corrupted, truncated, foreign and
+    inconsistent blobs are refused."""
+    from popkv_amd import wire
+
+    for tokens, tg, g, dtype in ((150, 64, 64, torch.bfloat16), (128, 128, 16, torch.float16),
+                                 (37, 32, 32, torch.float32), (0, 8, 32, torch.bfloat16)):
+        cache = _oracle_cache(tokens, tg, g, cap=256, dtype=dtype)
+        blob = wire.to_bytes(cache)
+        back = wire.from_bytes(blob)
+        assert (back.group_size, back.dim_group_size, back.token_count, back.sealed_tokens) == \
+            (tg, g, tokens, tokens // tg * tg)
+        for a, b in zip(back.packed, cache.packed):
+            assert a.dtype == b.dtype and a.shape == b.shape
+            assert torch.equal(a[:, :tokens].view(torch.int16 if a.dtype != torch.int32 else torch.int32),
+                               b[:, :tokens].view(torch.int16 if b.dtype != torch.int32 else torch.int32))
+            assert not a[:, tokens:].view(torch.int16 if a.dtype != torch.int32 else torch.int32).any()
+        assert back.active_keys.dtype == dtype and torch.equal(back.active_keys, cache.active_keys)
+        path = str(tmp_path / f"c{tokens}.pkv")
+        wire.save(cache, path)
+        assert wire.to_bytes(wire.load(path)) == blob
+    blob = bytearray(wire.to_bytes(_oracle_cache()))
+    bad = bytearray(blob)
+    bad[100] ^= 1
+    with pytest.raises(ValueError, match="checksum"):
+        wire.from_bytes(bytes(bad))
+    with pytest.raises(ValueError, match="magic"):
+        wire.from_bytes(b"NOTPOPKV" + bytes(blob[8:]))
+    with pytest.raises(ValueError):
+        wire.from_bytes(bytes(blob[:-40]))
+    cache = _oracle_cache()
+    with pytest.raises(ValueError, match="sealed_tokens"):
+        wire.validate(popkv.PopKVCache(64, 64, 150, 64, cache.packed, cache.active_keys))
+    with pytest.raises(ValueError, match="active_keys"):
+        wire.validate(popkv.PopKVCache(64, 64, 150, 128, cache.packed, cache.active_keys[:, :3]))
+    with pytest.raises(ValueError, match="k_low must be"):
+        wire.validate(popkv.PopKVCache(64, 64, 150, 128, (cache.packed[0], cache.packed[1],
+                                                           cache.packed[2][:, :, :1], cache.packed[3]),
+                                       cache.active_keys))
+    neg = cache.packed[3].clone()
+    neg[0, 5, 0] = -1.0
+    with pytest.raises(ValueError, match="delta must be non-negative"):
+        wire.validate(popkv.PopKVCache(64, 64, 150, 128, cache.packed[:3] + (neg,), cache.active_keys))
+    with pytest.raises(ValueError, match="token_count"):
+        wire.validate(popkv.PopKVCache(64, 64, 300, 256, cache.packed, torch.zeros(2, 44, 128)))
