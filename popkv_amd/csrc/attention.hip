@@ -66,8 +66,25 @@ __device__ __forceinline__ void merge_state(SoftmaxState& a, float m2, float l2,
 // Writes a workgroup's (m, l, acc[d]) to dst: the row slots of each wave
 // (lanes with equal dim slice) merge through shuffles, the waves through LDS.
 // All threads of the block call it.
+// Partial states handed from one workgroup to another inside a kernel (the
+// layer step's fused merge) are written and read as device-scope relaxed
+// atomics: plain global stores / loads with the device-coherence bit, which
+// go through to memory instead of staying in one XCD's L2, so no L2
+// write-back or invalidate is needed for them.
+template <bool COH>
+__device__ __forceinline__ void st_f32(float* p, float v) {
+    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <bool COH>
+__device__ __forceinline__ float ld_f32(const float* p) {
+    if constexpr (COH) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+
 template <int LPR>
-__device__ __forceinline__ void store_partial(SoftmaxState st, int lane, int wave, int dim0, int d, float* dst) {
+__device__ __forceinline__ void store_partial(SoftmaxState st, int lane, int wave, int dim0, int d, float* dst,
+                                              bool coherent = false) {
     auto merge_xor = [&](auto mtag) {
         constexpr int M = decltype(mtag)::value;
         const float m2 = lane_xor<M>(st.m);
@@ -100,8 +117,19 @@ __device__ __forceinline__ void store_partial(SoftmaxState st, int lane, int wav
         l += s_l[w] * wt;
         if (dim < d) a += s_acc[w][dim] * wt;
     }
-    if (dim < d) dst[2 + dim] = a;
-    if (dim == 0) { dst[0] = mx; dst[1] = l; }
+    if (coherent) {
+        if (dim < d) st_f32<true>(dst + 2 + dim, a);
+        if (dim == 0) {
+            st_f32<true>(dst, mx);
+            st_f32<true>(dst + 1, l);
+        }
+    } else {
+        if (dim < d) dst[2 + dim] = a;
+        if (dim == 0) {
+            dst[0] = mx;
+            dst[1] = l;
+        }
+    }
 }
 
 // Merge `nsplit` states [(m, l, acc[D])] of one head into out[0..D).  The
@@ -344,6 +372,116 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
 }
 
 
+// Split states a merge loads in its first burst (and per batch after it).
+constexpr int kMergeFirst = 16;
+
+// Row of current_k / current_v for merge block h, and (for a batched step)
+// the row's current-token index and its slot k in the indices: sequence b =
+// h / q_heads has min(tokens[b], bound) cached tokens (*current holds the
+// launch bound on entry).  Unbatched: KV head head_to_kv[h] (clamped), or
+// h / (QH / KVH) without a mapping (the dense layers).
+__device__ __forceinline__ int64_t merge_kv_row(const SeqTable& seq, const int64_t* __restrict__ head_to_kv, int h,
+                                                int kv_heads, int rows, int64_t* idx_slot, int64_t* current) {
+    if (seq.tokens != nullptr) {
+        const int64_t b = h / seq.q_heads;
+        *current = seq_tokens_of(seq, b, *current);
+        *idx_slot = min(static_cast<int64_t>(seq.budget) - 1, *current);
+        return b * seq.kv_heads +
+               min(max(head_to_kv[h - b * seq.q_heads], static_cast<int64_t>(0)), static_cast<int64_t>(seq.kv_heads - 1));
+    }
+    return head_to_kv != nullptr ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
+                                 : h / (rows / kv_heads);
+}
+
+// Merge of one head by one wave (lane l owning dims l and l + 64): the
+// head's nsplit states ps[s] = (m, l, acc[128]) plus the current token
+// (logit qh . ck * scale, value cv), written to outh in the query dtype.
+// No LDS or barrier: the split maxima and denominators are wave reductions
+// (lane s holds split s of each 64-split group), and the weights reach the
+// accumulation through readlane.  qh, ck, cv, the first group's maxima and
+// denominators and the first kMergeFirst splits' accumulators are loaded in
+// one burst, so a layer step's merge pays one memory latency for all of
+// them; further splits follow in batches of kMergeFirst.  Accumulation
+// order: the current token, then the splits in ascending order.  COH: the
+// states are read with device-coherent loads (written by other workgroups
+// of the same kernel).
+template <typename T, bool COH>
+__device__ __forceinline__ void merge_head(const float* __restrict__ ps, int nsplit, const T* __restrict__ qh,
+                                           const T* __restrict__ ck, const T* __restrict__ cv, float scale,
+                                           T* __restrict__ outh) {
+    constexpr int S = 128 + 2;
+    const int lane = threadIdx.x & (kWave - 1);
+    // the burst (with nsplit == 0 the accumulator loads read split 0's slot,
+    // which every workspace holds, and are not used)
+    const float q0 = Elem<T>::load(qh, lane), q1 = Elem<T>::load(qh, lane + 64);
+    const float k0 = Elem<T>::load(ck, lane), k1 = Elem<T>::load(ck, lane + 64);
+    const float v0 = Elem<T>::load(cv, lane), v1 = Elem<T>::load(cv, lane + 64);
+    float m0 = -INFINITY, l0 = 0.0f;  // split `lane`
+    if (lane < nsplit) {
+        m0 = ld_f32<COH>(ps + (static_cast<int64_t>(lane) * S));
+        l0 = ld_f32<COH>(ps + (static_cast<int64_t>(lane) * S + 1));
+    }
+    const int nf = min(nsplit, kMergeFirst);
+    float a0[kMergeFirst], a1[kMergeFirst];
+#pragma unroll
+    for (int j = 0; j < kMergeFirst; ++j) {
+        const int64_t so = static_cast<int64_t>(max(min(j, nf - 1), 0)) * S + 2;
+        a0[j] = ld_f32<COH>(ps + (so + lane));
+        a1[j] = ld_f32<COH>(ps + (so + lane + 64));
+    }
+    // the maxima of every split and the current token's logit
+    float mx = m0;
+    for (int s0 = kWave; s0 < nsplit; s0 += kWave)
+        if (s0 + lane < nsplit) mx = fmaxf(mx, ld_f32<COH>(ps + (static_cast<int64_t>(s0 + lane) * S)));
+    const float cur_m = wave_sum(q0 * k0 + q1 * k1) * scale;
+    mx = fmaxf(wave_max(mx), cur_m);
+    const float wc = __expf(cur_m - mx);
+    const float w0 = m0 == -INFINITY ? 0.0f : __expf(m0 - mx);
+    float den = l0 * w0, num0 = wc * v0, num1 = wc * v1;
+#pragma unroll
+    for (int j = 0; j < kMergeFirst; ++j) {
+        if (j < nf) {
+            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w0), j));
+            num0 = fmaf(ws, a0[j], num0);
+            num1 = fmaf(ws, a1[j], num1);
+        }
+    }
+    for (int s0 = 0; s0 < nsplit; s0 += kWave) {
+        float w = w0;
+        if (s0 > 0) {
+            float m = -INFINITY, l = 0.0f;
+            if (s0 + lane < nsplit) {
+                m = ld_f32<COH>(ps + (static_cast<int64_t>(s0 + lane) * S));
+                l = ld_f32<COH>(ps + (static_cast<int64_t>(s0 + lane) * S + 1));
+            }
+            w = m == -INFINITY ? 0.0f : __expf(m - mx);
+            den += l * w;
+        }
+        const int n = min(kWave, nsplit - s0);
+        for (int b = s0 == 0 ? nf : 0; b < n; b += kMergeFirst) {
+            float c0[kMergeFirst], c1[kMergeFirst];
+#pragma unroll
+            for (int j = 0; j < kMergeFirst; ++j) {
+                const int64_t so = static_cast<int64_t>(s0 + min(b + j, n - 1)) * S + 2;
+                c0[j] = ld_f32<COH>(ps + (so + lane));
+                c1[j] = ld_f32<COH>(ps + (so + lane + 64));
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeFirst; ++j) {
+                if (b + j < n) {
+                    const float ws =
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b + j));
+                    num0 = fmaf(ws, c0[j], num0);
+                    num1 = fmaf(ws, c1[j], num1);
+                }
+            }
+        }
+    }
+    den = wave_sum(den) + wc;
+    Elem<T>::store(outh, lane, num0 / den);
+    Elem<T>::store(outh, lane + 64, num1 / den);
+}
+
 // ---------------------------------------------------------------- layer step
 
 // Layer-step attention.  Row slot q of a workgroup (16 lanes, one 16-byte
@@ -471,7 +609,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
     const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
     uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
-    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq) {
+    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq,
+    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
     constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
     constexpr int CH = kChunkThreads * KPT;
@@ -546,11 +685,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
             }
         }
     }
+    const bool fused = out != nullptr;  // the merge runs in the head's last block (see the end)
     if constexpr (SEQ) {
         if (c >= nch) {  // past this sequence's tokens: an empty state (the merge weighs it 0)
-            if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
+            if (c == 0 && (tid > 0 || !fused)) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
             float* dst = partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2);
             if (tid < D + 2) dst[tid] = tid == 0 ? -INFINITY : 0.0f;
+            if (fused && c == 0 && wave == 0) {
+                // an empty sequence: no chunk takes a ticket, and the merge
+                // is the current token alone
+                const int64_t kvh = min(max(map, static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+                const int64_t crow = (b * seq.kv_heads + kvh) * D;
+                if (idx_out != nullptr && lane == 0) idx_out[static_cast<int64_t>(h) * idx_stride + k] = ntok;
+                merge_head<T, false>(dst, 0, q + static_cast<int64_t>(h) * D, cur_k + crow, cur_v + crow, scale,
+                                     out + static_cast<int64_t>(h) * D);
+            }
             return;
         }
     }
@@ -635,7 +784,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
         s_g2[tid] = g2;
         s_p2[tid] = p2;
     }
-    if (c == 0) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
+    // (bin 0 -- which no real key reaches -- holds the fused merge's ticket)
+    if (c == 0 && (tid > 0 || !fused)) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
     __syncthreads();
 
     // 3. T from the chunk histograms; the block's list: the tokens above bin
@@ -714,7 +864,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
         issue(s_list, base + slot * NB, n_list, CH);
         fold_rows<T, NB>(st, qr, kr, vr, live, scale);
     }
-    store_partial<LPR>(st, lane, wave, dim0, D, partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2));
+    float* const pdst = partials + (static_cast<int64_t>(h) * nchunks + c) * (D + 2);
+    store_partial<LPR>(st, lane, wave, dim0, D, pdst, fused);
+    if (!fused) return;
+    // 5. fused merge: the state went out with device-coherent stores; once
+    //    every thread's stores are acknowledged the block takes a ticket
+    //    (ghist[h][0], zero between calls), and the head's last block --
+    //    which sees every other chunk's stores -- merges the chunks and the
+    //    current token, resets the ticket and writes the output (one wave).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    const uint32_t parts = static_cast<uint32_t>(SEQ ? max(nch, 1) : nchunks);
+    if (tid == 0) {
+        const uint32_t old =
+            __hip_atomic_fetch_add(&ghist[static_cast<int64_t>(h) * 256], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old + 1u == parts ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last == 0u || wave != 0) return;
+    if (lane == 0) {
+        __hip_atomic_store(&ghist[static_cast<int64_t>(h) * 256], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (idx_out != nullptr) idx_out[static_cast<int64_t>(h) * idx_stride + k] = ntok;
+    }
+    const int64_t crow = ((SEQ ? b * seq.kv_heads : 0) + kvh) * D;
+    merge_head<T, true>(partials + static_cast<int64_t>(h) * nchunks * (D + 2), static_cast<int>(parts),
+                        q + static_cast<int64_t>(h) * D, cur_k + crow, cur_v + crow, scale,
+                        out + static_cast<int64_t>(h) * D);
 }
 
 // Dense attention (the reference's full layers, popkv.py:1022-1038): every
@@ -920,37 +1096,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_mfma_kernel(
     }
 }
 
-// Layer-step merge: the split states of head h plus the current token
-// (logit q.cur_k * scale, value cur_v), written in the query dtype.  One
-// wave per head, lane l owning dims l and l + 64, and no LDS or barrier:
-// the split maxima and denominators are wave reductions (lane s holds split
-// s of each 64-split group), and the weights reach the accumulation through
-// readlane.  q, cur_k, cur_v, the first group's maxima and denominators and
-// the first kMergeFirst splits' accumulators are loaded in one burst, so a
-// layer step's merge (at most 64 chunks, 16 at C1) pays one memory latency
-// for all of them; further splits (dense layers) follow in batches of
-// kMergeFirst.  Accumulation order: the current token, then the splits in
-// ascending order.
-constexpr int kMergeFirst = 16;
 
-// Row of current_k / current_v for merge block h, and (for a batched step)
-// the row's current-token index and its slot k in the indices: sequence b =
-// h / q_heads has min(tokens[b], bound) cached tokens (*current holds the
-// launch bound on entry).  Unbatched: KV head head_to_kv[h] (clamped), or
-// h / (QH / KVH) without a mapping (the dense layers).
-__device__ __forceinline__ int64_t merge_kv_row(const SeqTable& seq, const int64_t* __restrict__ head_to_kv, int h,
-                                                int kv_heads, int64_t* idx_slot, int64_t* current) {
-    if (seq.tokens != nullptr) {
-        const int64_t b = h / seq.q_heads;
-        *current = seq_tokens_of(seq, b, *current);
-        *idx_slot = min(static_cast<int64_t>(seq.budget) - 1, *current);
-        return b * seq.kv_heads +
-               min(max(head_to_kv[h - b * seq.q_heads], static_cast<int64_t>(0)), static_cast<int64_t>(seq.kv_heads - 1));
-    }
-    return head_to_kv != nullptr ? min(max(head_to_kv[h], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1))
-                                 : h / (static_cast<int>(gridDim.x) / kv_heads);
-}
-
+// Layer-step merge kernel (the unfused form: popkv_layer_step_attention's
+// timing runs, and the dense layers): one wave per head, see merge_head.
 template <typename T>
 __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     const float* __restrict__ partials, int nsplit, const T* __restrict__ q, const T* __restrict__ cur_k,
@@ -963,81 +1111,10 @@ __global__ __launch_bounds__(kWave) void attn_merge_current_kernel(
     // the current token's index slot of the layer step's int64 indices, and
     // the KV row of its current k/v (no mapping: the plain GQA grouping of
     // the dense layers)
-    const int64_t kvh = merge_kv_row(seq, head_to_kv, h, kv_heads, &idx_slot, &current);
+    const int64_t kvh = merge_kv_row(seq, head_to_kv, h, kv_heads, gridDim.x, &idx_slot, &current);
     if (idx_out != nullptr && lane == 0) idx_out[static_cast<int64_t>(h) * idx_stride + idx_slot] = current;
-    const float* ps = partials + static_cast<int64_t>(h) * nsplit * S;
-    const T* qh = q + static_cast<int64_t>(h) * D;
-    const T* ck = cur_k + kvh * D;
-    const T* cv = cur_v + kvh * D;
-    // the burst (with nsplit == 0 the accumulator loads read split 0's slot,
-    // which every workspace holds, and are not used)
-    const float q0 = Elem<T>::load(qh, lane), q1 = Elem<T>::load(qh, lane + 64);
-    const float k0 = Elem<T>::load(ck, lane), k1 = Elem<T>::load(ck, lane + 64);
-    const float v0 = Elem<T>::load(cv, lane), v1 = Elem<T>::load(cv, lane + 64);
-    float m0 = -INFINITY, l0 = 0.0f;  // split `lane`
-    if (lane < nsplit) {
-        m0 = ps[static_cast<int64_t>(lane) * S];
-        l0 = ps[static_cast<int64_t>(lane) * S + 1];
-    }
-    const int nf = min(nsplit, kMergeFirst);
-    float a0[kMergeFirst], a1[kMergeFirst];
-#pragma unroll
-    for (int j = 0; j < kMergeFirst; ++j) {
-        const int64_t so = static_cast<int64_t>(max(min(j, nf - 1), 0)) * S + 2;
-        a0[j] = ps[so + lane];
-        a1[j] = ps[so + lane + 64];
-    }
-    // the maxima of every split and the current token's logit
-    float mx = m0;
-    for (int s0 = kWave; s0 < nsplit; s0 += kWave)
-        if (s0 + lane < nsplit) mx = fmaxf(mx, ps[static_cast<int64_t>(s0 + lane) * S]);
-    const float cur_m = wave_sum(q0 * k0 + q1 * k1) * scale;
-    mx = fmaxf(wave_max(mx), cur_m);
-    const float wc = __expf(cur_m - mx);
-    const float w0 = m0 == -INFINITY ? 0.0f : __expf(m0 - mx);
-    float den = l0 * w0, num0 = wc * v0, num1 = wc * v1;
-#pragma unroll
-    for (int j = 0; j < kMergeFirst; ++j) {
-        if (j < nf) {
-            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w0), j));
-            num0 = fmaf(ws, a0[j], num0);
-            num1 = fmaf(ws, a1[j], num1);
-        }
-    }
-    for (int s0 = 0; s0 < nsplit; s0 += kWave) {
-        float w = w0;
-        if (s0 > 0) {
-            float m = -INFINITY, l = 0.0f;
-            if (s0 + lane < nsplit) {
-                m = ps[static_cast<int64_t>(s0 + lane) * S];
-                l = ps[static_cast<int64_t>(s0 + lane) * S + 1];
-            }
-            w = m == -INFINITY ? 0.0f : __expf(m - mx);
-            den += l * w;
-        }
-        const int n = min(kWave, nsplit - s0);
-        for (int b = s0 == 0 ? nf : 0; b < n; b += kMergeFirst) {
-            float c0[kMergeFirst], c1[kMergeFirst];
-#pragma unroll
-            for (int j = 0; j < kMergeFirst; ++j) {
-                const int64_t so = static_cast<int64_t>(s0 + min(b + j, n - 1)) * S + 2;
-                c0[j] = ps[so + lane];
-                c1[j] = ps[so + lane + 64];
-            }
-#pragma unroll
-            for (int j = 0; j < kMergeFirst; ++j) {
-                if (b + j < n) {
-                    const float ws =
-                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b + j));
-                    num0 = fmaf(ws, c0[j], num0);
-                    num1 = fmaf(ws, c1[j], num1);
-                }
-            }
-        }
-    }
-    den = wave_sum(den) + wc;
-    Elem<T>::store(out + static_cast<int64_t>(h) * D, lane, num0 / den);
-    Elem<T>::store(out + static_cast<int64_t>(h) * D, lane + 64, num1 / den);
+    merge_head<T, false>(partials + static_cast<int64_t>(h) * nsplit * S, nsplit, q + static_cast<int64_t>(h) * D,
+                         cur_k + kvh * D, cur_v + kvh * D, scale, out + static_cast<int64_t>(h) * D);
 }
 
 // Merge for many splits (dense layers: one split per 512 tokens): four
@@ -1057,7 +1134,7 @@ __global__ __launch_bounds__(kWave * kMergeWaves) void attn_merge_wide_kernel(
     const int h = blockIdx.x;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int64_t kvh = merge_kv_row(seq, head_to_kv, h, kv_heads, &idx_slot, &current);
+    const int64_t kvh = merge_kv_row(seq, head_to_kv, h, kv_heads, gridDim.x, &idx_slot, &current);
     if (idx_out != nullptr && threadIdx.x == 0) idx_out[static_cast<int64_t>(h) * idx_stride + idx_slot] = current;
     const float* ps = partials + static_cast<int64_t>(h) * nsplit * S;
     float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
@@ -1358,7 +1435,8 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
                                   const uint16_t* keys, int64_t key_stride, int64_t tokens, int64_t k,
                                   const uint32_t* rec, const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                   const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
-                                  int64_t idx_stride, const SeqTable& seq, hipStream_t stream) {
+                                  int64_t idx_stride, const SeqTable& seq, const void* cur_k, const void* cur_v,
+                                  void* out, hipStream_t stream) {
     // 10 rows per slot and pass: 160 per pass, so a chunk holding up to 320
     // selected tokens (C1: 204-294 in chunks of 2048) is gathered in two
     // passes.  Measured at C1, select + attention: 8 rows 16.5 us (three
@@ -1377,16 +1455,18 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
     const int kv_clamp = batched ? seq.kv_heads : kv_heads;
     const dim3 grid(static_cast<unsigned>(ch.count * q_heads));
     const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
+    const T *ck_ = static_cast<const T*>(cur_k), *cv_ = static_cast<const T*>(cur_v);
+    T* o_ = static_cast<T*>(out);
 #define POPKV_SC(KPT)                                                                                            \
     case KPT:                                                                                                    \
         if (batched)                                                                                             \
             hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, true>), grid, dim3(kAttnThreads), 0, stream, \
                                q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
-                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq);                  \
+                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_);    \
         else                                                                                                     \
             hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, false>), grid, dim3(kAttnThreads), 0, stream, \
                                q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
-                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq);                  \
+                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_);    \
         break
     switch (ch.kpt) {
         POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
@@ -1422,21 +1502,25 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                           int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
+                                          const void* current_k, const void* current_v, void* output,
                                           hipStream_t stream) {
     if (tokens <= 0 || q_heads <= 0) return hipSuccess;
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_select_chunks_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
-                                                 kv_heads, partials, idx_out, idx_stride, seq, stream);
+                                                 kv_heads, partials, idx_out, idx_stride, seq, current_k,
+                                                 current_v, output, stream);
         case POPKV_DTYPE_F16:
             return launch_select_chunks_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
-                                                 kv_heads, partials, idx_out, idx_stride, seq, stream);
+                                                 kv_heads, partials, idx_out, idx_stride, seq, current_k,
+                                                 current_v, output, stream);
         default:
             return launch_select_chunks_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                   key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
-                                                  kv_heads, partials, idx_out, idx_stride, seq, stream);
+                                                  kv_heads, partials, idx_out, idx_stride, seq, current_k,
+                                                 current_v, output, stream);
     }
 }
 

@@ -387,22 +387,17 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     if (st) return clear_hist(st);
     // 3. per (chunk, head): the chunk's selected tokens (also written as
     //    int64 at their rank when indices_out is given) and the sparse
-    //    attention over them (re-zeroes the histograms),
-    // 4. log-sum-exp merge of the chunks and the current token (whose index
-    //    goes to slot k)
+    //    attention over them (re-zeroes the histograms); the head's last
+    //    chunk to finish does
+    // 4. the log-sum-exp merge of the chunks and the current token (whose
+    //    index goes to slot k)
     st = launched(popkv::launch_attention_select_chunks(queries, dtype, prefix_k, prefix_v, k_head_stride,
                                                         v_head_stride, keys, L.score_stride, tokens, L.k, rec, h2,
                                                         gt1, hist, head_to_kv, static_cast<int>(q_heads),
                                                         static_cast<int>(kv_heads), partials, indices_out, L.k + 1,
-                                                        popkv::SeqTable{}, s),
-                  "popkv_layer_step(select + attention)");
+                                                        popkv::SeqTable{}, current_k, current_v, output, s),
+                  "popkv_layer_step(select + attention + merge)");
     if (st) return clear_hist(st);
-    st = launched(popkv::launch_merge_current(partials, static_cast<int>(L.nchunks), queries, dtype, current_k,
-                                              current_v, head_to_kv, static_cast<int>(q_heads),
-                                              static_cast<int>(kv_heads), output, indices_out, L.k + 1, L.k, tokens,
-                                              popkv::SeqTable{}, s),
-                  "popkv_layer_step(merge)");
-    if (st) return st;
     return POPKV_OK;
 }
 
@@ -513,14 +508,10 @@ int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* 
                                                         cache_rows * 128, keys, L.score_stride, max_tokens, L.k, rec,
                                                         h2, gt1, hist, head_to_kv, static_cast<int>(rows),
                                                         static_cast<int>(kv_heads), partials, indices_out,
-                                                        index_row_stride, seq, s),
-                  "popkv_layer_step_batched(select + attention)");
+                                                        index_row_stride, seq, current_k, current_v, output, s),
+                  "popkv_layer_step_batched(select + attention + merge)");
     if (st) return clear_hist(st);
-    return launched(popkv::launch_merge_current(partials, static_cast<int>(L.nchunks), queries, dtype, current_k,
-                                                current_v, head_to_kv, static_cast<int>(rows),
-                                                static_cast<int>(kv_heads), output, indices_out, index_row_stride,
-                                                L.k, max_tokens, seq, s),
-                    "popkv_layer_step_batched(merge)");
+    return POPKV_OK;
 }
 
 int popkv_append(const void* new_k, const void* new_v, int32_t dtype, void* key_cache, void* value_cache,
@@ -570,7 +561,8 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* p
                         reinterpret_cast<const uint32_t*>(ws + L.rec), reinterpret_cast<const uint16_t*>(ws + L.h2),
                         reinterpret_cast<const uint32_t*>(ws + L.gt1), reinterpret_cast<uint32_t*>(ws + L.hist),
                         head_to_kv, static_cast<int>(q_heads), static_cast<int>(kv_heads),
-                        reinterpret_cast<float*>(ws + L.partials), nullptr, 0, popkv::SeqTable{}, as_stream(stream)),
+                        reinterpret_cast<float*>(ws + L.partials), nullptr, 0, popkv::SeqTable{}, nullptr, nullptr,
+                        nullptr, as_stream(stream)),
                     "popkv_layer_step_attention");
 }
 

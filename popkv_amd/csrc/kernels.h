@@ -113,7 +113,10 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
 // then selects, per (chunk, head), the chunk's tokens among the row's k
 // largest keys (lowest index first among ties), attends over them into
 // partials[head][chunk][130], writes them as int64 to idx_out[head][rank]
-// when idx_out is non-null, and re-zeroes ghist.
+// when idx_out is non-null, and re-zeroes ghist.  With output non-null the
+// merge is fused: the last workgroup of each head merges its chunks with
+// the current token (current_k / current_v) into output (and writes the
+// current token's index), so no merge launch follows.
 hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t rows, int64_t tokens, int64_t k,
                              const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, const SeqTable& seq,
                              hipStream_t stream);
@@ -123,6 +126,7 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                           int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
+                                          const void* current_k, const void* current_v, void* output,
                                           hipStream_t stream);
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.

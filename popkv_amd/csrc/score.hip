@@ -476,7 +476,10 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
                 const uint32_t b = bits;
                 const uint32_t sgn = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(b), 15, 1));
                 const uint32_t key = sc != sc ? 0xffffu : b ^ (sgn | 0x8000u);
-                *dst = static_cast<uint16_t>(key);
+                // written through to memory (a device-coherent store): the
+                // kernel then ends with little dirty data in L2, and its
+                // end-of-kernel write-back is shorter (C1 step 28.2 -> 27.7 us)
+                __hip_atomic_store(dst, static_cast<uint16_t>(key), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 atomicAdd(&s_hist[h][(key >> 8) & 0xffu], 1u);
             } else {
                 *dst = bits;
