@@ -648,9 +648,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     Raw8<T> qr;
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
     const int64_t map = head_to_kv[hl + z];
+    int64_t seq_ntok = ntok;
+    if constexpr (SEQ) seq_ntok = seq_tokens_of(seq, b, ntok);
+    uint32_t rank0 = 0;
+    uint32_t g2 = 0, p2 = 0;  // bin tid of the chunk histograms over every chunk / over chunks before c
+    // The threshold record, bin tid of the first HB chunk histograms and
+    // (lane l) the keys above bin b1 in chunk l -- every chunk: a step has at
+    // most 64 -- are loaded whatever the mode (the workspace always holds
+    // them; unused values are ignored).  With every path issuing the same
+    // loads in the same order, the waits for the keys, the record and the
+    // mapping before the first gather pass count exactly and leave these in
+    // flight, and the histograms are summed only once that pass is out (step
+    // 2).  Measured at C1: a wait for every load before the pass -- what
+    // loads on mode-dependent paths compile to -- sent it out about 3 us
+    // later.
+    constexpr int HB = 16;
+    const uint32_t b1 = rec[4 * h + z], above1 = rec[4 * h + 1 + z];
+    const uint16_t* hr = h2 + static_cast<int64_t>(h) * nchunks * 256 + tid;
+    uint32_t hv[HB];
+#pragma unroll
+    for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(j, nchunks - 1)) * 256];
+    const uint32_t gx = gt1[static_cast<int64_t>(h) * nchunks + min(lane, nchunks - 1)];
     int nch = nchunks;  // this row's chunks
     if constexpr (SEQ) {
-        ntok = static_cast<int>(seq_tokens_of(seq, b, ntok));
+        ntok = static_cast<int>(seq_ntok);
         k = min(seq.budget - 1, ntok);
         nch = (ntok + CH - 1) / CH;
     }
@@ -660,31 +681,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
     __shared__ uint32_t s_g2[256], s_p2[256];
     __shared__ uint32_t s_scan1[kAttnWaves], s_scan2[kAttnWaves];
     __shared__ __align__(16) uint16_t s_list[CH];
-    uint32_t b1 = 0, above1 = 0, rank0 = 0;
-    uint32_t g2 = 0, p2 = 0;  // bin tid of the chunk histograms over every chunk / over chunks before c
-    uint32_t gt1_before = 0;  // keys above bin b1 in earlier chunks
-    if (SEQ || mode == 2) {
-        b1 = rec[4 * h + z];
-        above1 = rec[4 * h + 1 + z];
-        const uint16_t* hr = h2 + static_cast<int64_t>(h) * nchunks * 256 + tid;
-        for (int c0 = 0; c0 < nchunks; c0 += 16) {
-            uint32_t v[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = hr[static_cast<int64_t>(min(c0 + j, nchunks - 1)) * 256];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const uint32_t x = c0 + j < nch ? v[j] : 0u;
-                g2 += x;
-                p2 += c0 + j < c ? x : 0u;
-            }
-        }
-        if (idx_out != nullptr) {
-            for (int c0 = 0; c0 < c; c0 += kWave) {
-                const uint32_t x = c0 + lane < c ? gt1[static_cast<int64_t>(h) * nchunks + c0 + lane] : 0u;
-                gt1_before += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
-            }
-        }
-    }
     const bool fused = out != nullptr;  // the merge runs in the head's last block (see the end)
     if constexpr (SEQ) {
         if (c >= nch) {  // past this sequence's tokens: an empty state (the merge weighs it 0)
@@ -779,7 +775,31 @@ __global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
             vr[b].load(reinterpret_cast<const T*>(vb + off));
         }
     };
-    if (wfirst > 0) issue(s_wlist[wave], (slot % SLOTS) * NB, wfirst, WCAP);
+    // (issued in every block, all rows dead when the wave listed none, so
+    // that the sums below wait for the histograms alone)
+    issue(s_wlist[wave], (slot % SLOTS) * NB, wfirst, WCAP);
+    // (and the sums stay behind the pass: the scheduler would otherwise
+    // hoist some of them, with their waits, above its loads)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < HB; ++j) {
+        const uint32_t x = j < nch ? hv[j] : 0u;
+        g2 += x;
+        p2 += j < c ? x : 0u;
+    }
+    for (int c0 = HB; c0 < nch; c0 += HB) {  // steps of more than HB chunks (large budgets)
+#pragma unroll
+        for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(c0 + j, nchunks - 1)) * 256];
+#pragma unroll
+        for (int j = 0; j < HB; ++j) {
+            const uint32_t x = c0 + j < nch ? hv[j] : 0u;
+            g2 += x;
+            p2 += c0 + j < c ? x : 0u;
+        }
+    }
+    // keys above bin b1 in earlier chunks
+    const uint32_t gt1_before = static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(lane < c ? gx : 0u, lane)), kWave - 1));
     if (mode == 2) {
         s_g2[tid] = g2;
         s_p2[tid] = p2;

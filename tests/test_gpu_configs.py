@@ -263,3 +263,25 @@ def test_packed_metadata_hand_off_through_the_wire_format():
         want = core.pack_keys(f32(keys), token_group_size=w.token_group, dim_group_size=w.dim_group)
         for a, b in zip(_packed_np(back), want):
             assert np.array_equal(a[:, :n], b)
+
+
+@pytest.mark.parametrize("g", [16, 32, 64])
+def test_permuted_head_mapping(g):
+    """A head_to_kv that is not the plain grouping (group j reads KV head
+    7 - j): the scorer reads the mapped rows, and the scores, indices and
+    attention follow the mapping exactly as the oracle does."""
+    base = workloads.scaled(workloads.C1, context=5000, budget=700)
+    w = workloads.Workload(base.name, base.method, 32, 8, 128, 5000, 700, 64 if g == 64 else 128, g,
+                           torch.bfloat16, 31 + g, True)
+    layer, _, cache = _setup(w)
+    mapping = (7 - torch.arange(32, device=DEV) // 4).to(torch.int64)
+    sc, idx, out = _oracle(w, layer, mapping, cache)
+    enc = popkv_cuda.query_encode(layer.queries.unsqueeze(0).contiguous(), dim_group_size=g)
+    scores = popkv_cuda.score_encoded(enc, cache.packed, head_to_kv=mapping, tokens=layer.prefix_tokens,
+                                      dim_group_size=g)
+    assert np.array_equal(bits(scores[0]), sc)
+    o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(got.cpu().numpy(), idx)
+    _assert_attention(o, out)
+
