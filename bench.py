@@ -159,11 +159,13 @@ def bench_c4(args) -> int:
     """C4: a batch of 8 independent sequences x 64K context (PopKV-S, budget
     4096, bf16), each with its own static K/V cache [8, 8, rows, 128] and
     packed metadata [8, 8, capacity, .] (popkv_amd.batch).  A step is one
-    layer's decode step for the whole batch in two C-ABI calls: the batched
-    layer step (encode, score, top-k + current, split attention, merge;
-    every sequence at its own device-side length) and the fused append
-    (the new token's K/V rows into the static caches and the re-encode of
-    each sequence's active token group, read in place).  The replays repeat
+    layer's decode step for the whole batch in one C-ABI call
+    (popkv_decode_layer_batched): the batched layer step (encode, score,
+    top-k + current, split attention, merge; every sequence at its own
+    device-side length) and the fused append (the new token's K/V rows into
+    the static caches and the re-encode of each sequence's active token
+    group, read in place), the append running beside the step's select and
+    attention on a second stream.  The replays repeat
     the same token position (the lengths are not advanced inside the timed
     graph; advancing them is one 8-element add per decode step, not per
     layer).  The one-time prepack of the eight 64K prefixes is timed on its
@@ -203,8 +205,7 @@ def bench_c4(args) -> int:
     def step(i: int) -> None:
         cache, lengths, out = sets[i % n_sets]
         pb.popkv_layer_step_batched(q, cache, lengths, cur_k, cur_v, mapping, budget=w.budget, workspace=ws,
-                                    out=out)
-        pb.append_batched(cache, lengths, cur_k, cur_v)
+                                    out=out, append=True)
 
     def prepack(i: int) -> None:
         cache, lengths, _ = sets[i % n_sets]

@@ -244,6 +244,27 @@ int popkv_append(const void* new_k, const void* new_v, int32_t dtype,
                  const int64_t* token_counts, int64_t batch, int64_t kv_heads,
                  int32_t token_group_size, int32_t dim_group_size, int32_t* status, void* stream);
 
+/* One layer of a batched decode step: popkv_layer_step_batched followed by
+ * popkv_append of the current token (new_k/new_v = current_k/current_v,
+ * token_group_size, status as for popkv_append), with the same results as
+ * the two calls in that order, in three kernels instead of four: the
+ * append runs in extra workgroups of the select + attention launch, beside
+ * the selection and the attention (neither reads what the append writes:
+ * the static caches' rows at the counts, the active groups' packed rows).
+ * No counterpart in the reference: it replaces, for one layer, the
+ * reference decode loop's retrieval step and append (popkv.py:1076-1115
+ * with :438-459 / :883-942 and the static cache write of :964-972) for a
+ * batch. */
+int popkv_decode_layer_batched(const void* queries, int32_t dtype,
+                               int32_t* k_sign, int32_t* k_mag, void* k_low, void* k_delta,
+                               int64_t capacity, void* key_cache, void* value_cache, int64_t cache_rows,
+                               const void* current_k, const void* current_v,
+                               const int64_t* head_to_kv, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                               const int64_t* token_counts, int64_t max_tokens, int64_t budget,
+                               int32_t dim_group_size, int32_t token_group_size, void* output,
+                               int64_t* indices_out, int64_t index_row_stride, int32_t* status,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free form of popkv_layer_step: the same kernels and results,
  * with the workspace taken from a library-owned device array of
  * POPKV_LAYER_STEP_SCRATCH_BYTES per GPU (a file-scope __device__ array,

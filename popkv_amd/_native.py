@@ -56,6 +56,9 @@ _SIGNATURES = {
     "popkv_layer_step_batched": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _vp,
                                                 _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _vp, _vp,
                                                 _c_i64, _vp, _c_size, _vp]),
+    "popkv_decode_layer_batched": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _vp,
+                                                  _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
+                                                  _vp, _vp, _c_i64, _vp, _vp, _c_size, _vp]),
     "popkv_append": (ctypes.c_int, [_vp, _vp, _c_i32, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64,
                                     _c_i64, _c_i32, _c_i32, _vp, _vp]),
     "popkv_layer_step_scratch_bytes": (_c_size, []),

@@ -177,7 +177,8 @@ def append_batched(cache: BatchedPopKVCache, lengths: SequenceLengths, new_k: to
 def popkv_layer_step_batched(q: torch.Tensor, cache: BatchedPopKVCache, lengths: SequenceLengths,
                              k: torch.Tensor, v: torch.Tensor, head_to_kv: torch.Tensor, *, budget: int,
                              max_tokens: int | None = None, workspace: LayerStepWorkspace | None = None,
-                             out: torch.Tensor | None = None, return_indices: bool = False):
+                             out: torch.Tensor | None = None, return_indices: bool = False,
+                             append: bool = False, status: torch.Tensor | None = None):
     """The retrieval step of one sparse layer for every sequence of the
     batch (q [B, QH, 128], current k/v [B, KVH, 128], head_to_kv [QH]):
     sequence b scores its lengths[b] cached tokens, selects
@@ -186,7 +187,13 @@ def popkv_layer_step_batched(q: torch.Tensor, cache: BatchedPopKVCache, lengths:
     device lengths for the launch -- give the largest length a captured
     graph will see.  Returns out [B, QH, 128] (and int64 indices
     [B, QH, min(budget - 1, max_tokens) + 1] whose row (b, h) holds
-    k_b + 1 valid entries, the current token last)."""
+    k_b + 1 valid entries, the current token last).
+
+    ``append=True`` also appends the current token (k, v) to the layer's
+    caches, with the results of ``append_batched(cache, lengths, k, v,
+    status=status)`` after the step, in one C-ABI call
+    (popkv_decode_layer_batched) whose append runs in extra workgroups of
+    the step's select + attention launch."""
     batch, kv_heads = (int(x) for x in cache.key_cache.shape[:2])
     if q.ndim != 3 or int(q.shape[0]) != batch or int(q.shape[2]) != 128:
         raise ValueError(f"q must be [{batch}, query heads, 128]")
@@ -209,6 +216,11 @@ def popkv_layer_step_batched(q: torch.Tensor, cache: BatchedPopKVCache, lengths:
         raise RuntimeError("invalid score token count")
     if out is not None and (tuple(out.shape) != tuple(q.shape) or not out.is_contiguous() or out.dtype != q.dtype):
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    if append:
+        if max(lengths.host) >= min(cache.capacity, int(cache.packed[0].shape[2])):
+            raise RuntimeError("Pop-KV cache reserve exhausted")
+        if status is not None and (status.dtype != torch.int32 or not status.is_cuda):
+            raise ValueError("status must be a CUDA int32 tensor")
     dev = q.device
     if any(t.dtype != q.dtype for t in (k, v, cache.key_cache)):
         raise RuntimeError("queries, current K/V and the static caches must share a dtype")
@@ -222,9 +234,17 @@ def popkv_layer_step_batched(q: torch.Tensor, cache: BatchedPopKVCache, lengths:
     idx = torch.full((batch, q_heads, kk + 1), -1, device=dev, dtype=torch.int64) if return_indices else None
     ks, km, kl, kd = cache.packed
     with torch.cuda.device(dev):
-        nat.call("popkv_layer_step_batched", qc.data_ptr(), nat.dtype_code(qc), ks.data_ptr(), km.data_ptr(),
-                 kl.data_ptr(), kd.data_ptr(), int(ks.shape[2]), cache.key_cache.data_ptr(),
-                 cache.value_cache.data_ptr(), cache.capacity, kc.data_ptr(), vc.data_ptr(), mapping.data_ptr(),
-                 batch, q_heads, kv_heads, lengths.device.data_ptr(), bound, int(budget), g, output.data_ptr(),
-                 nat.ptr(idx), kk + 1, ws.data_ptr(), ws.numel(), nat.stream_of(dev))
+        if append:
+            nat.call("popkv_decode_layer_batched", qc.data_ptr(), nat.dtype_code(qc), ks.data_ptr(), km.data_ptr(),
+                     kl.data_ptr(), kd.data_ptr(), int(ks.shape[2]), cache.key_cache.data_ptr(),
+                     cache.value_cache.data_ptr(), cache.capacity, kc.data_ptr(), vc.data_ptr(), mapping.data_ptr(),
+                     batch, q_heads, kv_heads, lengths.device.data_ptr(), bound, int(budget), g, cache.group_size,
+                     output.data_ptr(), nat.ptr(idx), kk + 1, nat.ptr(status), ws.data_ptr(), ws.numel(),
+                     nat.stream_of(dev))
+        else:
+            nat.call("popkv_layer_step_batched", qc.data_ptr(), nat.dtype_code(qc), ks.data_ptr(), km.data_ptr(),
+                     kl.data_ptr(), kd.data_ptr(), int(ks.shape[2]), cache.key_cache.data_ptr(),
+                     cache.value_cache.data_ptr(), cache.capacity, kc.data_ptr(), vc.data_ptr(), mapping.data_ptr(),
+                     batch, q_heads, kv_heads, lengths.device.data_ptr(), bound, int(budget), g, output.data_ptr(),
+                     nat.ptr(idx), kk + 1, ws.data_ptr(), ws.numel(), nat.stream_of(dev))
     return (output, idx) if return_indices else output

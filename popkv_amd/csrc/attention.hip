@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "device_common.h"
+#include "pack128.h"
 #include "kernels.h"
 #include "select_common.h"
 
@@ -579,6 +580,21 @@ __device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk
     }
 }
 
+// The current token's append in a batched decode step's select + attention
+// launch: workgroups 0 .. blocks - 1 run pack128_append for (sequence, KV
+// head) blockIdx.x < batch * kv_heads (blocks is rounded up to a multiple of
+// 8 so that the select + attention workgroups keep their XCD placement).
+template <typename T>
+struct StepAppendArgs {
+    AppendArgs<T> ap;
+    int32_t* k_sign = nullptr;
+    int32_t* k_mag = nullptr;
+    uint16_t* k_low = nullptr;
+    uint16_t* k_delta = nullptr;
+    int64_t cap = 0;
+    int tg = 1, g = 64, blocks = 0, items = 0;
+};
+
 // Layer step: the select's second half fused with the sparse attention.
 // Block (c, h) owns chunk c of head h's key row (kChunkThreads * KPT tokens,
 // KPT per thread).  The selection is every key > T plus the lowest-index
@@ -603,21 +619,47 @@ __device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk
 // Block 0 of each head re-zeroes the scorer's histogram ghist[h] (its last
 // reader, chunk_hist_kernel, has finished).  The grid is one-dimensional
 // (chunk_head_of_block).
+// (The batched form also carries the decode step's append code; asked for
+// three waves per SIMD, it keeps the residency of the plain step -- 168
+// VGPRs at bf16 against 200 unconstrained.  Measured at C4: 161.2 us per step
+// with the append in this launch, 167.9 with a separate append launch.)
 template <typename T, int KPT, int NB, bool SEQ>
-__global__ __launch_bounds__(kAttnThreads) void attn_select_chunk_kernel(
+__global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
     const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
     uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
     float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq,
-    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out) {
+    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out, StepAppendArgs<T> apx) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
+    int block = static_cast<int>(blockIdx.x);
+    if constexpr (SEQ) {
+        // The decode step's append: nothing below reads what it writes (the
+        // static caches' rows at the counts -- the select reads the rows
+        // below them, the current K/V come from cur_k / cur_v -- and the
+        // active groups' packed rows, which only the scorer read).
+        if (block < apx.blocks) {
+            __shared__ float s_app[kPack128Lds];
+            if (block >= apx.items) return;
+            if (apx.g == 16)
+                pack128_append<T, 16>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta, apx.cap,
+                                      s_app);
+            else if (apx.g == 32)
+                pack128_append<T, 32>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta, apx.cap,
+                                      s_app);
+            else
+                pack128_append<T, 64>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta, apx.cap,
+                                      s_app);
+            return;
+        }
+        block -= apx.blocks;
+    }
     constexpr int D = 128, LPR = 16, SLOTS = kWave / LPR, NSLOT = SLOTS * kAttnWaves;
     constexpr int CH = kChunkThreads * KPT;
     constexpr int PASS = NSLOT * NB;  // entries per pass
     static_assert(NB % 2 == 0, "a slot's entries of one pass are whole 32-bit LDS words");
     int c, h;
-    chunk_head_of_block(static_cast<int>(blockIdx.x), nchunks, qpk, kv_groups, &c, &h);
+    chunk_head_of_block(block, nchunks, qpk, kv_groups, &c, &h);
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -1456,7 +1498,7 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
                                   const uint32_t* rec, const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                   const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
                                   int64_t idx_stride, const SeqTable& seq, const void* cur_k, const void* cur_v,
-                                  void* out, hipStream_t stream) {
+                                  void* out, hipStream_t stream, const DecodeAppend* app) {
     // 10 rows per slot and pass: 160 per pass, so a chunk holding up to 320
     // selected tokens (C1: 204-294 in chunks of 2048) is gathered in two
     // passes.  Measured at C1, select + attention: 8 rows 16.5 us (three
@@ -1473,7 +1515,27 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
     const bool groups = kv_all % 8 == 0 && (batched || q_heads % kv_heads == 0);
     const int qpk = groups ? qpk_all : 1;
     const int kv_clamp = batched ? seq.kv_heads : kv_heads;
-    const dim3 grid(static_cast<unsigned>(ch.count * q_heads));
+    StepAppendArgs<T> apx;
+    if (app != nullptr && batched) {
+        apx.ap.new_k = static_cast<const T*>(app->new_k);
+        apx.ap.new_v = static_cast<const T*>(app->new_v);
+        apx.ap.key_cache = static_cast<T*>(app->key_cache);
+        apx.ap.value_cache = static_cast<T*>(app->value_cache);
+        apx.ap.cache_rows = app->cache_rows;
+        apx.ap.counts = seq.tokens;
+        apx.ap.kv_heads = seq.kv_heads;
+        apx.ap.status = app->status;
+        apx.k_sign = app->k_sign;
+        apx.k_mag = app->k_mag;
+        apx.k_low = app->k_low;
+        apx.k_delta = app->k_delta;
+        apx.cap = app->capacity;
+        apx.tg = app->token_group_size;
+        apx.g = app->dim_group_size;
+        apx.items = (q_heads / seq.q_heads) * seq.kv_heads;
+        apx.blocks = (apx.items + 7) / 8 * 8;
+    }
+    const dim3 grid(static_cast<unsigned>(ch.count * q_heads + apx.blocks));
     const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
     const T *ck_ = static_cast<const T*>(cur_k), *cv_ = static_cast<const T*>(cur_v);
     T* o_ = static_cast<T*>(out);
@@ -1482,11 +1544,11 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
         if (batched)                                                                                             \
             hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, true>), grid, dim3(kAttnThreads), 0, stream, \
                                q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
-                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_);    \
+                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_, apx); \
         else                                                                                                     \
             hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, false>), grid, dim3(kAttnThreads), 0, stream, \
                                q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
-                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_);    \
+                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_, apx); \
         break
     switch (ch.kpt) {
         POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
@@ -1523,24 +1585,24 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                           int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
                                           const void* current_k, const void* current_v, void* output,
-                                          hipStream_t stream) {
+                                          hipStream_t stream, const DecodeAppend* append) {
     if (tokens <= 0 || q_heads <= 0) return hipSuccess;
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_select_chunks_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
                                                  kv_heads, partials, idx_out, idx_stride, seq, current_k,
-                                                 current_v, output, stream);
+                                                 current_v, output, stream, append);
         case POPKV_DTYPE_F16:
             return launch_select_chunks_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
                                                  kv_heads, partials, idx_out, idx_stride, seq, current_k,
-                                                 current_v, output, stream);
+                                                 current_v, output, stream, append);
         default:
             return launch_select_chunks_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                   key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
                                                   kv_heads, partials, idx_out, idx_stride, seq, current_k,
-                                                 current_v, output, stream);
+                                                 current_v, output, stream, append);
     }
 }
 

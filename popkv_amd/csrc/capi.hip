@@ -445,13 +445,26 @@ size_t popkv_layer_step_batched_workspace_bytes(int64_t batch, int64_t q_heads, 
     return step_layout(batch * q_heads, max_tokens, budget).total;
 }
 
-int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
-                             const void* k_low, const void* k_delta, int64_t capacity, const void* key_cache,
-                             const void* value_cache, int64_t cache_rows, const void* current_k,
-                             const void* current_v, const int64_t* head_to_kv, int64_t batch, int64_t q_heads,
-                             int64_t kv_heads, const int64_t* token_counts, int64_t max_tokens, int64_t budget,
-                             int32_t dim_group_size, void* output, int64_t* indices_out, int64_t index_row_stride,
-                             void* workspace, size_t workspace_bytes, void* stream) {
+// The current token's append in a decode step (popkv_decode_layer_batched).
+struct StepAppend {
+    int32_t token_group_size;
+    int32_t* status;
+};
+
+// popkv_layer_step_batched, and with `app` the decode step: the append runs
+// in extra workgroups of the select + attention launch.  Neither that
+// kernel nor the chunk-histogram kernel before it reads what the append
+// writes: the static caches' rows at the sequences' counts (the select
+// reads rows below them; the current K/V come from current_k / current_v)
+// and the active groups' packed rows (read by the scorer, which has
+// finished).
+static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                            const void* k_low, const void* k_delta, int64_t capacity, const void* key_cache,
+                            const void* value_cache, int64_t cache_rows, const void* current_k,
+                            const void* current_v, const int64_t* head_to_kv, int64_t batch, int64_t q_heads,
+                            int64_t kv_heads, const int64_t* token_counts, int64_t max_tokens, int64_t budget,
+                            int32_t dim_group_size, void* output, int64_t* indices_out, int64_t index_row_stride,
+                            void* workspace, size_t workspace_bytes, const StepAppend* app, void* stream) {
     if (!queries || !k_sign || !k_mag || !k_low || !k_delta || !key_cache || !value_cache || !current_k ||
         !current_v || !head_to_kv || !token_counts || !output)
         return fail(POPKV_ERR_INVALID, "null pointer");
@@ -474,6 +487,25 @@ int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* 
         !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(current_k) || !aligned16(current_v) ||
         (cache_rows * 128 * static_cast<int64_t>(es)) % 16)
         return fail(POPKV_ERR_UNSUPPORTED, "batched layer step tensors need 16-byte alignment");
+    if (app && (app->token_group_size < 1 || app->token_group_size > 4096))
+        return fail(POPKV_ERR_INVALID, "token_group_size must be between 1 and 4096");
+    if (app && batch * kv_heads > 0x7fffffff) return fail(POPKV_ERR_INVALID, "bad batch or KV head count");
+    popkv::DecodeAppend dapp{};
+    if (app) {
+        dapp.new_k = current_k;
+        dapp.new_v = current_v;
+        dapp.key_cache = const_cast<void*>(key_cache);
+        dapp.value_cache = const_cast<void*>(value_cache);
+        dapp.cache_rows = cache_rows;
+        dapp.status = app->status;
+        dapp.k_sign = const_cast<int32_t*>(k_sign);
+        dapp.k_mag = const_cast<int32_t*>(k_mag);
+        dapp.k_low = static_cast<uint16_t*>(const_cast<void*>(k_low));
+        dapp.k_delta = static_cast<uint16_t*>(const_cast<void*>(k_delta));
+        dapp.capacity = capacity;
+        dapp.token_group_size = app->token_group_size;
+        dapp.dim_group_size = dim_group_size;
+    }
     popkv::SeqTable seq;
     seq.tokens = token_counts;
     seq.cache_rows = kv_heads * capacity;
@@ -489,7 +521,7 @@ int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* 
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
     hipStream_t s = as_stream(stream);
-    // the same four kernels as popkv_layer_step, every row at its own
+    // the same three kernels as popkv_layer_step, every row at its own
     // sequence's token count (see popkv::SeqTable)
     st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
                                                static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
@@ -508,10 +540,40 @@ int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* 
                                                         cache_rows * 128, keys, L.score_stride, max_tokens, L.k, rec,
                                                         h2, gt1, hist, head_to_kv, static_cast<int>(rows),
                                                         static_cast<int>(kv_heads), partials, indices_out,
-                                                        index_row_stride, seq, current_k, current_v, output, s),
-                  "popkv_layer_step_batched(select + attention + merge)");
+                                                        index_row_stride, seq, current_k, current_v, output, s,
+                                                        app ? &dapp : nullptr),
+                  app ? "popkv_decode_layer_batched(select + attention + merge + append)"
+                      : "popkv_layer_step_batched(select + attention + merge)");
     if (st) return clear_hist(st);
     return POPKV_OK;
+}
+
+int popkv_layer_step_batched(const void* queries, int32_t dtype, const int32_t* k_sign, const int32_t* k_mag,
+                             const void* k_low, const void* k_delta, int64_t capacity, const void* key_cache,
+                             const void* value_cache, int64_t cache_rows, const void* current_k,
+                             const void* current_v, const int64_t* head_to_kv, int64_t batch, int64_t q_heads,
+                             int64_t kv_heads, const int64_t* token_counts, int64_t max_tokens, int64_t budget,
+                             int32_t dim_group_size, void* output, int64_t* indices_out, int64_t index_row_stride,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    return batched_step_run(queries, dtype, k_sign, k_mag, k_low, k_delta, capacity, key_cache, value_cache,
+                            cache_rows, current_k, current_v, head_to_kv, batch, q_heads, kv_heads, token_counts,
+                            max_tokens, budget, dim_group_size, output, indices_out, index_row_stride, workspace,
+                            workspace_bytes, nullptr, stream);
+}
+
+int popkv_decode_layer_batched(const void* queries, int32_t dtype, int32_t* k_sign, int32_t* k_mag, void* k_low,
+                               void* k_delta, int64_t capacity, void* key_cache, void* value_cache,
+                               int64_t cache_rows, const void* current_k, const void* current_v,
+                               const int64_t* head_to_kv, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                               const int64_t* token_counts, int64_t max_tokens, int64_t budget,
+                               int32_t dim_group_size, int32_t token_group_size, void* output, int64_t* indices_out,
+                               int64_t index_row_stride, int32_t* status, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+    const StepAppend app{token_group_size, status};
+    return batched_step_run(queries, dtype, k_sign, k_mag, k_low, k_delta, capacity, key_cache, value_cache,
+                            cache_rows, current_k, current_v, head_to_kv, batch, q_heads, kv_heads, token_counts,
+                            max_tokens, budget, dim_group_size, output, indices_out, index_row_stride, workspace,
+                            workspace_bytes, &app, stream);
 }
 
 int popkv_append(const void* new_k, const void* new_v, int32_t dtype, void* key_cache, void* value_cache,

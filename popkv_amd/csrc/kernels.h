@@ -120,6 +120,23 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
 hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t rows, int64_t tokens, int64_t k,
                              const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, const SeqTable& seq,
                              hipStream_t stream);
+// The current token's append run inside a batched step's select + attention
+// launch (popkv_decode_layer_batched): the operands of popkv_append.
+struct DecodeAppend {
+    const void* new_k;
+    const void* new_v;
+    void* key_cache;
+    void* value_cache;
+    int64_t cache_rows;
+    int32_t* status;
+    int32_t* k_sign;
+    int32_t* k_mag;
+    uint16_t* k_low;
+    uint16_t* k_delta;
+    int64_t capacity;
+    int token_group_size;
+    int dim_group_size;
+};
 hipError_t launch_attention_select_chunks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                           int64_t k_head_stride, int64_t v_head_stride, const uint16_t* keys,
                                           int64_t key_stride, int64_t tokens, int64_t k, const uint32_t* rec,
@@ -127,7 +144,7 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                           int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
                                           const void* current_k, const void* current_v, void* output,
-                                          hipStream_t stream);
+                                          hipStream_t stream, const DecodeAppend* append = nullptr);
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
 // Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one

@@ -262,3 +262,82 @@ def test_c4_batch_after_an_append():
         for a, wp in zip(_packed_np(cache, b), want_pack):
             assert np.array_equal(a[:, :L], wp), b
     _check_batch(q, cache, lengths, cur_k, cur_v, mapping, w.budget, out, idx, check=(0, 7))
+
+
+def test_decode_layer_equals_step_then_append():
+    """popkv_decode_layer_batched (the step with append=True: the append in
+    extra workgroups of the select + attention launch) gives the same
+    output, indices, static caches and packed planes as the layer step
+    followed by append_batched -- eagerly, and in a HIP graph captured once
+    and replayed while the sequences grow (each replay checked against the
+    oracle at its own lengths)."""
+    starts = [3000, 1499, 2200]
+    batch, qh, kvh, rows, budget, g, tg = 3, 32, 8, 3100, 512, 64, 64
+    keys, values = _seq_data(batch, kvh, rows, seed=29)
+    mapping = torch.arange(qh, device=DEV) // (qh // kvh)
+
+    def fresh():
+        kc = torch.zeros(batch, kvh, rows, 128, dtype=torch.bfloat16, device=DEV)
+        vc = torch.zeros_like(kc)
+        for b, n in enumerate(starts):
+            kc[b, :, :n] = keys[b, :, :n].to(DEV)
+            vc[b, :, :n] = values[b, :, :n].to(DEV)
+        lengths = pb.SequenceLengths.create(starts, DEV)
+        return pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g), lengths
+
+    gq = torch.Generator().manual_seed(5)
+    q = torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+    ck = torch.stack([keys[b, :, starts[b]] for b in range(batch)]).to(DEV)
+    cv = torch.stack([values[b, :, starts[b]] for b in range(batch)]).to(DEV)
+    ca, la = fresh()
+    o1, i1 = pb.popkv_layer_step_batched(q, ca, la, ck, cv, mapping, budget=budget, return_indices=True)
+    pb.append_batched(ca, la, ck, cv)
+    cb, lb = fresh()
+    o2, i2 = pb.popkv_layer_step_batched(q, cb, lb, ck, cv, mapping, budget=budget, return_indices=True,
+                                         append=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(i1, i2)
+    assert torch.equal(ca.key_cache, cb.key_cache) and torch.equal(ca.value_cache, cb.value_cache)
+    for x, y in zip(ca.packed, cb.packed):
+        assert torch.equal(x, y)
+
+    # captured once, replayed with new tokens while the lengths grow
+    cache, lengths = fresh()
+    ws = pb.LayerStepWorkspace()
+    out = torch.empty_like(q)
+    idx = torch.empty(batch, qh, budget, dtype=torch.int64, device=DEV)
+    bound = max(starts) + 8
+
+    def step():
+        _, i = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, max_tokens=bound,
+                                           workspace=ws, out=out, return_indices=True, append=True)
+        idx.copy_(i)
+        lengths.device.add_(1)
+
+    def next_token():
+        q.copy_(torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16))
+        ck.copy_(torch.stack([keys[b, :, lengths.host[b]] for b in range(batch)]))
+        cv.copy_(torch.stack([values[b, :, lengths.host[b]] for b in range(batch)]))
+
+    next_token()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    lengths.host = [x + 1 for x in lengths.host]
+    graph = torch.cuda.CUDAGraph()
+    next_token()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    assert lengths.device.cpu().tolist() == lengths.host
+    for _ in range(3):
+        next_token()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _check_batch(q, cache, lengths, ck, cv, mapping, budget, out, idx)
+        lengths.host = [x + 1 for x in lengths.host]
+        assert lengths.device.cpu().tolist() == lengths.host
