@@ -620,9 +620,9 @@ struct StepAppendArgs {
 // reader, chunk_hist_kernel, has finished).  The grid is one-dimensional
 // (chunk_head_of_block).
 // (The batched form also carries the decode step's append code; asked for
-// three waves per SIMD, it keeps the residency of the plain step -- 168
-// VGPRs at bf16 against 200 unconstrained.  Measured at C4: 161.2 us per step
-// with the append in this launch, 167.9 with a separate append launch.)
+// three waves per SIMD it keeps the residency of the plain step: 142 VGPRs
+// at bf16.  Measured at C4: 160.4 us per step with the append in this
+// launch, 167.9 with a separate append launch.)
 template <typename T, int KPT, int NB, bool SEQ>
 __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
@@ -639,17 +639,16 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
         // below them, the current K/V come from cur_k / cur_v -- and the
         // active groups' packed rows, which only the scorer read).
         if (block < apx.blocks) {
-            __shared__ float s_app[kPack128Lds];
             if (block >= apx.items) return;
             if (apx.g == 16)
-                pack128_append<T, 16>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta, apx.cap,
-                                      s_app);
+                pack128_append<T, 16, true>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta,
+                                            apx.cap);
             else if (apx.g == 32)
-                pack128_append<T, 32>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta, apx.cap,
-                                      s_app);
+                pack128_append<T, 32, true>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta,
+                                            apx.cap);
             else
-                pack128_append<T, 64>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta, apx.cap,
-                                      s_app);
+                pack128_append<T, 64, true>(block, apx.ap, apx.tg, apx.k_sign, apx.k_mag, apx.k_low, apx.k_delta,
+                                            apx.cap);
             return;
         }
         block -= apx.blocks;

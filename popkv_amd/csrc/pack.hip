@@ -201,16 +201,15 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     constexpr int D = 128;
     static_assert(2 * D * static_cast<int>(sizeof(T)) / 16 <= kWave * pack128_waves<G>(),
                   "one 16-byte slice of the new K/V rows per thread");
-    __shared__ float s_lds[kPack128Lds];
     if constexpr (!APPEND) {
         const int64_t kvh = blockIdx.y;
         const int64_t gs = static_cast<int64_t>(blockIdx.x) * tg;
         const int n = static_cast<int>(min(gs + static_cast<int64_t>(tg), tokens) - gs);
         const T* base = keys + kvh * head_stride + gs * D;
         auto row_of = [&](int t) -> const T* { return base + static_cast<int64_t>(t) * D; };
-        pack128_group<T, G>(row_of, n, kvh * cap + offset + gs, k_sign, k_mag, k_low, k_delta, s_lds);
+        pack128_group<T, G>(row_of, n, kvh * cap + offset + gs, k_sign, k_mag, k_low, k_delta);
     } else {
-        pack128_append<T, G>(blockIdx.x, ap, tg, k_sign, k_mag, k_low, k_delta, cap, s_lds);
+        pack128_append<T, G>(blockIdx.x, ap, tg, k_sign, k_mag, k_low, k_delta, cap);
     }
 }
 

@@ -53,10 +53,6 @@ struct AppendArgs {
     int32_t* status = nullptr;
 };
 
-// LDS floats pack128_group needs: per-wave extrema of NW <= 4 waves and the
-// two threshold rows.
-constexpr int kPack128Lds = (2 * 4 + 2) * 128;
-
 // Encodes one token group (head_dim 128) into packed rows orow0 + t:
 //   Phase 1 -- lane l owns dims 2l and 2l+1; the waves stream interleaved
 //              rows of the group with coalesced loads, keeping
@@ -66,21 +62,19 @@ constexpr int kPack128Lds = (2 * 4 + 2) * 128;
 //              dimensions: the sign/magnitude words and the representatives,
 //              reduced in registers in the production tree order (G64 pairs
 //              dims j and j+32 first).
-// Rows come from row_of(t), t < n.  `lds` holds kPack128Lds floats.  Every
-// thread of the workgroup calls it; a workgroup wider than
-// pack128_waves<G>() waves has its extra waves join the barriers only.
-template <typename T, int G, typename RowOf>
+// Rows come from row_of(t), t < n.  Every thread of the workgroup calls it;
+// the workgroup has pack128_waves<G>() waves, or (WIDE) more, whose extra
+// waves join the barriers only.
+template <typename T, int G, bool WIDE = false, typename RowOf>
 __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_t orow0,
                                               int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
-                                              uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta,
-                                              float* lds) {
+                                              uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta) {
     constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
-    static_assert(NW <= 4, "kPack128Lds holds four waves' extrema");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     // Phase 1: extrema of dims 2*lane, 2*lane+1; wave w takes tokens w, w+NW, ...
     float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
-    for (int t0 = wave; wave < NW && t0 < n; t0 += PH1 * NW) {
+    for (int t0 = wave; (!WIDE || wave < NW) && t0 < n; t0 += PH1 * NW) {
         float a[PH1], b[PH1];
 #pragma unroll
         for (int i = 0; i < PH1; ++i) {
@@ -93,21 +87,19 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
             mn1 = fminf(mn1, b[i]); mx1 = fmaxf(mx1, b[i]);
         }
     }
-    float* const s_mn = lds;            // [NW][D]
-    float* const s_mx = lds + NW * D;   // [NW][D]
-    float* const s_hi = lds + 2 * NW * D;  // 0.5*max
-    float* const s_nlo = s_hi + D;      // -(0.5*min)
-    if (wave < NW) {
-        s_mn[wave * D + 2 * lane] = mn0; s_mn[wave * D + 2 * lane + 1] = mn1;
-        s_mx[wave * D + 2 * lane] = mx0; s_mx[wave * D + 2 * lane + 1] = mx1;
+    __shared__ float s_mn[NW][D], s_mx[NW][D];
+    __shared__ float s_hi[D], s_nlo[D];  // 0.5*max and -(0.5*min)
+    if (!WIDE || wave < NW) {
+        s_mn[wave][2 * lane] = mn0; s_mn[wave][2 * lane + 1] = mn1;
+        s_mx[wave][2 * lane] = mx0; s_mx[wave][2 * lane + 1] = mx1;
     }
     __syncthreads();
     if (threadIdx.x < D) {
-        float mn = s_mn[threadIdx.x], mx = s_mx[threadIdx.x];
+        float mn = s_mn[0][threadIdx.x], mx = s_mx[0][threadIdx.x];
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
-            mn = fminf(mn, s_mn[w * D + threadIdx.x]);
-            mx = fmaxf(mx, s_mx[w * D + threadIdx.x]);
+            mn = fminf(mn, s_mn[w][threadIdx.x]);
+            mx = fmaxf(mx, s_mx[w][threadIdx.x]);
         }
         s_nlo[threadIdx.x] = -(mn * 0.5f);
         s_hi[threadIdx.x] = mx * 0.5f;
@@ -120,7 +112,7 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
     // shifted in from the top (w = 2w + bit); |v| goes to the low or the high
     // bucket.  G64 adds dims j and j+32 (its two plane words) before the
     // halving tree; G32 / G16 reduce within one word.
-    if (wave >= NW) return;  // (a wider workgroup's other waves: no dimensions)
+    if (WIDE && wave >= NW) return;  // (a wider workgroup's other waves: no dimensions)
     const int c0 = wave * CH;
     if constexpr (G == 64) {
         // G64: wave w owns rep w (dims c0 .. c0+63, plane words 2w, 2w+1).
@@ -277,13 +269,13 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
 // place from the static key cache, then the new key itself, sealed = count -
 // count % tg -- and the whole group is re-encoded into packed rows sealed ..
 // count; the new K/V rows are written to the static caches.  Every thread
-// of a workgroup of at least max(pack128_waves<G>(), 2 * D * sizeof(T) /
-// 16 / 64) waves calls it.
-template <typename T, int G>
+// of a workgroup of max(pack128_waves<G>(), 2 * D * sizeof(T) / 16 / 64)
+// waves (or, WIDE, more) calls it.
+template <typename T, int G, bool WIDE = false>
 __device__ __forceinline__ void pack128_append(int64_t bh, const AppendArgs<T>& ap, int tg,
                                                int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
                                                uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta,
-                                               int64_t cap, float* lds) {
+                                               int64_t cap) {
     constexpr int D = 128;
     const int64_t count = ap.counts[bh / ap.kv_heads];
     if (count < 0 || count >= ap.cache_rows || count >= cap) {
@@ -305,7 +297,7 @@ __device__ __forceinline__ void pack128_append(int64_t bh, const AppendArgs<T>& 
     const T* base = ap.key_cache + (bh * ap.cache_rows + sealed) * D;
     const T* last = ap.new_k + bh * D;
     auto row_of = [&](int t) -> const T* { return t == n - 1 ? last : base + static_cast<int64_t>(t) * D; };
-    pack128_group<T, G>(row_of, n, bh * cap + sealed, k_sign, k_mag, k_low, k_delta, lds);
+    pack128_group<T, G, WIDE>(row_of, n, bh * cap + sealed, k_sign, k_mag, k_low, k_delta);
 }
 
 }  // namespace popkv
