@@ -53,6 +53,33 @@ struct AppendArgs {
     int32_t* status = nullptr;
 };
 
+// One dimension of the encode for this lane's token: the sign bit (v >= 0)
+// and the magnitude bit m = (v > hi) | (v < lo) shifted into ws / wm from
+// the bottom (w = 2w + bit: one add with the compare's lane mask as the
+// carry-in), and |v| into the low bucket xl (m = 0) or the high bucket xh
+// (m = 1), the other bucket 0.  The masks live in SGPRs written and read
+// only inside this block, ordered so that each VALU read of an SGPR comes
+// at least two instructions after the VALU write of it (gfx950's wait
+// states for a VALU-written SGPR read by VALU, which the compiler does not
+// insert into inline assembly), and the block ends with two instructions
+// that write no SGPR.
+__device__ __forceinline__ void encode_dim(float v, float hi, float lo, uint32_t& ws, uint32_t& wm, float& xl,
+                                           float& xh) {
+    uint64_t ms, m1, m2, carry;
+    asm volatile(
+        "v_cmp_le_f32_e64 %[ms], 0, %[v]\n\t"
+        "v_cmp_gt_f32_e64 %[m1], %[v], %[hi]\n\t"
+        "v_cmp_lt_f32_e64 %[m2], %[v], %[lo]\n\t"
+        "v_addc_co_u32_e64 %[ws], %[carry], %[ws], %[ws], %[ms]\n\t"
+        "s_or_b64 %[m1], %[m1], %[m2]\n\t"
+        "v_addc_co_u32_e64 %[wm], %[carry], %[wm], %[wm], %[m1]\n\t"
+        "v_cndmask_b32_e64 %[xl], |%[v]|, 0, %[m1]\n\t"
+        "v_cndmask_b32_e64 %[xh], 0, |%[v]|, %[m1]"
+        : [ws] "+v"(ws), [wm] "+v"(wm), [xl] "=&v"(xl), [xh] "=&v"(xh), [ms] "=&s"(ms), [m1] "=&s"(m1),
+          [m2] "=&s"(m2), [carry] "=&s"(carry)
+        : [v] "v"(v), [hi] "v"(hi), [lo] "v"(lo));
+}
+
 // Encodes one token group (head_dim 128) into packed rows orow0 + t:
 //   Phase 1 -- lane l owns dims 2l and 2l+1; the waves stream interleaved
 //              rows of the group with coalesced loads, keeping
@@ -72,46 +99,102 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
     constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    // Phase 1: extrema of dims 2*lane, 2*lane+1; wave w takes tokens w, w+NW, ...
-    float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
-    for (int t0 = wave; (!WIDE || wave < NW) && t0 < n; t0 += PH1 * NW) {
-        float a[PH1], b[PH1];
+    __shared__ __align__(16) float s_hi[D], s_lo[D];  // 0.5*max and 0.5*min, read four at a time
+    if constexpr (!WIDE) {
+        // Phase 1: lane l reads dims d8 .. d8+7 (16 bytes) of row slot
+        // l / 16, so one load covers four rows; in each pass of 64 rows wave
+        // w reads the row quads w, w + NW, ... (rows past n repeat row n-1:
+        // min/max unchanged).  The 4*NW partial extrema of a dimension meet
+        // in LDS.
+        constexpr int QW = 16 / NW;
+        const int sub = lane >> 4, d8 = 8 * (lane & 15);
+        float mn[8], mx[8];
 #pragma unroll
-        for (int i = 0; i < PH1; ++i) {
-            const int t = min(t0 + i * NW, n - 1);  // repeats the last row: min/max unchanged
-            load2<T>(row_of(t) + 2 * lane, a[i], b[i]);
-        }
+        for (int e = 0; e < 8; ++e) { mn[e] = INFINITY; mx[e] = -INFINITY; }
+        for (int r0 = 0; r0 < n; r0 += 64) {
+            Raw8<T> raw[QW];
+            if (r0 + 64 <= n) {
 #pragma unroll
-        for (int i = 0; i < PH1; ++i) {
-            mn0 = fminf(mn0, a[i]); mx0 = fmaxf(mx0, a[i]);
-            mn1 = fminf(mn1, b[i]); mx1 = fmaxf(mx1, b[i]);
-        }
-    }
-    __shared__ float s_mn[NW][D], s_mx[NW][D];
-    __shared__ float s_hi[D], s_nlo[D];  // 0.5*max and -(0.5*min)
-    if (!WIDE || wave < NW) {
-        s_mn[wave][2 * lane] = mn0; s_mn[wave][2 * lane + 1] = mn1;
-        s_mx[wave][2 * lane] = mx0; s_mx[wave][2 * lane + 1] = mx1;
-    }
-    __syncthreads();
-    if (threadIdx.x < D) {
-        float mn = s_mn[0][threadIdx.x], mx = s_mx[0][threadIdx.x];
+                for (int k = 0; k < QW; ++k) raw[k].load(row_of(r0 + 4 * (wave + NW * k) + sub) + d8);
+            } else {
 #pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            mn = fminf(mn, s_mn[w][threadIdx.x]);
-            mx = fmaxf(mx, s_mx[w][threadIdx.x]);
+                for (int k = 0; k < QW; ++k) raw[k].load(row_of(min(r0 + 4 * (wave + NW * k) + sub, n - 1)) + d8);
+            }
+#pragma unroll
+            for (int k = 0; k < QW; ++k) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    mn[e] = fminf(mn[e], raw[k].get(e));
+                    mx[e] = fmaxf(mx[e], raw[k].get(e));
+                }
+            }
         }
-        s_nlo[threadIdx.x] = -(mn * 0.5f);
-        s_hi[threadIdx.x] = mx * 0.5f;
+        __shared__ __align__(16) float s_mn[4 * NW][D], s_mx[4 * NW][D];
+        float4* pn = reinterpret_cast<float4*>(&s_mn[4 * wave + sub][d8]);
+        float4* px = reinterpret_cast<float4*>(&s_mx[4 * wave + sub][d8]);
+        pn[0] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+        pn[1] = make_float4(mn[4], mn[5], mn[6], mn[7]);
+        px[0] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+        px[1] = make_float4(mx[4], mx[5], mx[6], mx[7]);
+        __syncthreads();
+        if (threadIdx.x < D) {
+            float lo = s_mn[0][threadIdx.x], hi = s_mx[0][threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < 4 * NW; ++w) {
+                lo = fminf(lo, s_mn[w][threadIdx.x]);
+                hi = fmaxf(hi, s_mx[w][threadIdx.x]);
+            }
+            s_lo[threadIdx.x] = lo * 0.5f;
+            s_hi[threadIdx.x] = hi * 0.5f;
+        }
+    } else {
+        // Phase 1 (a wider workgroup, one group per call): extrema of dims
+        // 2*lane, 2*lane+1; wave w < NW takes tokens w, w+NW, ...
+        float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
+        for (int t0 = wave; wave < NW && t0 < n; t0 += PH1 * NW) {
+            float a[PH1], b[PH1];
+#pragma unroll
+            for (int i = 0; i < PH1; ++i) {
+                const int t = min(t0 + i * NW, n - 1);  // repeats the last row: min/max unchanged
+                load2<T>(row_of(t) + 2 * lane, a[i], b[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < PH1; ++i) {
+                mn0 = fminf(mn0, a[i]); mx0 = fmaxf(mx0, a[i]);
+                mn1 = fminf(mn1, b[i]); mx1 = fmaxf(mx1, b[i]);
+            }
+        }
+        __shared__ float s_mn[NW][D], s_mx[NW][D];
+        if (wave < NW) {
+            s_mn[wave][2 * lane] = mn0; s_mn[wave][2 * lane + 1] = mn1;
+            s_mx[wave][2 * lane] = mx0; s_mx[wave][2 * lane + 1] = mx1;
+        }
+        __syncthreads();
+        if (threadIdx.x < D) {
+            float mn = s_mn[0][threadIdx.x], mx = s_mx[0][threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                mn = fminf(mn, s_mn[w][threadIdx.x]);
+                mx = fmaxf(mx, s_mx[w][threadIdx.x]);
+            }
+            s_lo[threadIdx.x] = mn * 0.5f;
+            s_hi[threadIdx.x] = mx * 0.5f;
+        }
     }
     __syncthreads();
 
     // Phase 2: wave w encodes dims [w*CH, w*CH + CH) of one token per lane,
     // one 32-dimension plane word at a time.  Per dimension: sign
-    // s = v >= 0, magnitude m = s ? v > hi : v < lo; the word bits are
-    // shifted in from the top (w = 2w + bit); |v| goes to the low or the high
-    // bucket.  G64 adds dims j and j+32 (its two plane words) before the
-    // halving tree; G32 / G16 reduce within one word.
+    // s = v >= 0, magnitude m = s ? |v| > hi : |v| > -lo; the word bits are
+    // shifted in from the top (w = 2w + bit, one carry-in add); |v| goes to
+    // the low or the high bucket.  m is formed as (v > hi) | (v < lo): for
+    // v >= 0 (v = -0 included) v < lo cannot hold (lo is half a minimum
+    // that is at most v, or negative) and for v < 0 v > hi cannot (hi is
+    // half a maximum that is at least v, or at least 0), -v > -lo is
+    // v < lo exactly, and a NaN fails both -- two compares instead of a
+    // compare, a select and a compare.  G64 adds dims j and j+32 (its two
+    // plane words) before the halving tree; G32 / G16 reduce within one
+    // word.
     if (WIDE && wave >= NW) return;  // (a wider workgroup's other waves: no dimensions)
     const int c0 = wave * CH;
     if constexpr (G == 64) {
@@ -120,66 +203,55 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
         // first level pairs (i, i+32) with (i+16, i+48); iteration i takes
         // those four dimensions and leaves z[i] = (x[i] + x[i+32]) +
         // (x[i+16] + x[i+48]) -- the same additions as the plain order, with
-        // 16 partial sums live instead of 64 contributions.  Bits are placed
-        // at their positions directly.  The row stays packed (8 x 16 bytes).
+        // 16 partial sums live instead of 64 contributions.  The iterations
+        // run i = 15 .. 0, so each quarter q of the rep (dims 16q .. 16q+15)
+        // gets its bits shifted in from the top; the halving tree then adds
+        // the z[i] in its fixed order.  The row stays packed (8 x 16 bytes).
         for (int t = lane; t < n; t += kWave) {
             const T* row = row_of(t) + c0;
             const int64_t orow = orow0 + t;
             Raw8<T> raw[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) raw[c].load(row + 8 * c);
-            uint32_t sw0 = 0, mw0 = 0, sw1 = 0, mw1 = 0;
-            // z(i): dims i, i+16, i+32, i+48 -> (low, high) level-16 sums;
-            // i is a compile-time constant (the row registers are indexed
-            // statically)
-            auto z = [&](auto ic) {
-                constexpr int i = decltype(ic)::value;
-                float xl[4], xh[4];
+            uint32_t sq[4] = {0u, 0u, 0u, 0u}, mq[4] = {0u, 0u, 0u, 0u};
+            float2 z[16];
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int ib = 3; ib >= 0; --ib) {
+                // thresholds of dims 16q + 4ib .. 16q + 4ib + 3, four to a read;
+                // the empty asm keeps the reads in this block
+                f32x4 h4[4], l4[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int dm = i + 16 * q;
-                    // the empty asm ties the thresholds to the bit words:
-                    // read one dimension at a time, not all hoisted
-                    float hi = s_hi[c0 + dm], nlo = s_nlo[c0 + dm];
-                    asm volatile("" : "+v"(hi), "+v"(nlo), "+v"(sw0), "+v"(sw1));
-                    const float v = raw[dm / 8].get(dm % 8);
-                    const float a = fabsf(v);
-                    const bool sg = v >= 0.0f;
-                    const bool mg = a > (sg ? hi : nlo);  // as in the plain path below
-                    const int bit = dm & 31;
-                    if (q < 2) {
-                        sw0 |= static_cast<uint32_t>(sg) << bit;
-                        mw0 |= static_cast<uint32_t>(mg) << bit;
-                    } else {
-                        sw1 |= static_cast<uint32_t>(sg) << bit;
-                        mw1 |= static_cast<uint32_t>(mg) << bit;
-                    }
-                    xl[q] = mg ? 0.0f : a;
-                    xh[q] = mg ? a : 0.0f;
+                    h4[q] = *reinterpret_cast<const f32x4*>(s_hi + c0 + 16 * q + 4 * ib);
+                    l4[q] = *reinterpret_cast<const f32x4*>(s_lo + c0 + 16 * q + 4 * ib);
                 }
-                return make_float2((xl[0] + xl[2]) + (xl[1] + xl[3]), (xh[0] + xh[2]) + (xh[1] + xh[3]));
-            };
+                asm volatile("" : "+v"(h4[0]), "+v"(h4[1]), "+v"(h4[2]), "+v"(h4[3]), "+v"(l4[0]), "+v"(l4[1]),
+                             "+v"(l4[2]), "+v"(l4[3]));
+#pragma unroll
+                for (int ii = 3; ii >= 0; --ii) {
+                    const int i = 4 * ib + ii;
+                    float xl[4], xh[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int dm = i + 16 * q;
+                        encode_dim(raw[dm / 8].get(dm % 8), h4[q][ii], l4[q][ii], sq[q], mq[q], xl[q], xh[q]);
+                    }
+                    z[i] = make_float2((xl[0] + xl[2]) + (xl[1] + xl[3]), (xh[0] + xh[2]) + (xh[1] + xh[3]));
+                    // and the sums here, keeping few values live
+                    asm volatile("" : "+v"(z[i].x), "+v"(z[i].y));
+                }
+            }
             auto add2 = [](float2 u, float2 w) { return make_float2(u.x + w.x, u.y + w.y); };
-            using std::integral_constant;
-            // the halving tree over z(0..15) (levels 8, 4, 2, 1), evaluated
-            // depth-first so only a few partial sums are live
-            auto a8 = [&](auto ic) {
-                constexpr int i = decltype(ic)::value;
-                const float2 u = z(integral_constant<int, i>{});
-                return add2(u, z(integral_constant<int, i + 8>{}));
-            };
-            auto b4 = [&](auto ic) {
-                constexpr int i = decltype(ic)::value;
-                const float2 u = a8(integral_constant<int, i>{});
-                return add2(u, a8(integral_constant<int, i + 4>{}));
-            };
-            auto c2 = [&](auto ic) {
-                constexpr int i = decltype(ic)::value;
-                const float2 u = b4(integral_constant<int, i>{});
-                return add2(u, b4(integral_constant<int, i + 2>{}));
-            };
-            const float2 c0s = c2(integral_constant<int, 0>{});
-            const float2 sums = add2(c0s, c2(integral_constant<int, 1>{}));
+            // the halving tree over z[0..15] (levels 8, 4, 2, 1)
+            float2 a8[8], b4[4];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a8[i] = add2(z[i], z[i + 8]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b4[i] = add2(a8[i], a8[i + 4]);
+            const float2 sums = add2(add2(b4[0], b4[2]), add2(b4[1], b4[3]));
+            const uint32_t sw0 = sq[0] | (sq[1] << 16), sw1 = sq[2] | (sq[3] << 16);
+            const uint32_t mw0 = mq[0] | (mq[1] << 16), mw1 = mq[2] | (mq[3] << 16);
             const int hn = __popc(mw0) + __popc(mw1);
             float lo, de;
             finish_rep(sums.x, 64 - hn, sums.y, hn, lo, de);
@@ -197,7 +269,6 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
         constexpr int NWD = CH / 32, NR = CH / G;
         uint32_t sw[NWD], mw[NWD];
         float lows[NR], deltas[NR];
-        float pl[32], ph[32];  // G64: first-level pair sums
 #pragma unroll
         for (int wi = 0; wi < NWD; ++wi) {
             float v[32];
@@ -205,36 +276,23 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
             for (int i = 0; i < 32; i += 8) load8<T>(row + wi * 32 + i, v + i);
             uint32_t sgw = 0, mgw = 0;
             float xl[32], xh[32];
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-            for (int j = 31; j >= 0; --j) {
-                // m = s ? v > hi : v < lo is |v| > (s ? hi : -lo): for v < 0,
-                // v < lo <=> -v > -lo; for v = -0 both sides read 0 > hi; a
-                // NaN has s = 0 and fails the compare.  The thresholds pass
-                // through an empty asm: the same in every lane, they stay in
-                // VGPRs, and the dimensions stay in order.
-                float hi = s_hi[c0 + wi * 32 + j], nlo = s_nlo[c0 + wi * 32 + j];
-                asm volatile("" : "+v"(hi), "+v"(nlo), "+v"(sgw), "+v"(mgw));
-                const float a = fabsf(v[j]);
-                const bool sg = v[j] >= 0.0f;
-                const bool mg = a > (sg ? hi : nlo);
-                sgw = sgw * 2u + static_cast<uint32_t>(sg);
-                mgw = mgw * 2u + static_cast<uint32_t>(mg);
-                xl[j] = mg ? 0.0f : a;
-                xh[j] = mg ? a : 0.0f;
+            for (int jb = 7; jb >= 0; --jb) {
+                // thresholds of dims 4jb .. 4jb+3 of the word, one read each;
+                // the empty asm keeps the reads in this block
+                f32x4 h4 = *reinterpret_cast<const f32x4*>(s_hi + c0 + wi * 32 + 4 * jb);
+                f32x4 l4 = *reinterpret_cast<const f32x4*>(s_lo + c0 + wi * 32 + 4 * jb);
+                asm volatile("" : "+v"(h4), "+v"(l4));
+#pragma unroll
+                for (int jj = 3; jj >= 0; --jj) {
+                    const int j = 4 * jb + jj;
+                    encode_dim(v[j], h4[jj], l4[jj], sgw, mgw, xl[j], xh[j]);
+                }
             }
             sw[wi] = sgw;
             mw[wi] = mgw;
-            if constexpr (G == 64) {
-                if (wi == 0) {
-#pragma unroll
-                    for (int j = 0; j < 32; ++j) { pl[j] = xl[j]; ph[j] = xh[j]; }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 32; ++j) { pl[j] = pl[j] + xl[j]; ph[j] = ph[j] + xh[j]; }
-                    const int hn = __popc(mw[0]) + __popc(mgw);
-                    finish_rep(tree_halving(pl, 32), 64 - hn, tree_halving(ph, 32), hn, lows[0], deltas[0]);
-                }
-            } else if constexpr (G == 32) {
+            if constexpr (G == 32) {
                 const int hn = __popc(mgw);
                 finish_rep(tree_halving(xl, 32), 32 - hn, tree_halving(xh, 32), hn, lows[0], deltas[0]);
             } else {

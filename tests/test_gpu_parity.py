@@ -106,6 +106,48 @@ def test_pack_outlier_keys_and_capacity_tail():
         assert np.array_equal(bits(a)[:, :999], b)
 
 
+def _special_keys(dtype, heads: int, tokens: int, seed: int) -> torch.Tensor:
+    """Keys whose encode sits on every edge of the magnitude test
+    mag = v >= 0 ? v > 0.5*max : v < 0.5*min: values equal to half a
+    group extremum, dimensions with a positive minimum or a negative
+    maximum, signed zeros only, the dtype's subnormals, NaNs and
+    infinities, beside random dimensions."""
+    g = torch.Generator().manual_seed(seed)
+    shape = (heads, tokens, 128)
+    vals = torch.tensor([-4.0, -2.0, -1.0, -0.5, -0.0, 0.0, 0.5, 1.0, 2.0, 4.0])
+    x = vals[torch.randint(0, len(vals), shape, generator=g)]
+    x[..., 0:8] = x[..., 0:8].abs() + 0.5
+    x[..., 8:16] = -(x[..., 8:16].abs() + 0.5)
+    x[..., 16:24] = torch.where(torch.rand(heads, tokens, 8, generator=g) < 0.5, -0.0, 0.0)
+    tiny = {torch.bfloat16: 2.0 ** -133, torch.float16: 2.0 ** -24, torch.float32: 2.0 ** -149}[dtype]
+    x[..., 24:32] = torch.randint(-3, 4, (heads, tokens, 8), generator=g).float() * tiny
+    x[:, ::7, 40] = float("nan")
+    x[:, 3::11, 70] = float("nan")
+    x[0, 5::13, 90] = float("inf")
+    x[-1, 9::17, 100] = float("-inf")
+    x[..., 110:] = torch.randn(heads, tokens, 18, generator=g) * 3.0
+    return x.to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("tg", (64, 128))
+def test_pack_edge_values_bit_exact(tg, g, dtype):
+    """Sign and magnitude planes bit-exact on the edge values above; the
+    representatives bit-exact wherever the oracle's is a number, NaN where
+    it is NaN (a NaN's payload is not compared)."""
+    keys = _special_keys(dtype, 2, 2 * tg + 37, seed=tg + g)
+    packed = popkv_cuda.pack_keys(keys.contiguous(), token_group_size=tg, dim_group_size=g)
+    want = core.pack_keys(f32(keys), token_group_size=tg, dim_group_size=g)
+    assert np.array_equal(bits(packed[0]), want[0]) and np.array_equal(bits(packed[1]), want[1])
+    for a, b in zip(packed[2:], want[2:]):
+        got = bits(a)
+        nan = (b & 0x7C00 == 0x7C00) & (b & 0x03FF != 0)
+        assert np.array_equal(got[~nan], b[~nan])
+        assert np.all((got[nan] & 0x7C00 == 0x7C00) & (got[nan] & 0x03FF != 0))
+        assert nan.any() and (~nan).any()
+
+
 @pytest.mark.parametrize("tg", (8, 16, 32, 64, 128))
 def test_incremental_cache_crosses_every_token_group_boundary(tg):
     """tests/test_popkv.py:354-372 on the HIP path, bit-exact."""
