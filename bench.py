@@ -242,8 +242,8 @@ def bench_c4(args) -> int:
     for i in range(args.warmup):
         step(i)
     step_ms = graph_ms(step, max(1, args.steps // n_sets), trials=max(10, args.trials))
-    # the one-time prepack of the eight 64K prefixes, into the existing planes (one launch per sequence)
-    prepack_ms = graph_ms(prepack, 4)
+    # the one-time prepack of the eight 64K prefixes, into the existing planes: median of 5 trials
+    prepack_ms = graph_ms(prepack, 2, trials=5)
     per_seq = workloads.algorithmic_bytes(w)
     meta_row = 32 + 4 * (w.head_dim // w.dim_group)
     active = L % w.token_group + 1  # tokens re-encoded by the append (the new one included)

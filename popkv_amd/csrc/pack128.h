@@ -99,7 +99,7 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
     constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    __shared__ __align__(16) float s_hi[D], s_lo[D];  // 0.5*max and 0.5*min, read four at a time
+    __shared__ __align__(16) float s_hi[D], s_lo[D];  // 0.5*max and 0.5*min, read in vectors
     if constexpr (!WIDE) {
         // Phase 1: lane l reads dims d8 .. d8+7 (16 bytes) of row slot
         // l / 16, so one load covers four rows; in each pass of 64 rows wave
@@ -203,10 +203,13 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
         // first level pairs (i, i+32) with (i+16, i+48); iteration i takes
         // those four dimensions and leaves z[i] = (x[i] + x[i+32]) +
         // (x[i+16] + x[i+48]) -- the same additions as the plain order, with
-        // 16 partial sums live instead of 64 contributions.  The iterations
+        // few partial sums live instead of 64 contributions.  The iterations
         // run i = 15 .. 0, so each quarter q of the rep (dims 16q .. 16q+15)
-        // gets its bits shifted in from the top; the halving tree then adds
-        // the z[i] in its fixed order.  The row stays packed (8 x 16 bytes).
+        // gets its bits shifted in from the top, and the halving tree over
+        // z[0..15] (levels 8, 4, 2, 1) forms each sum once both operands
+        // exist, in its fixed order.  The row stays packed (8 x 16 bytes);
+        // the thresholds of two consecutive i are read together (64-bit LDS
+        // reads: at 128 bits the extra registers cost more than the reads).
         for (int t = lane; t < n; t += kWave) {
             const T* row = row_of(t) + c0;
             const int64_t orow = orow0 + t;
@@ -214,42 +217,41 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
 #pragma unroll
             for (int c = 0; c < 8; ++c) raw[c].load(row + 8 * c);
             uint32_t sq[4] = {0u, 0u, 0u, 0u}, mq[4] = {0u, 0u, 0u, 0u};
-            float2 z[16];
-            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            float2 z[16];  // z[i], then the tree's partial sums in place
+            auto add2 = [](float2 u, float2 w) { return make_float2(u.x + w.x, u.y + w.y); };
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-            for (int ib = 3; ib >= 0; --ib) {
-                // thresholds of dims 16q + 4ib .. 16q + 4ib + 3, four to a read;
-                // the empty asm keeps the reads in this block
-                f32x4 h4[4], l4[4];
+            for (int ib = 7; ib >= 0; --ib) {
+                // thresholds of dims 16q + 2ib, 16q + 2ib + 1; the empty asm
+                // keeps the reads in this block
+                f32x2 h2[4], l2[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    h4[q] = *reinterpret_cast<const f32x4*>(s_hi + c0 + 16 * q + 4 * ib);
-                    l4[q] = *reinterpret_cast<const f32x4*>(s_lo + c0 + 16 * q + 4 * ib);
+                    h2[q] = *reinterpret_cast<const f32x2*>(s_hi + c0 + 16 * q + 2 * ib);
+                    l2[q] = *reinterpret_cast<const f32x2*>(s_lo + c0 + 16 * q + 2 * ib);
                 }
-                asm volatile("" : "+v"(h4[0]), "+v"(h4[1]), "+v"(h4[2]), "+v"(h4[3]), "+v"(l4[0]), "+v"(l4[1]),
-                             "+v"(l4[2]), "+v"(l4[3]));
+                asm volatile("" : "+v"(h2[0]), "+v"(h2[1]), "+v"(h2[2]), "+v"(h2[3]), "+v"(l2[0]), "+v"(l2[1]),
+                             "+v"(l2[2]), "+v"(l2[3]));
 #pragma unroll
-                for (int ii = 3; ii >= 0; --ii) {
-                    const int i = 4 * ib + ii;
+                for (int ii = 1; ii >= 0; --ii) {
+                    const int i = 2 * ib + ii;
                     float xl[4], xh[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int dm = i + 16 * q;
-                        encode_dim(raw[dm / 8].get(dm % 8), h4[q][ii], l4[q][ii], sq[q], mq[q], xl[q], xh[q]);
+                        encode_dim(raw[dm / 8].get(dm % 8), h2[q][ii], l2[q][ii], sq[q], mq[q], xl[q], xh[q]);
                     }
                     z[i] = make_float2((xl[0] + xl[2]) + (xl[1] + xl[3]), (xh[0] + xh[2]) + (xh[1] + xh[3]));
-                    // and the sums here, keeping few values live
+                    // the tree levels whose second operand is now complete
+                    if (i < 8) z[i] = add2(z[i], z[i + 8]);
+                    if (i < 4) z[i] = add2(z[i], z[i + 4]);
+                    if (i < 2) z[i] = add2(z[i], z[i + 2]);
+                    if (i < 1) z[i] = add2(z[i], z[i + 1]);
+                    // the sums are formed here, so few values stay live
                     asm volatile("" : "+v"(z[i].x), "+v"(z[i].y));
                 }
             }
-            auto add2 = [](float2 u, float2 w) { return make_float2(u.x + w.x, u.y + w.y); };
-            // the halving tree over z[0..15] (levels 8, 4, 2, 1)
-            float2 a8[8], b4[4];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) a8[i] = add2(z[i], z[i + 8]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) b4[i] = add2(a8[i], a8[i + 4]);
-            const float2 sums = add2(add2(b4[0], b4[2]), add2(b4[1], b4[3]));
+            const float2 sums = z[0];
             const uint32_t sw0 = sq[0] | (sq[1] << 16), sw1 = sq[2] | (sq[3] << 16);
             const uint32_t mw0 = mq[0] | (mq[1] << 16), mw1 = mq[2] | (mq[3] << 16);
             const int hn = __popc(mw0) + __popc(mw1);
