@@ -230,6 +230,7 @@ template <int G>
 struct GroupState {
     uint32_t qs[kMaxGroupHeads][4], qm[kMaxGroupHeads][4];
     float ql[kMaxGroupHeads][128 / G], qd[kMaxGroupHeads][128 / G];
+    int npq[kMaxGroupHeads][128 / G];  // -(magnitude bits of the head's representative r)
 };
 
 // Encodes the group's query rows (head_dim 128) into `st` in the
@@ -299,6 +300,7 @@ __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk,
                 hn += __popc(bits);
             }
             finish_rep(sum, G - hn, hs, hn, st.ql[h][r], st.qd[h][r]);
+            st.npq[h][r] = -hn;
         }
     }
     __syncthreads();
@@ -317,6 +319,10 @@ __device__ void load_group_state(const int32_t* __restrict__ q_sign, const int32
     for (int i = threadIdx.x; i < qpk * R; i += kScoreThreads) {
         st.ql[i / R][i % R] = q_low[qrow0 * R + i];
         st.qd[i / R][i % R] = q_delta[qrow0 * R + i];
+        uint32_t qm[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) qm[w] = static_cast<uint32_t>(q_mag[(qrow0 + i / R) * 4 + w]);
+        st.npq[i / R][i % R] = -rep_popc<G>(qm, i % R);
     }
     __syncthreads();
 }
@@ -441,7 +447,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
         for (int r = 0; r < R; ++r) {
             ql[r] = st.ql[h][r];
             dq[r] = st.qd[h][r];
-            npq[r] = neg_opaque(rep_popc<G>(qm, r));
+            npq[r] = st.npq[h][r];
         }
         uint16_t* srow = scores + (qrow0 + h) * out_stride;
         // every token's score first, without a branch (a token past the end
