@@ -225,12 +225,19 @@ constexpr int kScoreThreads = 512;  // 8 waves: 1024 tokens x one GQA group per 
 template <int G> constexpr int score_tokens_per_thread() { return G == 64 ? 2 : 1; }
 constexpr int kMaxGroupHeads = 64;  // query heads per KV head the LDS stage holds
 
+// Query state of one head, contiguous in LDS (the scorer reads a head's
+// whole state from one base address with 16-byte reads).
+template <int G>
+struct __align__(16) HeadState {
+    uint32_t qs[4], qm[4];
+    float ql[128 / G], qd[128 / G];
+    int npq[128 / G];  // -(magnitude bits of representative r)
+};
+
 // Query state of one GQA group in LDS.
 template <int G>
 struct GroupState {
-    uint32_t qs[kMaxGroupHeads][4], qm[kMaxGroupHeads][4];
-    float ql[kMaxGroupHeads][128 / G], qd[kMaxGroupHeads][128 / G];
-    int npq[kMaxGroupHeads][128 / G];  // -(magnitude bits of the head's representative r)
+    HeadState<G> h[kMaxGroupHeads];
 };
 
 // Encodes the group's query rows (head_dim 128) into `st` in the
@@ -266,10 +273,10 @@ __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk,
         hi_c[h][lane + 64] = m1 ? a1 : 0.0f;
         const uint64_t bs0 = __ballot(s0), bs1 = __ballot(s1), bm0 = __ballot(m0), bm1 = __ballot(m1);
         if (lane == 0) {
-            st.qs[h][0] = static_cast<uint32_t>(bs0); st.qs[h][1] = static_cast<uint32_t>(bs0 >> 32);
-            st.qs[h][2] = static_cast<uint32_t>(bs1); st.qs[h][3] = static_cast<uint32_t>(bs1 >> 32);
-            st.qm[h][0] = static_cast<uint32_t>(bm0); st.qm[h][1] = static_cast<uint32_t>(bm0 >> 32);
-            st.qm[h][2] = static_cast<uint32_t>(bm1); st.qm[h][3] = static_cast<uint32_t>(bm1 >> 32);
+            st.h[h].qs[0] = static_cast<uint32_t>(bs0); st.h[h].qs[1] = static_cast<uint32_t>(bs0 >> 32);
+            st.h[h].qs[2] = static_cast<uint32_t>(bs1); st.h[h].qs[3] = static_cast<uint32_t>(bs1 >> 32);
+            st.h[h].qm[0] = static_cast<uint32_t>(bm0); st.h[h].qm[1] = static_cast<uint32_t>(bm0 >> 32);
+            st.h[h].qm[2] = static_cast<uint32_t>(bm1); st.h[h].qm[3] = static_cast<uint32_t>(bm1 >> 32);
         }
     }
     __syncthreads();
@@ -295,12 +302,12 @@ __device__ __forceinline__ void encode_group_fold(const float (*qv)[2], int qpk,
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 if ((w + 1) * 32 <= r * G || w * 32 >= (r + 1) * G) continue;
-                uint32_t bits = st.qm[h][w];
+                uint32_t bits = st.h[h].qm[w];
                 if constexpr (G == 16) bits = (r & 1) ? (bits >> 16) : (bits & 0xffffu);
                 hn += __popc(bits);
             }
-            finish_rep(sum, G - hn, hs, hn, st.ql[h][r], st.qd[h][r]);
-            st.npq[h][r] = -hn;
+            finish_rep(sum, G - hn, hs, hn, st.h[h].ql[r], st.h[h].qd[r]);
+            st.h[h].npq[r] = -hn;
         }
     }
     __syncthreads();
@@ -313,16 +320,16 @@ __device__ void load_group_state(const int32_t* __restrict__ q_sign, const int32
                                  int64_t qrow0, int qpk, GroupState<G>& st) {
     constexpr int R = 128 / G;
     for (int i = threadIdx.x; i < qpk * 4; i += kScoreThreads) {
-        st.qs[i / 4][i % 4] = static_cast<uint32_t>(q_sign[qrow0 * 4 + i]);
-        st.qm[i / 4][i % 4] = static_cast<uint32_t>(q_mag[qrow0 * 4 + i]);
+        st.h[i / 4].qs[i % 4] = static_cast<uint32_t>(q_sign[qrow0 * 4 + i]);
+        st.h[i / 4].qm[i % 4] = static_cast<uint32_t>(q_mag[qrow0 * 4 + i]);
     }
     for (int i = threadIdx.x; i < qpk * R; i += kScoreThreads) {
-        st.ql[i / R][i % R] = q_low[qrow0 * R + i];
-        st.qd[i / R][i % R] = q_delta[qrow0 * R + i];
+        st.h[i / R].ql[i % R] = q_low[qrow0 * R + i];
+        st.h[i / R].qd[i % R] = q_delta[qrow0 * R + i];
         uint32_t qm[4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) qm[w] = static_cast<uint32_t>(q_mag[(qrow0 + i / R) * 4 + w]);
-        st.npq[i / R][i % R] = -rep_popc<G>(qm, i % R);
+        st.h[i / R].npq[i % R] = -rep_popc<G>(qm, i % R);
     }
     __syncthreads();
 }
@@ -439,15 +446,15 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
         float ql[R], dq[R];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            qs[w] = st.qs[h][w];
-            qm[w] = st.qm[h][w];
+            qs[w] = st.h[h].qs[w];
+            qm[w] = st.h[h].qm[w];
         }
         int npq[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            ql[r] = st.ql[h][r];
-            dq[r] = st.qd[h][r];
-            npq[r] = st.npq[h][r];
+            ql[r] = st.h[h].ql[r];
+            dq[r] = st.h[h].qd[r];
+            npq[r] = st.h[h].npq[r];
         }
         uint16_t* srow = scores + (qrow0 + h) * out_stride;
         // every token's score first, without a branch (a token past the end
