@@ -77,7 +77,8 @@ __device__ __forceinline__ void encode_dim(float v, float hi, float lo, uint32_t
         "v_cndmask_b32_e64 %[xh], 0, |%[v]|, %[m1]"
         : [ws] "+v"(ws), [wm] "+v"(wm), [xl] "=&v"(xl), [xh] "=&v"(xh), [ms] "=&s"(ms), [m1] "=&s"(m1),
           [m2] "=&s"(m2), [carry] "=&s"(carry)
-        : [v] "v"(v), [hi] "v"(hi), [lo] "v"(lo));
+        : [v] "v"(v), [hi] "v"(hi), [lo] "v"(lo)
+        : "scc");  // s_or_b64 sets SCC
 }
 
 // Encodes one token group (head_dim 128) into packed rows orow0 + t:
