@@ -82,10 +82,11 @@ __device__ __forceinline__ void encode_dim(float v, float hi, float lo, uint32_t
 }
 
 // Encodes one token group (head_dim 128) into packed rows orow0 + t:
-//   Phase 1 -- lane l owns dims 2l and 2l+1; the waves stream interleaved
-//              rows of the group with coalesced loads, keeping
-//              per-dimension min/max in registers; the partial extrema meet
-//              in LDS and the thresholds 0.5*max / 0.5*min go to LDS.
+//   Phase 1 -- the waves stream the group's rows with coalesced loads (16
+//              bytes of one of four rows per lane; in the WIDE form 4 bytes,
+//              lane l owning dims 2l and 2l+1), keeping per-dimension
+//              min/max in registers; the partial extrema meet in LDS and
+//              the thresholds 0.5*max / 0.5*min go to LDS.
 //   Phase 2 -- one token per lane, each wave on its chunk of CH = max(G, 32)
 //              dimensions: the sign/magnitude words and the representatives,
 //              reduced in registers in the production tree order (G64 pairs
