@@ -367,13 +367,21 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
 
     // 1. query encode + popcount score -> radix order keys of the fp16 scores
     //    (rows padded to a multiple of 128 tokens, so every row starts
-    //    256-byte aligned) + per-head high-byte key histograms
-    st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
-                                               static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
-                                               static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
-                                               tokens, dim_group_size, keys, L.score_stride, hist, popkv::SeqTable{}, s),
-                  "popkv_layer_step(score)");
-    if (st) return st;
+    //    256-byte aligned) + per-head high-byte key histograms.  With
+    //    k >= tokens every cached token is selected (k <= 0: none), so no
+    //    score can change the result: the scorer and the chunk histograms
+    //    are skipped and the select + attention kernel takes its
+    //    every-token (no-token) path, which reads none of their outputs.
+    if (L.k > 0 && L.k < tokens) {
+        st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag,
+                                                   static_cast<const uint16_t*>(k_low),
+                                                   static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
+                                                   static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
+                                                   tokens, dim_group_size, keys, L.score_stride, hist,
+                                                   popkv::SeqTable{}, s),
+                      "popkv_layer_step(score)");
+        if (st) return st;
+    }
     // From here on the scorer has added into the histogram region, which
     // must be zero when the next call begins: a failed launch clears it.
     auto clear_hist = [&](int status) {
