@@ -341,3 +341,46 @@ def test_decode_layer_equals_step_then_append():
         _check_batch(q, cache, lengths, ck, cv, mapping, budget, out, idx)
         lengths.host = [x + 1 for x in lengths.host]
         assert lengths.device.cpu().tolist() == lengths.host
+
+
+@pytest.mark.parametrize("g, tg", [(16, 128), (32, 32), (64, 8)])
+def test_decode_layer_append_other_group_shapes(g, tg):
+    """The append inside the select + attention launch for the 16- and
+    32-dimension encodes (four waves of the launch's workgroup) and a short
+    token group: the same output, indices, static caches and packed planes
+    as the layer step followed by append_batched, and the planes equal to
+    the oracle's pack of the grown sequences.  The lengths put the new token
+    at a group's first row, inside a group and at its last row."""
+    batch, qh, kvh, rows, budget = 3, 32, 8, 1200, 256
+    starts = [tg * 7, tg * 5 + 3, tg * 6 - 1]
+    keys, values = _seq_data(batch, kvh, rows, seed=31 + g)
+    mapping = torch.arange(qh, device=DEV) // (qh // kvh)
+
+    def fresh():
+        kc = torch.zeros(batch, kvh, rows, 128, dtype=torch.bfloat16, device=DEV)
+        vc = torch.zeros_like(kc)
+        for b, n in enumerate(starts):
+            kc[b, :, :n] = keys[b, :, :n].to(DEV)
+            vc[b, :, :n] = values[b, :, :n].to(DEV)
+        lengths = pb.SequenceLengths.create(starts, DEV)
+        return pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g), lengths
+
+    gq = torch.Generator().manual_seed(7 + g)
+    q = torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+    ck = torch.stack([keys[b, :, starts[b]] for b in range(batch)]).to(DEV)
+    cv = torch.stack([values[b, :, starts[b]] for b in range(batch)]).to(DEV)
+    ca, la = fresh()
+    o1, i1 = pb.popkv_layer_step_batched(q, ca, la, ck, cv, mapping, budget=budget, return_indices=True)
+    pb.append_batched(ca, la, ck, cv)
+    cb, lb = fresh()
+    o2, i2 = pb.popkv_layer_step_batched(q, cb, lb, ck, cv, mapping, budget=budget, return_indices=True,
+                                         append=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(i1, i2)
+    assert torch.equal(ca.key_cache, cb.key_cache) and torch.equal(ca.value_cache, cb.value_cache)
+    for x, y in zip(ca.packed, cb.packed):
+        assert torch.equal(x, y)
+    for b, n in enumerate(starts):
+        want = core.pack_keys(f32(cb.key_cache[b, :, :n + 1]), token_group_size=tg, dim_group_size=g)
+        for a, wp in zip(_packed_np(cb, b), want):
+            assert np.array_equal(a[:, :n + 1], wp), (g, tg, b)
