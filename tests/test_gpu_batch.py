@@ -343,21 +343,22 @@ def test_decode_layer_equals_step_then_append():
         assert lengths.device.cpu().tolist() == lengths.host
 
 
-@pytest.mark.parametrize("g, tg", [(16, 128), (32, 32), (64, 8)])
-def test_decode_layer_append_other_group_shapes(g, tg):
+@pytest.mark.parametrize("g, tg, dtype", [(16, 128, torch.bfloat16), (32, 32, torch.bfloat16), (64, 8, torch.bfloat16),
+                                         (64, 64, torch.float16), (32, 32, torch.float32)])
+def test_decode_layer_append_other_group_shapes(g, tg, dtype):
     """The append inside the select + attention launch for the 16- and
-    32-dimension encodes (four waves of the launch's workgroup) and a short
-    token group: the same output, indices, static caches and packed planes
+    32-dimension encodes (four waves of the launch's workgroup), a short
+    token group and the fp16 / fp32 caches: the same output, indices, static caches and packed planes
     as the layer step followed by append_batched, and the planes equal to
     the oracle's pack of the grown sequences.  The lengths put the new token
     at a group's first row, inside a group and at its last row."""
     batch, qh, kvh, rows, budget = 3, 32, 8, 1200, 256
     starts = [tg * 7, tg * 5 + 3, tg * 6 - 1]
-    keys, values = _seq_data(batch, kvh, rows, seed=31 + g)
+    keys, values = _seq_data(batch, kvh, rows, seed=31 + g, dtype=dtype)
     mapping = torch.arange(qh, device=DEV) // (qh // kvh)
 
     def fresh():
-        kc = torch.zeros(batch, kvh, rows, 128, dtype=torch.bfloat16, device=DEV)
+        kc = torch.zeros(batch, kvh, rows, 128, dtype=dtype, device=DEV)
         vc = torch.zeros_like(kc)
         for b, n in enumerate(starts):
             kc[b, :, :n] = keys[b, :, :n].to(DEV)
@@ -366,7 +367,7 @@ def test_decode_layer_append_other_group_shapes(g, tg):
         return pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g), lengths
 
     gq = torch.Generator().manual_seed(7 + g)
-    q = torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+    q = torch.randn(batch, qh, 128, generator=gq).to(dtype).to(DEV)
     ck = torch.stack([keys[b, :, starts[b]] for b in range(batch)]).to(DEV)
     cv = torch.stack([values[b, :, starts[b]] for b in range(batch)]).to(DEV)
     ca, la = fresh()
@@ -383,4 +384,4 @@ def test_decode_layer_append_other_group_shapes(g, tg):
     for b, n in enumerate(starts):
         want = core.pack_keys(f32(cb.key_cache[b, :, :n + 1]), token_group_size=tg, dim_group_size=g)
         for a, wp in zip(_packed_np(cb, b), want):
-            assert np.array_equal(a[:, :n + 1], wp), (g, tg, b)
+            assert np.array_equal(a[:, :n + 1], wp), (g, tg, dtype, b)
