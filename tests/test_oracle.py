@@ -262,6 +262,31 @@ def test_incremental_append_equals_full_encode(tg):
                 assert np.array_equal(a[:, :n], b)
 
 
+def test_magnitude_rule_equals_two_compares():
+    """The HIP encode forms the magnitude bit as (v > 0.5*max) | (v < 0.5*min)
+    without a sign-dependent select; the reference's rule is
+    v >= 0 ? v > 0.5*max : v < 0.5*min with max / min over the group (NaNs
+    ignored, as fmaxf / fminf do).  The two agree on every element of groups
+    built from signed zeros, subnormals, ties at half an extremum, infinities,
+    NaNs and random values, including all-negative and all-positive groups."""
+    g = rng(11)
+    special = np.array([0.0, -0.0, 1e-45, -1e-45, 2.0 ** -126, -(2.0 ** -126), 0.5, -0.5, 1.0, -1.0, 2.0, -2.0,
+                        4.0, -4.0, np.inf, -np.inf, np.nan, 3.4e38, -3.4e38], np.float32)
+    cases = [special, np.abs(special), -np.abs(special)]
+    for _ in range(300):
+        n = int(g.integers(1, 9))
+        vals = np.concatenate([g.choice(special, n), (g.standard_normal(n) * 10.0 ** g.integers(-40, 38))])
+        cases.append(g.permutation(vals).astype(np.float32))
+    with np.errstate(over="ignore", invalid="ignore"):
+        for v in cases:
+            mx = np.fmax.reduce(v)  # NaNs ignored, like fmaxf
+            mn = np.fmin.reduce(v)
+            hi, lo = np.float32(mx * np.float32(0.5)), np.float32(mn * np.float32(0.5))
+            ref = np.where(v >= 0, v > hi, v < lo)
+            two = (v > hi) | (v < lo)
+            assert np.array_equal(ref, two), v
+
+
 def test_pack_capacity_exceeded():
     keys = np.zeros((1, 10, 128), np.float32)
     packed = core.alloc_packed(1, 12, 128, 32)
