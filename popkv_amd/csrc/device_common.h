@@ -256,29 +256,6 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int /*lane*/) {
     return v;
 }
 
-// Exclusive prefix sum across a block of `waves` wave64s.  `sh` holds at
-// least `waves` + 1 words of LDS.  Returns the exclusive prefix; *total gets
-// the block sum.  Contains three __syncthreads() (the first protects `sh`
-// from a previous call's readers), so every thread of the block must call it.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, int waves, uint32_t* total) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    uint32_t incl = wave_incl_scan(v, lane);
-    __syncthreads();
-    if (lane == kWave - 1) sh[wave] = incl;
-    __syncthreads();
-    if (wave == 0) {
-        uint32_t w = lane < waves ? sh[lane] : 0u;
-        uint32_t wi = wave_incl_scan(w, lane);
-        if (lane < waves) sh[lane] = wi - w;
-        if (lane == waves - 1) sh[waves] = wi;
-    }
-    __syncthreads();
-    uint32_t base = sh[wave];
-    *total = sh[waves];
-    return base + incl - v;
-}
-
 // Exclusive prefix sum across a block of `waves` wave64s with a single
 // barrier: DPP scan inside each wave, wave totals through `sh` (`waves`
 // words).  For one use of `sh` per kernel (nothing may still be reading it).
