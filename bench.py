@@ -170,8 +170,8 @@ def bench_c4(args) -> int:
     top-k + current, split attention, merge; every sequence at its own
     device-side length) and the fused append (the new token's K/V rows into
     the static caches and the re-encode of each sequence's active token
-    group, read in place), the append running beside the step's select and
-    attention on a second stream.  The replays repeat
+    group, read in place), the append running in extra workgroups of the
+    step's select + attention launch.  The replays repeat
     the same token position (the lengths are not advanced inside the timed
     graph; advancing them is one 8-element add per decode step, not per
     layer).  The one-time prepack of the eight 64K prefixes is timed on its
