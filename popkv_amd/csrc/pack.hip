@@ -191,8 +191,10 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
 // Prefix prepack (APPEND false): block (x, y) encodes token group x of KV
 // head y, rows [x*tg, min(x*tg + tg, tokens)) of `keys`, into packed rows
 // y*cap + offset + x*tg + t.  Fused append (APPEND true): block i appends
-// the new token of (sequence, KV head) i (pack128_append).
-template <typename T, int G, bool APPEND>
+// the new token of (sequence, KV head) i (pack128_append).  STAGE (16-bit
+// rows, G 64, tg <= 64): the group's rows are read from memory once, into
+// LDS, and the encode pass reads them there.
+template <typename T, int G, bool APPEND, bool STAGE = false>
 __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     const T* __restrict__ keys, int64_t head_stride, int64_t tokens, int tg,
     int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
@@ -207,9 +209,9 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
         const int n = static_cast<int>(min(gs + static_cast<int64_t>(tg), tokens) - gs);
         const T* base = keys + kvh * head_stride + gs * D;
         auto row_of = [&](int t) -> const T* { return base + static_cast<int64_t>(t) * D; };
-        pack128_group<T, G>(row_of, n, kvh * cap + offset + gs, k_sign, k_mag, k_low, k_delta);
+        pack128_group<T, G, false, STAGE>(row_of, n, kvh * cap + offset + gs, k_sign, k_mag, k_low, k_delta);
     } else {
-        pack128_append<T, G>(blockIdx.x, ap, tg, k_sign, k_mag, k_low, k_delta, cap);
+        pack128_append<T, G, false, STAGE>(blockIdx.x, ap, tg, k_sign, k_mag, k_low, k_delta, cap);
     }
 }
 
@@ -223,7 +225,11 @@ hipError_t launch_pack_t(const T* keys, int64_t kvh, int64_t tokens, int d, int6
                       ((head_stride * static_cast<int64_t>(sizeof(T))) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(ks) % 16 == 0) && (reinterpret_cast<uintptr_t>(km) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(kl) % 16 == 0) && (reinterpret_cast<uintptr_t>(kd) % 16 == 0);
-    if (fast)
+    constexpr bool kStageable = G == 64 && sizeof(T) == 2;
+    if (fast && kStageable && tg <= 64)
+        hipLaunchKernelGGL((pack128_kernel<T, G, false, kStageable>), grid, dim3(kWave * pack128_waves<G>()), 0,
+                           stream, keys, head_stride, tokens, tg, ks, km, kl, kd, cap, off, AppendArgs<T>{});
+    else if (fast)
         hipLaunchKernelGGL((pack128_kernel<T, G, false>), grid, dim3(kWave * pack128_waves<G>()), 0, stream, keys,
                            head_stride, tokens, tg, ks, km, kl, kd, cap, off, AppendArgs<T>{});
     else
@@ -257,6 +263,13 @@ hipError_t launch_append_t(const AppendArgs<T>& ap, int64_t rows, int tg, int g,
                                nullptr, 0, 0, tg, ks, km, kl, kd, cap, 0, ap);
             break;
         default:
+            if constexpr (sizeof(T) == 2) {
+                if (tg <= 64) {
+                    hipLaunchKernelGGL((pack128_kernel<T, 64, true, true>), grid, dim3(kWave * pack128_waves<64>()), 0,
+                                       stream, nullptr, 0, 0, tg, ks, km, kl, kd, cap, 0, ap);
+                    break;
+                }
+            }
             hipLaunchKernelGGL((pack128_kernel<T, 64, true>), grid, dim3(kWave * pack128_waves<64>()), 0, stream,
                                nullptr, 0, 0, tg, ks, km, kl, kd, cap, 0, ap);
             break;

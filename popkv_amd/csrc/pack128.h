@@ -94,14 +94,21 @@ __device__ __forceinline__ void encode_dim(float v, float hi, float lo, uint32_t
 // Rows come from row_of(t), t < n.  Every thread of the workgroup calls it;
 // the workgroup has pack128_waves<G>() waves, or (WIDE) more, whose extra
 // waves join the barriers only.
-template <typename T, int G, bool WIDE = false, typename RowOf>
+template <typename T, int G, bool WIDE = false, bool STAGE = false, typename RowOf>
 __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_t orow0,
                                               int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
                                               uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta) {
     constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
+    static_assert(!STAGE || (!WIDE && sizeof(T) == 2 && G == 64), "the staged form: 16-bit rows, G64");
+    // STAGE (n <= 64): phase 1 also keeps the group's rows in LDS, at SROW
+    // bytes per row (16 more than a row, so that phase 2's lanes, a row each,
+    // reading 16 bytes at one offset spread over all banks), and phase 2
+    // reads them there instead of from memory.
+    constexpr int SROW = D * static_cast<int>(sizeof(T)) + 16;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     __shared__ __align__(16) float s_hi[D], s_lo[D];  // 0.5*max and 0.5*min, read in vectors
+    __shared__ __align__(16) uint8_t s_rows[STAGE ? 64 * SROW : 16];
     if constexpr (!WIDE) {
         // Phase 1: lane l reads dims d8 .. d8+7 (16 bytes) of row slot
         // l / 16, so one load covers four rows; in each pass of 64 rows wave
@@ -121,6 +128,11 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
             } else {
 #pragma unroll
                 for (int k = 0; k < QW; ++k) raw[k].load(row_of(min(r0 + 4 * (wave + NW * k) + sub, n - 1)) + d8);
+            }
+            if constexpr (STAGE) {  // one pass (n <= 64): row slot 4*(wave + NW*k) + sub
+#pragma unroll
+                for (int k = 0; k < QW; ++k)
+                    *reinterpret_cast<uint4*>(s_rows + (4 * (wave + NW * k) + sub) * SROW + d8 * 2) = raw[k].u;
             }
 #pragma unroll
             for (int k = 0; k < QW; ++k) {
@@ -213,11 +225,16 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
         // the thresholds of two consecutive i are read together (64-bit LDS
         // reads: at 128 bits the extra registers cost more than the reads).
         for (int t = lane; t < n; t += kWave) {
-            const T* row = row_of(t) + c0;
             const int64_t orow = orow0 + t;
             Raw8<T> raw[8];
+            if constexpr (STAGE) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) raw[c].load(row + 8 * c);
+                for (int c = 0; c < 8; ++c) raw[c].u = *reinterpret_cast<const uint4*>(s_rows + t * SROW + (c0 + 8 * c) * 2);
+            } else {
+                const T* row = row_of(t) + c0;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) raw[c].load(row + 8 * c);
+            }
             uint32_t sq[4] = {0u, 0u, 0u, 0u}, mq[4] = {0u, 0u, 0u, 0u};
             float2 z[16];  // z[i], then the tree's partial sums in place
             auto add2 = [](float2 u, float2 w) { return make_float2(u.x + w.x, u.y + w.y); };
@@ -333,7 +350,7 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
 // count; the new K/V rows are written to the static caches.  Every thread
 // of a workgroup of max(pack128_waves<G>(), 2 * D * sizeof(T) / 16 / 64)
 // waves (or, WIDE, more) calls it.
-template <typename T, int G, bool WIDE = false>
+template <typename T, int G, bool WIDE = false, bool STAGE = false>
 __device__ __forceinline__ void pack128_append(int64_t bh, const AppendArgs<T>& ap, int tg,
                                                int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
                                                uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta,
@@ -359,7 +376,7 @@ __device__ __forceinline__ void pack128_append(int64_t bh, const AppendArgs<T>& 
     const T* base = ap.key_cache + (bh * ap.cache_rows + sealed) * D;
     const T* last = ap.new_k + bh * D;
     auto row_of = [&](int t) -> const T* { return t == n - 1 ? last : base + static_cast<int64_t>(t) * D; };
-    pack128_group<T, G, WIDE>(row_of, n, bh * cap + sealed, k_sign, k_mag, k_low, k_delta);
+    pack128_group<T, G, WIDE, STAGE>(row_of, n, bh * cap + sealed, k_sign, k_mag, k_low, k_delta);
 }
 
 }  // namespace popkv

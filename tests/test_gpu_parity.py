@@ -148,6 +148,39 @@ def test_pack_edge_values_bit_exact(tg, g, dtype):
         assert nan.any() and (~nan).any()
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+@pytest.mark.parametrize("tg", (8, 16, 32, 64))
+def test_pack_staged_groups_bit_exact(tg, dtype):
+    """The G64 encode that keeps each group's rows in LDS (16-bit keys,
+    token groups of at most 64), through the C-ABI: every fill level of the
+    last group, keys at a head stride wider than their rows, packed rows
+    written at an offset; rows outside the written range keep their fill."""
+    for n_last in (1, tg // 2 + 1, tg):
+        tokens, offset = 2 * tg + n_last, 3
+        buf = _special_keys(dtype, 3, tokens + 5, seed=tg + n_last)
+        keys = buf[:, :tokens]  # head stride (tokens + 5) rows
+        cap = tokens + offset + 2
+        planes = (torch.full((3, cap, 4), -7, dtype=torch.int32, device=DEV),
+                  torch.full((3, cap, 4), -7, dtype=torch.int32, device=DEV),
+                  torch.full((3, cap, 2), 1.5, dtype=torch.float16, device=DEV),
+                  torch.full((3, cap, 2), 1.5, dtype=torch.float16, device=DEV))
+        with torch.cuda.device(DEV):
+            _native.call("popkv_pack", keys.data_ptr(), _native.dtype_code(keys), 3, tokens, 128, buf.stride(0),
+                         *(t.data_ptr() for t in planes), cap, offset, tg, 64, _native.stream_of(DEV))
+        want = core.pack_keys(f32(keys.contiguous()), token_group_size=tg, dim_group_size=64)
+        for a, b, fill in zip(planes, want, (-7, -7, 1.5, 1.5)):
+            got = bits(a)
+            assert np.array_equal(got[:, :offset], bits(torch.full_like(a[:, :offset], fill)))
+            assert np.array_equal(got[:, offset + tokens:], bits(torch.full_like(a[:, offset + tokens:], fill)))
+            mid = got[:, offset:offset + tokens]
+            if a.dtype == torch.int32:
+                assert np.array_equal(mid, b)
+            else:
+                nan = (b & 0x7C00 == 0x7C00) & (b & 0x03FF != 0)
+                assert np.array_equal(mid[~nan], b[~nan])
+                assert np.all((mid[nan] & 0x7C00 == 0x7C00) & (mid[nan] & 0x03FF != 0))
+
+
 @pytest.mark.parametrize("tg", (8, 16, 32, 64, 128))
 def test_incremental_cache_crosses_every_token_group_boundary(tg):
     """tests/test_popkv.py:354-372 on the HIP path, bit-exact."""
