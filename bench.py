@@ -7,9 +7,9 @@
 A "step" is one sparse layer's retrieval step at configuration C1 (PopKV-S,
 Llama-3.1-8B shapes: 32 query heads / 8 KV heads, head_dim 128, 32K context,
 budget 4096, bf16 K/V): query encode + popcount score over 32767 cached
-tokens + per-head top-4095 + current token + 256-token split sparse
-attention with the log-sum-exp merge -- one ``popkv_layer_step`` C-ABI call
-(four kernels), replayed from a HIP graph.  Inputs are resident in HBM; eight
+tokens + per-head top-4095 + current token + sparse attention over 2048-token
+chunks with the log-sum-exp merge -- one ``popkv_layer_step`` C-ABI call
+(three kernels), replayed from a HIP graph.  Inputs are resident in HBM; eight
 independent K/V + metadata sets (about 1.1 GB) rotate so the 256 MB MALL
 cannot hold the working set.
 
@@ -19,7 +19,10 @@ algorithmic HBM GB/s of the step, per-stage kernel times of the layer step
 kernel (the layer step's select + sparse attention), the achievable
 stream-copy bandwidth, and a CPU baseline (the torch-CPU counterpart of the
 reference's readable path on every host thread, a bounded sample of the same
-workload).  ``value`` is the median of --trials trials, each exactly --steps
+workload).  Beside them: the prepack of the prefix, the standalone append,
+one whole decode layer (the step plus the append of the current token, one
+``popkv_decode_layer_batched`` call at B = 1) and the reference-API stages.
+``value`` is the median of --trials trials, each exactly --steps
 consecutive layer steps replayed from one HIP graph.
 """
 from __future__ import annotations
@@ -430,6 +433,35 @@ def main() -> int:
     prepack_bytes = w.kv_heads * L * (w.head_dim * 2 + meta_row)
     append_bytes = w.kv_heads * int(active.shape[1]) * (w.head_dim * 2 + meta_row)
 
+    # ---- one whole decode layer: the step plus the append of the current
+    #      token (its K/V rows into static caches, its active token group
+    #      re-encoded in place), one popkv_decode_layer_batched call at B = 1
+    #      whose append runs in extra workgroups of the select + attention
+    #      launch; the same N_BUFFERS rotation (the lengths are not advanced,
+    #      so every call appends the same token at row L)
+    from popkv_amd import batch as pb
+    dsets = []
+    for pk, pv, _ in sets:
+        kc = torch.zeros(1, w.kv_heads, L + 64, w.head_dim, dtype=pk.dtype, device=dev)
+        vc = torch.zeros_like(kc)
+        kc[0, :, :L] = pk
+        vc[0, :, :L] = pv
+        lengths1 = pb.SequenceLengths.create([L], dev)
+        dsets.append((pb.build_batched_popkv_cache(kc, vc, lengths1, group_size=w.token_group,
+                                                   dim_group_size=w.dim_group), lengths1, torch.empty_like(q)[None]))
+    dws = popkv.LayerStepWorkspace()
+    q1, k1, v1 = q[None].contiguous(), cur_k[None].contiguous(), cur_v[None].contiguous()
+
+    def decode_layer(i: int) -> None:
+        cache1, lengths1, out1 = dsets[i % N_BUFFERS]
+        pb.popkv_layer_step_batched(q1, cache1, lengths1, k1, v1, mapping, budget=w.budget, workspace=dws,
+                                    out=out1, append=True)
+
+    for i in range(N_BUFFERS):
+        decode_layer(i)
+    decode_ms = timed(decode_layer, aux_reps * N_BUFFERS) if args.no_graph else graph_timed(decode_layer, aux_reps)
+    del dsets
+
     # ---- reference-API stages (the entry points popkv_cuda / topk /
     #      sparse_kernels expose, same inputs), for comparison with the
     #      reference's per-stage numbers
@@ -494,6 +526,7 @@ def main() -> int:
                     "GBps": round(prepack_bytes / (prepack_ms * 1e-3) / 1e9, 1)},
         "append": {"active_tokens": int(active.shape[1]), "us": round(append_ms * 1e3, 3),
                    "algorithmic_bytes": append_bytes, "GBps": round(append_bytes / (append_ms * 1e-3) / 1e9, 1)},
+        "decode_layer_with_append_us": round(decode_ms * 1e3, 3),
         "unique_kv_rows_per_step": unique_rows,
         "roofline": {"bound": "hbm", "kernel": "attn_select_chunk_kernel (layer step select + attention)",
                      "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

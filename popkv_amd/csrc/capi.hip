@@ -530,13 +530,20 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
     float* partials = reinterpret_cast<float*>(ws + L.partials);
     hipStream_t s = as_stream(stream);
     // the same three kernels as popkv_layer_step, every row at its own
-    // sequence's token count (see popkv::SeqTable)
-    st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
-                                               static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
-                                               static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
-                                               max_tokens, dim_group_size, keys, L.score_stride, hist, seq, s),
-                  "popkv_layer_step_batched(score)");
-    if (st) return st;
+    // sequence's token count (see popkv::SeqTable).  With budget - 1 >=
+    // max_tokens every sequence selects all its cached tokens (its count is
+    // at most the bound), so, as in popkv_layer_step, the scorer and the
+    // chunk histograms are skipped and every select + attention workgroup
+    // takes its every-token (or, for an empty sequence, no-token) path.
+    if (L.k < max_tokens) {
+        st = launched(popkv::launch_score_d128_raw(queries, dtype, k_sign, k_mag,
+                                                   static_cast<const uint16_t*>(k_low),
+                                                   static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
+                                                   static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
+                                                   max_tokens, dim_group_size, keys, L.score_stride, hist, seq, s),
+                      "popkv_layer_step_batched(score)");
+        if (st) return st;
+    }
     auto clear_hist = [&](int status) {
         (void)popkv::launch_fill_u32(hist, rows * 256, 0u, s);
         return status;

@@ -163,6 +163,40 @@ def test_batched_layer_step_ragged_lengths(g, tg):
         lengths.advance()
 
 
+@pytest.mark.parametrize("append", [False, True])
+def test_batched_step_within_budget_and_past_it(append):
+    """A batch whose every sequence is within the budget (lengths 700, 1, 0,
+    1022 at budget 1024: the launch bound 1022 <= k, so the scorer and the
+    chunk histograms are skipped and every sequence selects all its tokens),
+    then a batch past it on the same workspace (the scorer runs), then the
+    first again: each call against the oracle; with the fused append, the
+    new rows and the re-encoded planes too."""
+    qh, kvh, rows, budget, g, tg = 32, 8, 3000, 1024, 64, 64
+    mapping = torch.arange(qh, device=DEV) // (qh // kvh)
+    ws = pb.LayerStepWorkspace()
+    runs = []
+    for starts, seed in (([700, 1, 0, 1022], 91), ([2900, 1, 0, 1500], 92)):
+        keys, values = _seq_data(len(starts), kvh, rows, seed=seed)
+        kc, vc = keys.to(DEV), values.to(DEV)
+        lengths = pb.SequenceLengths.create(starts, DEV)
+        cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g)
+        gq = torch.Generator().manual_seed(seed)
+        q = torch.randn(len(starts), qh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+        ck = torch.randn(len(starts), kvh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+        cv = torch.randn(len(starts), kvh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+        runs.append((cache, lengths, q, ck, cv))
+    for cache, lengths, q, ck, cv in (runs[0], runs[1], runs[0]):
+        out, idx = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, workspace=ws,
+                                               return_indices=True, append=append)
+        _check_batch(q, cache, lengths, ck, cv, mapping, budget, out, idx)
+        if append:
+            for b, n in enumerate(lengths.host):
+                assert torch.equal(cache.key_cache[b, :, n], ck[b]) and torch.equal(cache.value_cache[b, :, n], cv[b])
+                want = core.pack_keys(f32(cache.key_cache[b, :, :n + 1]), token_group_size=tg, dim_group_size=g)
+                for a, w in zip(_packed_np(cache, b), want):
+                    assert np.array_equal(a[:, :n + 1], w), (b, n)
+
+
 def test_batched_step_graph_replays_follow_growing_lengths():
     """One decode step -- layer step, fused append, lengths += 1 -- captured
     once in a HIP graph, then replayed three times with new tokens copied in
