@@ -571,12 +571,12 @@ __device__ __forceinline__ void chunk_head_of_block(int id, int nchunks, int qpk
     if (kv_groups) {
         const int per = nchunks * qpk;
         const int j = id >> 3;
-        const int g = j / per, within = j - g * per;
-        *c = within / qpk;
+        const int g = div_nonneg(j, per), within = j - g * per;
+        *c = div_nonneg(within, qpk);
         *h = ((g << 3) + (id & 7)) * qpk + (within - *c * qpk);
     } else {
-        *c = id % nchunks;
-        *h = id / nchunks;
+        *h = div_nonneg(id, nchunks);
+        *c = id - *h * nchunks;
     }
 }
 
@@ -671,7 +671,7 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     int64_t b = 0;
     int hl = h;
     if constexpr (SEQ) {
-        b = h / seq.q_heads;
+        b = div_nonneg(h, seq.q_heads);
         hl = h - static_cast<int>(b) * seq.q_heads;
     }
 

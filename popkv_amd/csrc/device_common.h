@@ -129,6 +129,14 @@ __device__ __forceinline__ uint32_t order_key(uint32_t h) {
     return nan ? 0xffffu : k;
 }
 
+// n / d for n >= 0, d > 0 (uniform values): a shift when d is a power of two
+// -- the usual head, group and chunk counts -- instead of the integer
+// division sequence (a float reciprocal and about twenty scalar steps).
+__device__ __forceinline__ int div_nonneg(int n, int d) {
+    if ((d & (d - 1)) == 0) return n >> __builtin_ctz(static_cast<unsigned>(d));
+    return n / d;
+}
+
 // Raw storage of 8 consecutive elements: one 16-byte packet for 16-bit types,
 // two for float32.  Rows stay packed in registers until they are consumed.
 template <typename T> struct Raw8 {

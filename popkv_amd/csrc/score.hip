@@ -353,23 +353,24 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     // for the select kernel.
     constexpr bool STEP = !std::is_void_v<QT>;
     const int qpk = QPK > 0 ? QPK : qpk_rt;
-    const int64_t grow = blockIdx.y;
-    const int64_t b = grow / kv_heads;
-    const int64_t slot = grow % kv_heads;
-    const int64_t qh0 = slot * qpk;
-    // A mapping outside [0, kv_heads) is clamped, never dereferenced.
-    const int64_t kvh = min(max(head_to_kv[qh0], static_cast<int64_t>(0)), static_cast<int64_t>(kv_heads - 1));
+    // block row (sequence b, KV group slot): 32-bit arithmetic, the grid's
+    // y extent being below 2^31
+    const int grow = static_cast<int>(blockIdx.y);
+    const int bi = div_nonneg(grow, kv_heads);
+    const int slot = grow - bi * kv_heads;
+    const int64_t b = bi;
+    const int64_t qh0 = static_cast<int64_t>(slot) * qpk;
     const int64_t qrow0 = b * q_heads + qh0;
-    // packed rows of this KV head (a batched step gives each sequence its own
-    // cache; the reference's batch shares one), and the tokens scored: a
-    // batched step's sequences end at their own counts (the loads below stay
-    // within the launch bound `tokens`, the stores within the sequence's)
-    const int64_t cbase = b * seq.cache_rows + kvh * cap;
-    const int64_t ntok_b = seq.tokens != nullptr ? seq_tokens_of(seq, b, tokens) : tokens;
 
-    // Load order matters: loads retire in issue order (vmcnt), so the raw
-    // query values the encode needs are loaded first, then this thread's
-    // token rows, whose latency then overlaps the encode.
+    // Loads, in issue order (they retire in that order, vmcnt): the raw
+    // query values the encode needs; the group's KV mapping and (batched)
+    // the sequence's token count, as vector loads at a lane-opaque zero
+    // offset (as scalar loads their wait would also hold back the query
+    // loads); then this thread's token rows at the KV head the mapping
+    // names for the standard grouping, head_to_kv[qh0] = slot, so that
+    // their latency overlaps the encode.  Once the mapping has arrived, a
+    // group that maps elsewhere (clamped into [0, kv_heads), never
+    // dereferenced outside) loads its rows again.
     constexpr int MAXW = QPK > 0 ? (QPK + kScoreThreads / kWave - 1) / (kScoreThreads / kWave)
                                  : kMaxGroupHeads / (kScoreThreads / kWave);
     float qv[std::is_void_v<QT> ? 1 : MAXW][2];
@@ -384,20 +385,32 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
             qv[i][1] = Elem<QT>::load(src, lane + 64);
         }
     }
+    int z = 0;
+    asm volatile("" : "+v"(z));
+    const int64_t map_v = head_to_kv[qh0 + z];
+    const int64_t ntok_v = seq.tokens != nullptr ? seq.tokens[b + z] : tokens;
     constexpr int TPT = score_tokens_per_thread<G>();
     using RepWord = std::conditional_t<R == 2, uint32_t, std::conditional_t<R == 4, uint2, uint4>>;
     uint4 s4[TPT], m4[TPT];
     RepWord lw[TPT], dw[TPT];
     int64_t tok[TPT];
+    // packed rows of KV head kvh (a batched step gives each sequence its own
+    // cache; the reference's batch shares one); the loads stay within the
+    // launch bound `tokens`, the stores below within the sequence's count
+    auto load_tokens = [&](int64_t kvh) {
+        const int64_t cbase = b * seq.cache_rows + kvh * cap;
 #pragma unroll
-    for (int it = 0; it < TPT; ++it) {
-        tok[it] = (static_cast<int64_t>(blockIdx.x) * TPT + it) * kScoreThreads + threadIdx.x;
-        const int64_t krow = cbase + min(tok[it], tokens - 1);
-        s4[it] = k_sign[krow];
-        m4[it] = k_mag[krow];
-        lw[it] = reinterpret_cast<const RepWord*>(k_low)[krow];
-        dw[it] = reinterpret_cast<const RepWord*>(k_delta)[krow];
-    }
+        for (int it = 0; it < TPT; ++it) {
+            const int64_t krow = cbase + min(tok[it], tokens - 1);
+            s4[it] = k_sign[krow];
+            m4[it] = k_mag[krow];
+            lw[it] = reinterpret_cast<const RepWord*>(k_low)[krow];
+            dw[it] = reinterpret_cast<const RepWord*>(k_delta)[krow];
+        }
+    };
+#pragma unroll
+    for (int it = 0; it < TPT; ++it) tok[it] = (static_cast<int64_t>(blockIdx.x) * TPT + it) * kScoreThreads + threadIdx.x;
+    load_tokens(slot);
 
     __shared__ GroupState<G> st;
     __shared__ uint32_t s_hist[STEP ? (QPK > 0 ? QPK : kMaxGroupHeads) : 1][256];
@@ -411,6 +424,12 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
         __shared__ __align__(16) float hi_c[QPK > 0 ? QPK : kMaxGroupHeads][128];
         encode_group_fold<G, MAXW>(qv, qpk, st, lo_c, hi_c);
     }
+    {
+        const int m = __builtin_amdgcn_readfirstlane(static_cast<int>(min(max(map_v, static_cast<int64_t>(0)),
+                                                                          static_cast<int64_t>(kv_heads - 1))));
+        if (m != slot) load_tokens(m);
+    }
+    const int64_t ntok_b = min(max(ntok_v, static_cast<int64_t>(0)), tokens);
 
     // Token-side operands, decoded once and reused for every head.
     uint32_t ks[TPT][4], km[TPT][4];

@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_hist_kernel(const uint16_
     uint32_t cnt[4];
     load_rank4(ghist + static_cast<int64_t>(h) * kBins, cnt);
     if (seq.tokens != nullptr) {  // a batched step: this row's own token count and k
-        ntok = static_cast<int>(seq_tokens_of(seq, h / seq.q_heads, ntok));
+        ntok = static_cast<int>(seq_tokens_of(seq, div_nonneg(h, seq.q_heads), ntok));
         k = min(seq.budget - 1, ntok);
         if (k <= 0 || k >= ntok || c * CH >= ntok) return;
     }
