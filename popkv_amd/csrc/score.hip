@@ -182,7 +182,8 @@ __device__ __forceinline__ int neg_opaque(int p) {
 //   ck  = 2*popc(m & km) - popc(km)
 //   cqk = 2*popc(m & qm & km) - popc(qm & km)
 // with popc(qm & km) - G counted as popc(~(qm & km)) down from -G, so each
-// count is one accumulating popcount per word and one shift-add.
+// count is one accumulating popcount per word and one shift-add; cs is
+// finished as a float by one fma (see below), the others are converted.
 // npq = -popc(query mag bits of r), npk = -popc(key mag bits of r): they
 // depend on one side only and are formed once per head / token by the caller.
 template <int G>
@@ -191,6 +192,8 @@ __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm
                                           float kl, float dk) {
     constexpr int NW = G == 64 ? 2 : 1;
     const int w0 = G == 64 ? 2 * r : (G == 32 ? r : r / 2);
+    // a counts up from the bit pattern of 2^23, so that as a float it reads
+    // 2^23 + popc(m) exactly (the count sits in the low mantissa bits)
     int a = 0, aq = 0, ak = 0, aqk = 0, nb = -G;
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
@@ -198,7 +201,7 @@ __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm
         const uint32_t sel = G == 16 ? rep_mask<16>(r, w) : 0xffffffffu;
         const uint32_t m = ~(qs[w] ^ ks[w]) & sel;
         if (i == 0) {
-            a = __popc(m);
+            a = popc_acc(m, 0x4b000000);
             aq = __popc(m & qm[w]);
             ak = __popc(m & km[w]);
             aqk = __popc(m & qm[w] & km[w]);
@@ -210,8 +213,12 @@ __device__ __forceinline__ float rep_term(const uint32_t* qs, const uint32_t* qm
         }
         nb = popc_acc(~(qm[w] & km[w]) & sel, nb);  // popc(~both) - G = -popc(both)
     }
-    const int cs = 2 * a - G, cq = 2 * aq + npq, ck = 2 * ak + npk, cqk = 2 * aqk + nb;
-    return fmaf(ql * kl, static_cast<float>(cs),
+    // cs = 2 popc(m) - G as a float: 2 (2^23 + popc) - (2^24 + G) in one fma,
+    // exact (both operands are exact and so is the small integer result, +0
+    // for 0) -- the count's add-shift and conversion in one instruction
+    const float cs = fmaf(__int_as_float(a), 2.0f, -(16777216.0f + static_cast<float>(G)));
+    const int cq = 2 * aq + npq, ck = 2 * ak + npk, cqk = 2 * aqk + nb;
+    return fmaf(ql * kl, cs,
                 fmaf(dq * kl, static_cast<float>(cq),
                      fmaf(ql * dk, static_cast<float>(ck), dq * dk * static_cast<float>(cqk))));
 }
