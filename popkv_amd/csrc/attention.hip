@@ -632,6 +632,8 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq,
     const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out, StepAppendArgs<T> apx) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
+    args_in_sgprs(q, kc, vc, k_hs, v_hs, keys, key_stride, ntok, k, rec, h2, gt1, nchunks, qpk,
+                  static_cast<int>(kv_groups), head_to_kv, kv_heads);
     int block = static_cast<int>(blockIdx.x);
     if constexpr (SEQ) {
         // The decode step's append: nothing below reads what it writes (the

@@ -129,6 +129,20 @@ __device__ __forceinline__ uint32_t order_key(uint32_t h) {
     return nan ? 0xffffu : k;
 }
 
+// Makes the given kernel arguments live in scalar registers at this point,
+// so that the compiler loads them in one batch -- one scalar-cache round
+// trip -- before it; left to itself it loads a few, waits, computes with
+// them and loads the rest in a second batch, all before a kernel's first
+// memory loads can be issued.
+template <typename A>
+__device__ __forceinline__ void arg_in_sgprs(const A& a) {
+    asm volatile("" : : "s"(a));
+}
+template <typename... A>
+__device__ __forceinline__ void args_in_sgprs(const A&... a) {
+    (arg_in_sgprs(a), ...);
+}
+
 // n / d for n >= 0, d > 0 (uniform values): a shift when d is a power of two
 // -- the usual head, group and chunk counts -- instead of the integer
 // division sequence (a float reciprocal and about twenty scalar steps).

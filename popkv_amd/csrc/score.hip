@@ -359,6 +359,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     // histogram of the keys' high byte is accumulated into ghist[row][256]
     // for the select kernel.
     constexpr bool STEP = !std::is_void_v<QT>;
+    args_in_sgprs(head_to_kv, k_sign, k_mag, k_low, k_delta, q_heads, kv_heads, qpk_rt, cap, tokens, seq.tokens,
+                  seq.cache_rows);
+    if constexpr (STEP) args_in_sgprs(q_raw);
     const int qpk = QPK > 0 ? QPK : qpk_rt;
     // block row (sequence b, KV group slot): 32-bit arithmetic, the grid's
     // y extent being below 2^31

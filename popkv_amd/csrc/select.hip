@@ -353,6 +353,7 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_hist_kernel(const uint16_
                                                                    uint32_t* __restrict__ gt1, int nchunks,
                                                                    SeqTable seq) {
     constexpr int CH = kChunkThreads * KPT;
+    args_in_sgprs(keys, key_stride, ntok, k, ghist, rec, h2, gt1, nchunks, seq.tokens, seq.q_heads);
     const int c = blockIdx.x;
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
