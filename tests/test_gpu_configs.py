@@ -285,3 +285,21 @@ def test_permuted_head_mapping(g):
     assert np.array_equal(got.cpu().numpy(), idx)
     _assert_attention(o, out)
 
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,context,budget", [(12, 4, 6000, 700), (24, 8, 7000, 1100),
+                                                             (40, 8, 3000, 500)])
+def test_layer_step_head_ratios_and_chunk_counts_not_powers_of_two(q_heads, kv_heads, context, budget):
+    """GQA groups of 3 and 5 query heads and chunk counts that are not powers
+    of two: the block -> (chunk, head) and (sequence, group) divisions take
+    their general path (the power-of-two ones are shifts); scores, indices
+    and attention against the oracle."""
+    w = workloads.Workload("ratio", "popkv-s", q_heads, kv_heads, 128, context, budget, 64, 64, torch.bfloat16,
+                           q_heads + context, True)
+    layer, mapping, cache = _setup(w)
+    sc, idx, out = _oracle(w, layer, mapping, cache)
+    o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(got.cpu().numpy(), idx)
+    err = np.abs(f32(o) - out)
+    assert (err <= ATTN_ATOL + ATTN_RTOL * np.abs(out)).all(), float(err.max())
