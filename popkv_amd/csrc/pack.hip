@@ -203,6 +203,11 @@ __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     constexpr int D = 128;
     static_assert(2 * D * static_cast<int>(sizeof(T)) / 16 <= kWave * pack128_waves<G>(),
                   "one 16-byte slice of the new K/V rows per thread");
+    if constexpr (APPEND)
+        args_in_sgprs(ap.counts, ap.kv_heads, ap.cache_rows, ap.new_k, ap.new_v, ap.key_cache, ap.value_cache, tg,
+                      k_sign, k_mag, k_low, k_delta, cap);
+    else
+        args_in_sgprs(keys, head_stride, tokens, tg, k_sign, k_mag, k_low, k_delta, cap, offset);
     if constexpr (!APPEND) {
         const int64_t kvh = blockIdx.y;
         const int64_t gs = static_cast<int64_t>(blockIdx.x) * tg;

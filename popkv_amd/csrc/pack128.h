@@ -356,7 +356,7 @@ __device__ __forceinline__ void pack128_append(int64_t bh, const AppendArgs<T>& 
                                                uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta,
                                                int64_t cap) {
     constexpr int D = 128;
-    const int64_t count = ap.counts[bh / ap.kv_heads];
+    const int64_t count = ap.counts[div_nonneg(static_cast<int>(bh), ap.kv_heads)];  // (bh < 2^31)
     if (count < 0 || count >= ap.cache_rows || count >= cap) {
         if (ap.status != nullptr && threadIdx.x == 0) *ap.status = 1;
         return;
