@@ -1505,7 +1505,7 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
     // passes.  Measured at C1, select + attention: 8 rows 16.5 us (three
     // passes above 256), 10 rows 15.5 us, 12 rows 16.4 us.
     constexpr int NB = 10;
-    const StepChunks ch = step_chunks(tokens, k);
+    const StepChunks ch = step_chunks(tokens, k, q_heads);
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
     // q_heads: rows of the step (a batched step: B * QH); the placement

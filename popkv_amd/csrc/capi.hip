@@ -60,7 +60,7 @@ StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     StepLayout L{};
     L.k = budget - 1 < tokens ? budget - 1 : tokens;
     L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 128) * 128;
-    L.nchunks = popkv::step_chunks(tokens, L.k).count;
+    L.nchunks = popkv::step_chunks(tokens, L.k, qh).count;
     const size_t nc = static_cast<size_t>(L.nchunks > 0 ? L.nchunks : 1);
     size_t off = 0;
     L.hist = off; off = align_up(off + static_cast<size_t>(qh) * 256 * 4);

@@ -106,7 +106,7 @@ hipError_t launch_attention_merge(const float* partials, int q_heads, int64_t sp
 // Layer-step chunked select + attention (head_dim 128, contiguous rows).
 // Key rows hold radix order keys (rows padded to 128 keys, tokens <=
 // 131072) and ghist[row][256] their high-byte histograms; the rows are cut
-// into step_chunks(tokens, k) chunks.  launch_chunk_hist (for 0 < k <
+// into step_chunks(tokens, k, rows) chunks.  launch_chunk_hist (for 0 < k <
 // tokens only) writes rec[row][4] (threshold bin, count above it),
 // h2[row][chunk][256] (uint16 low-byte histograms of the threshold bin) and
 // gt1[row][chunk] (counts above the bin).  launch_attention_select_chunks

@@ -550,7 +550,7 @@ hipError_t launch_chunk_hist(const uint16_t* keys, int64_t key_stride, int64_t r
                              const uint32_t* ghist, uint32_t* rec, uint16_t* h2, uint32_t* gt1, const SeqTable& seq,
                              hipStream_t stream) {
     if (rows <= 0 || k <= 0 || k >= tokens) return hipSuccess;
-    const StepChunks ch = step_chunks(tokens, k);
+    const StepChunks ch = step_chunks(tokens, k, rows);
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
     dim3 grid(static_cast<unsigned>(ch.count), static_cast<unsigned>(rows)), block(kChunkThreads);
 #define POPKV_CH(KPT)                                                                                          \
@@ -629,13 +629,13 @@ hipError_t launch_topk_select(const uint16_t* scores, int64_t rows, int64_t row_
     uint32_t* rec = reinterpret_cast<uint32_t*>(base + w.rec);
     uint32_t* gt1 = reinterpret_cast<uint32_t*>(base + w.gt1);
     uint16_t* h2 = reinterpret_cast<uint16_t*>(base + w.h2);
-    // chunk_hist_kernel runs for 0 < k < tokens only, on step_chunks(tokens, k)
+    // chunk_hist_kernel runs for 0 < k < tokens only, on step_chunks(tokens, k, rows)
     hipError_t e = launch_chunk_hist(keys, key_stride, rows, tokens, k, ghist, rec, h2, gt1, SeqTable{}, stream);
     if (e != hipSuccess) {
         (void)launch_fill_u32(ghist, rows * kBins, 0u, stream);  // the histograms stay zero between calls
         return e;
     }
-    const StepChunks ch = step_chunks(tokens, k > 0 && k < tokens ? k : tokens);
+    const StepChunks ch = step_chunks(tokens, k > 0 && k < tokens ? k : tokens, rows);
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k < tokens ? k : tokens),
               nc = static_cast<int>(ch.count);
     dim3 grid(static_cast<unsigned>(ch.count), static_cast<unsigned>(rows)), block(kChunkThreads);

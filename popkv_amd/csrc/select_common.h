@@ -151,8 +151,13 @@ __device__ __forceinline__ void load_rank4(const uint32_t* __restrict__ hist, ui
 // kChunkSelected of them.  At most 64 chunks; kpt from kChunkKpt (at most
 // 32 keys per thread).  Measured at C1 (32K tokens, k = 4095) with 10 rows
 // per slot and gather pass: 256 selected per chunk (16 chunks of 2048)
-// 30.5 us per layer step, 192 (22 chunks of 1536) 33.6 us.
+// 30.5 us per layer step, 192 (22 chunks of 1536) 33.6 us.  A step of few
+// rows (query heads x sequences) also gets at least kStepMinBlocks / rows
+// chunks, down to the smallest chunk (256 tokens): with the even-spread rule
+// alone C0 (8 rows, k = 511 of 4095) ran 16 blocks on the GPU's 256 CUs --
+// 17.3 us per step against 16.1 with 16 chunks of 256 tokens.
 constexpr int kChunkSelected = 256;
+constexpr int64_t kStepMinBlocks = 256;
 constexpr int kChunkKpt[] = {1, 2, 4, 6, 8, 12, 16, 24, 32};
 
 struct StepChunks {
@@ -160,12 +165,14 @@ struct StepChunks {
     int64_t tokens_per_chunk, count;
 };
 
-inline StepChunks step_chunks(int64_t tokens, int64_t k) {
+inline StepChunks step_chunks(int64_t tokens, int64_t k, int64_t rows) {
     StepChunks c{1, kChunkThreads, 0};
     if (tokens <= 0) return c;
-    // tokens per chunk wanted: about kChunkSelected selected ones, at least
-    // tokens / 64
+    // tokens per chunk wanted: about kChunkSelected selected ones, few enough
+    // that rows * chunks reaches kStepMinBlocks, at least tokens / 64
     int64_t want = k > 0 ? tokens * kChunkSelected / k : tokens;
+    if (rows > 0 && rows < kStepMinBlocks && want > tokens * rows / kStepMinBlocks)
+        want = tokens * rows / kStepMinBlocks;
     const int64_t floor64 = (tokens + 63) / 64;
     if (want < floor64) want = floor64;
     int kpt = 1;

@@ -175,12 +175,15 @@ def test_c3_context_points(context):
 
 # ------------------------------------------------------------------ chunk plans
 
-def _step_kpt(tokens: int, k: int) -> int:
+def _step_kpt(tokens: int, k: int, rows: int = 32) -> int:
     """Keys per thread of the layer step's chunked select: the plan of
     step_chunks() in csrc/select_common.h (chunks of 256 * kpt tokens holding
-    about 256 selected tokens each, at most 64 chunks)."""
+    about 256 selected tokens each, small enough that rows * chunks reaches
+    256 blocks, at most 64 chunks)."""
     kpts = (1, 2, 4, 6, 8, 12, 16, 24, 32)
     want = tokens * 256 // k if k > 0 else tokens
+    if rows < 256:
+        want = min(want, tokens * rows // 256)
     want = max(want, (tokens + 63) // 64)
     kpt = 1
     for x in kpts:
@@ -192,7 +195,7 @@ def _step_kpt(tokens: int, k: int) -> int:
 
 
 @pytest.mark.parametrize("context,budget,kpt", [(3001, 2001, 1), (8192, 4096, 2), (16384, 4096, 4),
-                                                (28001, 4096, 6), (32768, 2501, 12), (32768, 1101, 24)])
+                                                (28001, 4096, 6), (32768, 2501, 12), (65536, 2501, 24)])
 def test_layer_step_every_chunk_plan(context, budget, kpt):
     """Each keys-per-thread instantiation of the chunk-histogram and the
     fused select + attention kernels that the other tests leave out (8, 16

@@ -479,7 +479,10 @@ def test_layer_step_long_context(context):
 def test_layer_step_batch_laid_along_heads_equals_per_sequence_steps():
     """C4's batching: sequences side by side along the head axis (K/V and
     packed caches [B*KVH, ...], queries [B*QH, D], head i -> KV head i // 4)
-    give exactly the per-sequence results."""
+    give exactly the per-sequence selection, and attention outputs within two
+    bf16 rounding steps of theirs (the chunk plan -- hence the order in which
+    the chunks' partial states are merged -- depends on the step's row count,
+    96 here against 32)."""
     w = workloads.scaled(workloads.C1, context=3000, budget=700)
     seqs = [workloads.make_layer(w, seed=11 + b).to(DEV) for b in range(3)]
     mapping = workloads.head_to_kv(w, DEV)
@@ -500,7 +503,8 @@ def test_layer_step_batch_laid_along_heads_equals_per_sequence_steps():
                                       keys[:, L].contiguous(), values[:, L].contiguous(), bmap, budget=w.budget,
                                       return_indices=True)
     assert torch.equal(idx, torch.cat([i for _, i in singles], 0))
-    assert torch.equal(out, torch.cat([o for o, _ in singles], 0))
+    ref = torch.cat([o for o, _ in singles], 0).float()
+    assert ((out.float() - ref).abs() <= 2.0 ** -7 * ref.abs() + 1e-4).all()
 
 
 @pytest.mark.parametrize("context,dtype", [(3000, torch.bfloat16), (700, torch.float32), (1, torch.bfloat16),
