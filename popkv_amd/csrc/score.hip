@@ -228,7 +228,8 @@ constexpr int kScoreThreads = 512;  // 8 waves: 1024 tokens x one GQA group per 
 // per-head state reads and the in-kernel encode are amortised over more
 // tokens), one for G32 / G16 (longer per-token work: more waves hide it
 // better).  Measured at 32K tokens: G64 7.4 vs 7.6 us, G32 8.4 vs 8.5 us,
-// G16 11.6 vs 12.4 us.
+// G16 11.6 vs 12.4 us (again with the fma-finished count: the C2 layer step
+// 29.1 vs 30.2 us, two tokens taking 160 VGPRs).
 template <int G> constexpr int score_tokens_per_thread() { return G == 64 ? 2 : 1; }
 constexpr int kMaxGroupHeads = 64;  // query heads per KV head the LDS stage holds
 
