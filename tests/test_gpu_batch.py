@@ -197,13 +197,15 @@ def test_batched_step_within_budget_and_past_it(append):
                     assert np.array_equal(a[:, :n + 1], w), (b, n)
 
 
-def test_batched_step_graph_replays_follow_growing_lengths():
+@pytest.mark.parametrize("starts", [[3000, 1500, 2200], [300, 150, 220]])
+def test_batched_step_graph_replays_follow_growing_lengths(starts):
     """One decode step -- layer step, fused append, lengths += 1 -- captured
     once in a HIP graph, then replayed three times with new tokens copied in
     between: every replay's output and indices match the oracle at that
-    replay's lengths (the counts are read on the device)."""
-    starts = [3000, 1500, 2200]
-    batch, qh, kvh, rows, budget, g, tg = 3, 32, 8, 3100, 512, 64, 64
+    replay's lengths (the counts are read on the device).  The second batch
+    stays within the budget, so the captured step has no scorer launch."""
+    batch, qh, kvh, budget, g, tg = 3, 32, 8, 512, 64, 64
+    rows = max(starts) + 100
     keys, values = _seq_data(batch, kvh, rows, seed=17)
     kc = torch.zeros(batch, kvh, rows, 128, dtype=torch.bfloat16, device=DEV)
     vc = torch.zeros_like(kc)
@@ -219,8 +221,8 @@ def test_batched_step_graph_replays_follow_growing_lengths():
     ck = torch.empty(batch, kvh, 128, dtype=torch.bfloat16, device=DEV)
     cv = torch.empty_like(ck)
     out = torch.empty_like(q)
-    idx = torch.empty(batch, qh, budget, dtype=torch.int64, device=DEV)
     bound = max(starts) + 8
+    idx = torch.empty(batch, qh, min(budget - 1, bound) + 1, dtype=torch.int64, device=DEV)
 
     def step():
         o, i = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, max_tokens=bound,
@@ -339,8 +341,8 @@ def test_decode_layer_equals_step_then_append():
     cache, lengths = fresh()
     ws = pb.LayerStepWorkspace()
     out = torch.empty_like(q)
-    idx = torch.empty(batch, qh, budget, dtype=torch.int64, device=DEV)
     bound = max(starts) + 8
+    idx = torch.empty(batch, qh, min(budget - 1, bound) + 1, dtype=torch.int64, device=DEV)
 
     def step():
         _, i = pb.popkv_layer_step_batched(q, cache, lengths, ck, cv, mapping, budget=budget, max_tokens=bound,
