@@ -27,9 +27,10 @@ _i64 = ctypes.c_int64
 _int = ctypes.c_int
 
 
-def build() -> Path:
-    """Compile the oracle with its Makefile (gcc, IEEE binary32)."""
-    subprocess.run(["make", "-s", "-C", str(_DIR), "libpopkv_oracle.so"], check=True)
+def build(force: bool = False) -> Path:
+    """Compile the oracle with its Makefile (gcc, IEEE binary32); with
+    ``force`` even when the library is newer than its source."""
+    subprocess.run(["make", "-s"] + (["-B"] if force else []) + ["-C", str(_DIR), "libpopkv_oracle.so"], check=True)
     return _LIB_PATH
 
 
