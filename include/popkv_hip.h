@@ -182,8 +182,10 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Batched decode step of one sparse layer over B independent sequences of
- * different lengths, head_dim 128, in one call (the same four kernels as
- * popkv_layer_step, every row at its own sequence's shape).  Layouts, all
+ * different lengths, head_dim 128, in one call (the same three kernels as
+ * popkv_layer_step, every row at its own sequence's shape; with
+ * budget - 1 >= max_tokens every sequence selects all its cached tokens and
+ * only the select + attention kernel runs).  Layouts, all
  * contiguous:
  *   queries, output        [B, QH, 128]       (dtype)
  *   k_sign/k_mag           [B, KVH, capacity, 4]    int32
@@ -247,7 +249,7 @@ int popkv_append(const void* new_k, const void* new_v, int32_t dtype,
 /* One layer of a batched decode step: popkv_layer_step_batched followed by
  * popkv_append of the current token (new_k/new_v = current_k/current_v,
  * token_group_size, status as for popkv_append), with the same results as
- * the two calls in that order, in three kernels instead of four: the
+ * the two calls in that order, with one launch fewer than the two: the
  * append runs in extra workgroups of the select + attention launch, beside
  * the selection and the attention (neither reads what the append writes:
  * the static caches' rows at the counts, the active groups' packed rows).
