@@ -8,10 +8,11 @@ static K/V cache append (popkv.py:105-111, :964-972), ``_append_current`` /
 ``_sparse_layer_indices`` (popkv.py:283-291), and the PopKV branch of
 ``LlamaSparseDecoder.decode`` (popkv.py:1076-1115) as ``popkv_retrieval_step``.
 
-``popkv_layer_step`` is the same step as one C-ABI call (four kernels:
+``popkv_layer_step`` is the same step as one C-ABI call (three kernels:
 encode + score with per-head key histograms, per-chunk histograms of the
-threshold bin, per-chunk select + sparse attention, log-sum-exp merge with
-the current token).
+threshold bin, per-chunk select + sparse attention whose last workgroup per
+head does the log-sum-exp merge with the current token; with k >= tokens
+only the last).
 """
 from __future__ import annotations
 
