@@ -174,7 +174,9 @@ def bench_c4(args) -> int:
     device-side length) and the fused append (the new token's K/V rows into
     the static caches and the re-encode of each sequence's active token
     group, read in place), the append running in extra workgroups of the
-    step's select + attention launch.  The replays repeat
+    step's select + attention launch.  The appended (current) token is
+    N(0,1) (workloads.new_tokens), the prefixes follow the C1 distribution
+    with seed 123 + b.  The replays repeat
     the same token position (the lengths are not advanced inside the timed
     graph; advancing them is one 8-element add per decode step, not per
     layer).  The one-time prepack of the eight 64K prefixes is timed on its
@@ -196,12 +198,13 @@ def bench_c4(args) -> int:
     qs = []
     for b in range(B):
         lay = workloads.make_layer(w, seed=w.seed + b)
-        kc0[b, :, :L + 1] = lay.keys.to(dev)
-        vc0[b, :, :L + 1] = lay.values.to(dev)
+        kc0[b, :, :L] = lay.keys[:, :L].to(dev)
+        vc0[b, :, :L] = lay.values[:, :L].to(dev)
         qs.append(lay.queries)
         del lay
     q = torch.stack(qs).to(dev)
-    cur_k, cur_v = kc0[:, :, L].clone(), vc0[:, :, L].clone()
+    # the token the timed step appends (and attends as the current one): N(0,1)
+    cur_k, cur_v = (t.to(dev) for t in workloads.new_tokens(w, 0))
     for i in range(n_sets):
         kc, vc = (kc0, vc0) if i == 0 else (kc0.clone(), vc0.clone())
         lengths = pb.SequenceLengths.create([L] * B, dev)
@@ -264,7 +267,7 @@ def bench_c4(args) -> int:
         "value": round(step_ms * 1e3, 3), "unit": "us/step-layer", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 6), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded per sequence; outlier-channel K, peaked Q; resident in HBM)",
+        "data": "synthetic (seeded per sequence; outlier-channel K, peaked Q, N(0,1) decode token; resident in HBM)",
         "config": {"workload": w.name, "method": w.method, "batch": B, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
                    "head_dim": w.head_dim, "context": w.context, "budget": w.budget, "rotating_buffers": n_sets,
                    "timing": "hip-graph replay, median of trials"},

@@ -253,6 +253,10 @@ int popkv_append(const void* new_k, const void* new_v, int32_t dtype,
  * append runs in extra workgroups of the select + attention launch, beside
  * the selection and the attention (neither reads what the append writes:
  * the static caches' rows at the counts, the active groups' packed rows).
+ * A sequence whose device count lies outside [0, max_tokens] is stepped
+ * at the clamped count and sets *status |= 2 (status may be NULL): a
+ * captured step replayed past the bound it was captured with reports it
+ * there, so poll status after replays.
  * No counterpart in the reference: it replaces, for one layer, the
  * reference decode loop's retrieval step and append (popkv.py:1076-1115
  * with :438-459 / :883-942 and the static cache write of :964-972) for a

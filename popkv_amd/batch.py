@@ -82,6 +82,47 @@ def _check_static(key_cache: torch.Tensor, value_cache: torch.Tensor) -> None:
         raise ValueError("static K/V caches must share an fp32/fp16/bf16 dtype")
 
 
+def _check_planes(cache: BatchedPopKVCache) -> int:
+    """The packed planes every batched kernel addresses: contiguous int32
+    sign/mag [B, KVH, cap, 4] and fp16 low/delta [B, KVH, cap, 128/G], with
+    the static caches' batch and KV head counts and one capacity
+    (ValueError; devices are checked by _check_on_device after the
+    host-side checks).  Returns the planes' capacity."""
+    _check_static(cache.key_cache, cache.value_cache)
+    if cache.dim_group_size not in (16, 32, 64):
+        raise ValueError("dim_group_size must be one of 16, 32, 64")
+    if not 1 <= cache.group_size <= MAX_TOKEN_GROUP_SIZE:
+        raise ValueError(f"Pop-KV group_size must be between 1 and {MAX_TOKEN_GROUP_SIZE}")
+    if len(cache.packed) != 4:
+        raise ValueError("packed must contain (k_sign, k_mag, k_low, k_delta)")
+    batch, kv_heads = (int(x) for x in cache.key_cache.shape[:2])
+    sign = cache.packed[0]
+    cap = int(sign.shape[2]) if sign.ndim == 4 else -1
+    reps = 128 // cache.dim_group_size
+    for t, dt, width, what in zip(cache.packed, (torch.int32, torch.int32, torch.float16, torch.float16),
+                                  (4, 4, reps, reps), ("k_sign", "k_mag", "k_low", "k_delta")):
+        if tuple(t.shape) != (batch, kv_heads, cap, width) or cap <= 0:
+            raise ValueError(f"packed {what} must be [{batch}, {kv_heads}, capacity, {width}], got {tuple(t.shape)}")
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"packed {what} must be a contiguous {dt} tensor")
+    return cap
+
+
+def _check_on_device(cache: BatchedPopKVCache, lengths: SequenceLengths, *tensors: torch.Tensor | None) -> None:
+    """The device token counts (a contiguous int64 [B]), the static caches,
+    the packed planes and every operand on one CUDA device: the kernels
+    dereference them all (RuntimeError, as the reference's TORCH_CHECKs)."""
+    if lengths.device.dtype != torch.int64 or lengths.device.ndim != 1 or not lengths.device.is_contiguous() \
+            or int(lengths.device.numel()) != lengths.batch:
+        raise ValueError("sequence lengths must be a contiguous int64 [batch] tensor")
+    dev = cache.key_cache.device
+    if dev.type != "cuda":
+        raise RuntimeError("the static caches must be on a CUDA device")
+    for t in (cache.value_cache, lengths.device) + tuple(cache.packed) + tuple(t for t in tensors if t is not None):
+        if t.device != dev:
+            raise RuntimeError(f"every operand must be on the caches' device {dev}, got {t.device}")
+
+
 def build_batched_popkv_cache(key_cache: torch.Tensor, value_cache: torch.Tensor, lengths: SequenceLengths, *,
                               group_size: int, dim_group_size: int) -> BatchedPopKVCache:
     """Prepack each sequence's cached prefix (rows [0, lengths[b]) of its
@@ -102,6 +143,8 @@ def build_batched_popkv_cache(key_cache: torch.Tensor, value_cache: torch.Tensor
         raise RuntimeError("Pop-KV cache capacity exceeded")
     cap = math.ceil(rows / group_size) * group_size
     dev = key_cache.device
+    if dev.type != "cuda" or value_cache.device != dev:
+        raise RuntimeError("the static caches must be on one CUDA device")
     reps = 128 // dim_group_size
     packed = (torch.zeros(batch, kv_heads, cap, 4, dtype=torch.int32, device=dev),
               torch.zeros(batch, kv_heads, cap, 4, dtype=torch.int32, device=dev),
@@ -116,13 +159,14 @@ def prepack_batched(cache: BatchedPopKVCache, lengths: SequenceLengths) -> None:
     """(Re-)encode every sequence's cached prefix into the cache's packed
     planes: one popkv_pack launch per non-empty sequence, reading rows
     [0, lengths[b]) of its static keys in place."""
+    cap = _check_planes(cache)
     batch, kv_heads = (int(x) for x in cache.key_cache.shape[:2])
     if lengths.batch != batch:
         raise ValueError(f"{lengths.batch} lengths for a batch of {batch}")
-    cap = int(cache.packed[0].shape[2])
     if max(lengths.host) > min(cache.capacity, cap):
         raise RuntimeError("Pop-KV cache capacity exceeded")
     dev = cache.key_cache.device
+    _check_on_device(cache, lengths)
     with torch.cuda.device(dev):
         stream = nat.stream_of(dev)
         if len(set(lengths.host)) == 1 and lengths.host[0] > 0:
@@ -158,14 +202,16 @@ def append_batched(cache: BatchedPopKVCache, lengths: SequenceLengths, new_k: to
         raise ValueError(f"new K/V must be [{batch}, {kv_heads}, 128]")
     if lengths.batch != batch:
         raise ValueError(f"{lengths.batch} lengths for a batch of {batch}")
-    if max(lengths.host) >= min(cache.capacity, int(cache.packed[0].shape[2])):
+    cap = _check_planes(cache)
+    if max(lengths.host) >= min(cache.capacity, cap):
         raise RuntimeError("Pop-KV cache reserve exhausted")
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1):
+        raise ValueError("status must be an int32 tensor of at least one element")
     nk, nv = new_k.contiguous(), new_v.contiguous()
     if nk.dtype != cache.key_cache.dtype or nv.dtype != cache.key_cache.dtype:
         raise RuntimeError("new K/V must have the static caches' dtype")
-    if status is not None and (status.dtype != torch.int32 or not status.is_cuda):
-        raise ValueError("status must be a CUDA int32 tensor")
     dev = cache.key_cache.device
+    _check_on_device(cache, lengths, nk, nv, status)
     ks, km, kl, kd = cache.packed
     with torch.cuda.device(dev):
         nat.call("popkv_append", nk.data_ptr(), nv.data_ptr(), nat.dtype_code(nk), cache.key_cache.data_ptr(),
@@ -193,7 +239,12 @@ def popkv_layer_step_batched(q: torch.Tensor, cache: BatchedPopKVCache, lengths:
     caches, with the results of ``append_batched(cache, lengths, k, v,
     status=status)`` after the step, in one C-ABI call
     (popkv_decode_layer_batched) whose append runs in extra workgroups of
-    the step's select + attention launch."""
+    the step's select + attention launch.  With ``append=True``, ``status``
+    (int32, on the cache's device) also gets bit 1 (value 2) when a
+    sequence's device count exceeds ``max_tokens`` (the step then ran on
+    the clamped count): poll it after replaying a captured step.  It is
+    only read with ``append=True``."""
+    cap = _check_planes(cache)
     batch, kv_heads = (int(x) for x in cache.key_cache.shape[:2])
     if q.ndim != 3 or int(q.shape[0]) != batch or int(q.shape[2]) != 128:
         raise ValueError(f"q must be [{batch}, query heads, 128]")
@@ -212,18 +263,19 @@ def popkv_layer_step_batched(q: torch.Tensor, cache: BatchedPopKVCache, lengths:
     bound = max(lengths.host) if max_tokens is None else int(max_tokens)
     if bound < max(lengths.host) or bound < 1:
         raise ValueError("max_tokens must be at least 1 and cover every sequence's length")
-    if bound > min(cache.capacity, int(cache.packed[0].shape[2])):
+    if bound > min(cache.capacity, cap):
         raise RuntimeError("invalid score token count")
     if out is not None and (tuple(out.shape) != tuple(q.shape) or not out.is_contiguous() or out.dtype != q.dtype):
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
     if append:
-        if max(lengths.host) >= min(cache.capacity, int(cache.packed[0].shape[2])):
+        if max(lengths.host) >= min(cache.capacity, cap):
             raise RuntimeError("Pop-KV cache reserve exhausted")
-        if status is not None and (status.dtype != torch.int32 or not status.is_cuda):
-            raise ValueError("status must be a CUDA int32 tensor")
-    dev = q.device
+    if status is not None and (not append or status.dtype != torch.int32 or status.numel() < 1):
+        raise ValueError("status must be an int32 tensor of at least one element, given with append=True")
     if any(t.dtype != q.dtype for t in (k, v, cache.key_cache)):
         raise RuntimeError("queries, current K/V and the static caches must share a dtype")
+    dev = cache.key_cache.device
+    _check_on_device(cache, lengths, q, k, v, out, status)
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
     mapping = head_to_kv.to(device=dev, dtype=torch.int64).contiguous()
     g = cache.dim_group_size

@@ -72,6 +72,23 @@ __device__ __forceinline__ void merge_state(SoftmaxState& a, float m2, float l2,
 // atomics: plain global stores / loads with the device-coherence bit, which
 // go through to memory instead of staying in one XCD's L2, so no L2
 // write-back or invalidate is needed for them.
+// The fused merges hand chunk states from workgroup to workgroup with no
+// release/acquire pair: the states are stored with relaxed agent-scope
+// atomic stores, each wave then waits with "s_waitcnt vmcnt(0)", the block
+// meets at a barrier, and one relaxed agent-scope atomic add takes the
+// ticket; the last block reads the states with relaxed agent-scope atomic
+// loads.  That is correct on gfx942 / gfx950 because (1) an agent-scope
+// atomic store or load is a global store / load with the sc1 bit, which
+// writes through and reads past the XCD's non-coherent L2 to the device's
+// coherence point, and (2) stores count in vmcnt on these targets, so
+// vmcnt(0) returns only once every store of the wave is acknowledged by
+// that point -- before the ticket is taken.  On targets that count stores
+// in a separate vscnt (gfx10 and later) or that cache agent-scope stores,
+// the wait would not cover the states: the build refuses them.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__) && !defined(__gfx942__)
+#error "the fused merge's hand-off relies on gfx942/gfx950 store acknowledgement (vmcnt) and sc1 write-through"
+#endif
+
 template <bool COH>
 __device__ __forceinline__ void st_f32(float* p, float v) {
     if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -385,6 +402,9 @@ __device__ __forceinline__ int64_t merge_kv_row(const SeqTable& seq, const int64
                                                 int kv_heads, int rows, int64_t* idx_slot, int64_t* current) {
     if (seq.tokens != nullptr) {
         const int64_t b = h / seq.q_heads;
+        const int64_t raw = seq.tokens[b];
+        if (seq.status != nullptr && (raw < 0 || raw > *current) && (threadIdx.x & (kWave - 1)) == 0)
+            atomicOr(seq.status, 2);
         *current = seq_tokens_of(seq, b, *current);
         *idx_slot = min(static_cast<int64_t>(seq.budget) - 1, *current);
         return b * seq.kv_heads +
@@ -691,8 +711,11 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     Raw8<T> qr;
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
     const int64_t map = head_to_kv[hl + z];
-    int64_t seq_ntok = ntok;
-    if constexpr (SEQ) seq_ntok = seq_tokens_of(seq, b, ntok);
+    int64_t seq_ntok = ntok, raw_ntok = ntok;
+    if constexpr (SEQ) {
+        raw_ntok = seq.tokens[b];
+        seq_ntok = raw_ntok < 0 ? 0 : (raw_ntok > ntok ? ntok : raw_ntok);
+    }
     uint32_t rank0 = 0;
     uint32_t g2 = 0, p2 = 0;  // bin tid of the chunk histograms over every chunk / over chunks before c
     // The threshold record, bin tid of the first HB chunk histograms and
@@ -714,6 +737,10 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     const uint32_t gx = gt1[static_cast<int64_t>(h) * nchunks + min(lane, nchunks - 1)];
     int nch = nchunks;  // this row's chunks
     if constexpr (SEQ) {
+        // a count outside [0, launch bound] runs clamped and is flagged (by
+        // one block per sequence)
+        if (seq.status != nullptr && c == 0 && hl == 0 && tid == 0 && (raw_ntok < 0 || raw_ntok > ntok))
+            atomicOr(seq.status, 2);
         ntok = static_cast<int>(seq_ntok);
         k = min(seq.budget - 1, ntok);
         nch = (ntok + CH - 1) / CH;
@@ -935,6 +962,9 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     //    (ghist[h][0], zero between calls), and the head's last block --
     //    which sees every other chunk's stores -- merges the chunks and the
     //    current token, resets the ticket and writes the output (one wave).
+    //    The ordering rests on the gfx942/gfx950 rule stated at st_f32:
+    //    this vmcnt(0) covers the sc1 stores, so they have reached the
+    //    coherence point before the barrier and the ticket.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __shared__ uint32_t s_last;

@@ -521,6 +521,7 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
     seq.q_heads = static_cast<int>(q_heads);
     seq.kv_heads = static_cast<int>(kv_heads);
     seq.budget = static_cast<int>(budget < 0x7fffffff ? budget : 0x7fffffff);
+    seq.status = app ? app->status : nullptr;
     char* ws = static_cast<char*>(workspace);
     uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
     uint32_t* rec = reinterpret_cast<uint32_t*>(ws + L.rec);

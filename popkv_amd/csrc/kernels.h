@@ -24,6 +24,9 @@ struct SeqTable {
     int64_t cache_rows = 0;
     int64_t k_bstride = 0, v_bstride = 0;
     int q_heads = 0, kv_heads = 0, budget = 0;
+    // When non-null: the merge sets bit 1 (value 2) when a sequence's count
+    // lies outside [0, bound] (the step then ran on the clamped count).
+    int32_t* status = nullptr;
 };
 
 // n 32-bit words of device memory set to `value` (a fill kernel).

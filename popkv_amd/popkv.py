@@ -413,11 +413,27 @@ def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v
     reads the keys and threshold histograms the step left there and rewrites
     the chunk partials inside the workspace.  A timing aid for the step's
     dominant kernel."""
-    dev = q.device
+    if q.ndim != 2 or int(q.shape[1]) != 128 or not q.is_contiguous():
+        raise ValueError("popkv_layer_step_attention requires a contiguous q [query heads, 128]")
+    if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
+        raise ValueError("prefix K/V must be [KV heads, tokens, 128]")
+    if prefix_k.stride(1) != 128 or prefix_k.stride(2) != 1 or prefix_v.stride(1) != 128 or prefix_v.stride(2) != 1:
+        raise ValueError("prefix K/V rows must be contiguous (token stride 128)")
+    q_heads, kv_heads, tokens = int(q.shape[0]), int(prefix_k.shape[0]), int(prefix_k.shape[1])
+    if q_heads <= 0 or kv_heads <= 0 or q_heads % kv_heads != 0:
+        raise ValueError("query heads must be a positive multiple of the KV heads")
+    if tokens <= 0:
+        raise ValueError("invalid score token count")
+    if budget <= 1:
+        raise ValueError("budget must reserve at least one retrieved and one current token")
+    _check_head_mapping(head_to_kv, q_heads)
     ws = workspace if isinstance(workspace, torch.Tensor) else workspace.buffer
     if ws is None:
         raise ValueError("the workspace has not been used by popkv_layer_step")
-    q_heads, kv_heads, tokens = int(q.shape[0]), int(prefix_k.shape[0]), int(prefix_k.shape[1])
+    _check_same_device("popkv_layer_step_attention", q, prefix_k, prefix_v)
+    if ws.device != q.device:
+        raise RuntimeError("popkv_layer_step_attention: every tensor must be on the same CUDA device")
+    dev = q.device
     mapping = head_to_kv.to(device=dev, dtype=torch.int64).contiguous()
     with torch.cuda.device(dev):
         nat.call("popkv_layer_step_attention", q.data_ptr(), nat.dtype_code(q), prefix_k.data_ptr(),

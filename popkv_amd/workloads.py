@@ -13,9 +13,11 @@ Configurations (by index):
       0.5 * mean of 64 random rows of its KV head's keys + N(0,1).  Seed 42.
   C2  PopKV-Q (TG 128 / G 16) at the same shapes, per layer seed 42 + layer.
   C3  PopKV-S context sweep 4K..128K, budget 4096, seed 7.
-  C4  PopKV-S, 8 sequences x 64K context, budget 4096, seed 123.
-The current token is the last row of K/V; the prefix holds L = context - 1
-tokens.
+  C4  PopKV-S, 8 sequences x 64K context, budget 4096, seed 123 + b for
+      sequence b; the tokens a decode step appends are N(0,1)
+      (``new_tokens``).
+The current token is the last row of K/V (C4: a ``new_tokens`` row); the
+prefix holds L = context - 1 tokens.
 """
 from __future__ import annotations
 
@@ -124,6 +126,18 @@ def make_layer(w: Workload, *, seed: int | None = None) -> LayerInputs:
             rows = torch.randint(0, prefix, (64,), generator=g)
             queries[h] = 0.5 * keys[h // qpk, rows].mean(0) + torch.randn(d, generator=g)
     return LayerInputs(keys.to(w.dtype), values.to(w.dtype), queries.to(w.dtype))
+
+
+def new_tokens(w: Workload, step: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """The N(0,1) key and value rows of the token a batched decode step
+    appends (C4: "the new tokens are N(0,1)"): [batch, KVH, D] each, drawn
+    on the CPU from seed ``w.seed + 10000 + step`` and cast to the workload
+    dtype."""
+    g = torch.Generator().manual_seed(w.seed + 10000 + step)
+    shape = (w.batch, w.kv_heads, w.head_dim)
+    k = torch.randn(shape, generator=g)
+    v = torch.randn(shape, generator=g)
+    return k.to(w.dtype), v.to(w.dtype)
 
 
 def head_to_kv(w: Workload, device=None) -> torch.Tensor:

@@ -12,8 +12,10 @@ CPU oracle.
     oracle's and its attention is within 2e-2 / 1e-2 -- before and after an
     append, and for a decode step captured once in a HIP graph and replayed
     while the device lengths grow.
-  * C4's shape: eight 64K sequences, two of them checked against their own
-    oracles after an append step.
+  * C4 as specified: eight 64K sequences with N(0,1) decode tokens, each
+    checked against its own oracle after an append and a decode layer.
+  * A captured decode layer replayed past its launch bound reports it in
+    its status word.
 """
 from __future__ import annotations
 
@@ -262,42 +264,111 @@ def test_batched_step_graph_replays_follow_growing_lengths(starts):
         assert lengths.device.cpu().tolist() == lengths.host
 
 
+def _c4_sequence_oracle(w, keys, values, q, ck, cv, L):
+    """One C4 sequence's oracle at L cached tokens: selection and attention
+    over its prefix encode, and the encode of the sequence grown by the
+    current token (what the decode layer's append leaves in the planes)."""
+    h2k = workloads.head_to_kv(w).numpy()
+    pk, pv = f32(keys[:, :L]), f32(values[:, :L])
+    pack = core.pack_keys(pk, token_group_size=w.token_group, dim_group_size=w.dim_group)
+    enc = core.query_encode(f32(q)[None], w.dim_group, order="fold")
+    sc = core.score_encoded(enc, pack, head_to_kv=h2k, tokens=L, dim_group_size=w.dim_group)[0]
+    idx = core.select(sc, w.k, L)
+    grown = core.pack_keys(np.concatenate([pk, f32(ck)[:, None]], 1), token_group_size=w.token_group,
+                           dim_group_size=w.dim_group)
+    return grown, idx, core.attention(f32(q), pk, pv, f32(ck), f32(cv), idx, h2k)
+
+
 def test_c4_batch_after_an_append():
-    """C4's shape: eight sequences of 64K (PopKV-S, budget 4096, bf16, the
-    C1 distribution with seed 123 + b).  The prefixes hold 65534 tokens; the
-    append step adds token 65534 (static K/V row and metadata), then one
-    batched step with token 65535 as the current one; sequences 0 and 7 are
-    checked against their own oracles."""
+    """C4 as specified: eight sequences of 64K (PopKV-S, budget 4096, bf16;
+    sequence b's prefix from the C1 distribution with seed 123 + b) whose
+    decode tokens are N(0,1) (workloads.new_tokens).  The prefixes hold
+    65534 tokens; the append adds N(0,1) token 0 (static K/V rows and
+    metadata), then one batched decode layer with N(0,1) token 1 as the
+    current one also appends it.  All eight sequences are checked against
+    their own oracles: indices exact, attention within 2e-2 / 1e-2, and the
+    packed planes of all 65536 tokens after the decode layer's append (which
+    seals the last token group) bit-exact."""
+    from concurrent.futures import ThreadPoolExecutor
+
     w = workloads.C4
-    batch, rows = w.batch, w.context
-    kc = torch.empty(batch, w.kv_heads, rows, 128, dtype=torch.bfloat16, device=DEV)
-    vc = torch.empty_like(kc)
-    qs, cks, cvs = [], [], []
+    batch, rows = w.batch, w.context + 64
+    L = w.prefix_tokens  # 65535 cached tokens once token 0 is appended
+    new_k, new_v = workloads.new_tokens(w, 0)
+    cur_k, cur_v = workloads.new_tokens(w, 1)
+    kc = torch.zeros(batch, w.kv_heads, rows, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    layers = []
     for b in range(batch):
         lay = workloads.make_layer(w, seed=w.seed + b)
-        kc[b] = lay.keys.to(DEV)
-        vc[b] = lay.values.to(DEV)
-        qs.append(lay.queries)
+        keys = torch.cat([lay.keys[:, :L - 1], new_k[b, :, None]], 1)
+        values = torch.cat([lay.values[:, :L - 1], new_v[b, :, None]], 1)
+        kc[b, :, :L - 1] = keys[:, :L - 1].to(DEV)
+        vc[b, :, :L - 1] = values[:, :L - 1].to(DEV)
+        layers.append((keys, values, lay.queries))
         del lay
-    L = w.prefix_tokens  # 65535
-    new_k, new_v = kc[:, :, L - 1].clone(), vc[:, :, L - 1].clone()
-    cur_k, cur_v = kc[:, :, L].clone(), vc[:, :, L].clone()
-    kc[:, :, L - 1:] = 0  # the append writes row L - 1 back; row L stays outside the prefix
-    vc[:, :, L - 1:] = 0
+    with ThreadPoolExecutor(max_workers=8) as pool:  # the C oracle releases the GIL
+        wants = list(pool.map(lambda b: _c4_sequence_oracle(w, *layers[b], cur_k[b], cur_v[b], L), range(batch)))
     lengths = pb.SequenceLengths.create([L - 1] * batch, DEV)
     cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=w.token_group, dim_group_size=w.dim_group)
-    pb.append_batched(cache, lengths, new_k, new_v)
+    pb.append_batched(cache, lengths, new_k.to(DEV), new_v.to(DEV))
     lengths.advance()
-    q = torch.stack(qs).to(DEV)
+    q = torch.stack([t[2] for t in layers]).to(DEV)
     mapping = workloads.head_to_kv(w, DEV)
-    out, idx = pb.popkv_layer_step_batched(q, cache, lengths, cur_k, cur_v, mapping, budget=w.budget,
-                                           return_indices=True)
+    out, idx = pb.popkv_layer_step_batched(q, cache, lengths, cur_k.to(DEV), cur_v.to(DEV), mapping,
+                                           budget=w.budget, return_indices=True, append=True)
     torch.cuda.synchronize()
-    for b in (0, 7):
-        want_pack = core.pack_keys(f32(kc[b, :, :L]), token_group_size=w.token_group, dim_group_size=w.dim_group)
-        for a, wp in zip(_packed_np(cache, b), want_pack):
-            assert np.array_equal(a[:, :L], wp), b
-    _check_batch(q, cache, lengths, cur_k, cur_v, mapping, w.budget, out, idx, check=(0, 7))
+    for b, (grown, want_idx, want_out) in enumerate(wants):
+        assert np.array_equal(idx[b].cpu().numpy(), want_idx), b
+        _assert_attention(out[b], want_out)
+        # the decode layer's own append: token 1 at row L, and the planes of
+        # all L + 1 tokens (its token group now sealed) equal to the oracle's
+        assert torch.equal(kc[b, :, L].cpu(), cur_k[b]) and torch.equal(vc[b, :, L].cpu(), cur_v[b])
+        for a, wp in zip(_packed_np(cache, b), grown):
+            assert np.array_equal(a[:, :L + 1], wp), b
+
+
+def test_decode_layer_flags_counts_past_the_bound():
+    """A captured decode layer replayed past the launch bound it was
+    captured with: the step runs at the clamped count and sets status bit 1
+    (value 2); within the bound the flag stays clear."""
+    starts = [900, 400]
+    batch, qh, kvh, rows, budget, g, tg = 2, 32, 8, 1100, 256, 64, 64
+    keys, values = _seq_data(batch, kvh, rows, seed=41)
+    kc, vc = keys.to(DEV), values.to(DEV)
+    lengths = pb.SequenceLengths.create(starts, DEV)
+    cache = pb.build_batched_popkv_cache(kc, vc, lengths, group_size=tg, dim_group_size=g)
+    mapping = torch.arange(qh, device=DEV) // (qh // kvh)
+    gq = torch.Generator().manual_seed(3)
+    q = torch.randn(batch, qh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+    ck = torch.randn(batch, kvh, 128, generator=gq).to(torch.bfloat16).to(DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ws = pb.LayerStepWorkspace()
+    bound = max(starts) + 1
+    out = torch.empty_like(q)
+
+    def step():
+        pb.popkv_layer_step_batched(q, cache, lengths, ck, ck, mapping, budget=budget, max_tokens=bound,
+                                    workspace=ws, out=out, append=True, status=status)
+        lengths.device.add_(1)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0  # count 900 <= bound 901
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    graph.replay()  # count 901 == bound: still clear
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    graph.replay()  # count 902 > bound 901
+    torch.cuda.synchronize()
+    assert int(status.item()) == 2
+    assert lengths.device.cpu().tolist() == [903, 403]
 
 
 def test_decode_layer_equals_step_then_append():

@@ -160,12 +160,90 @@ def test_c2_stack_dense_and_sparse_layers_eager_and_graph():
         torch.cuda.synchronize()
 
 
+def _c2_layer_case(li: int, dense: tuple[int, ...]):
+    """One C2 layer on the CPU: its bf16 inputs and its oracle -- for a
+    dense layer the attention over every token, for a sparse layer the
+    oracle's own prepack (bit patterns), selection and attention."""
+    w = workloads.c2_layer(li)
+    lay = workloads.make_layer(w)
+    h2k = workloads.head_to_kv(w).numpy()
+    q, pk, pv = f32(lay.queries), f32(lay.prefix_k()), f32(lay.prefix_v())
+    ck, cv = f32(lay.current_k()), f32(lay.current_v())
+    L = lay.prefix_tokens
+    if li in dense:
+        idx = np.tile(np.arange(L + 1, dtype=np.int64), (w.q_heads, 1))
+        return lay, None, None, core.attention(q, pk, pv, ck, cv, idx, h2k)
+    pack = core.pack_keys(pk, token_group_size=w.token_group, dim_group_size=w.dim_group)
+    enc = core.query_encode(q[None], w.dim_group, order="fold")
+    sc = core.score_encoded(enc, pack, head_to_kv=h2k, tokens=L, dim_group_size=w.dim_group)[0]
+    idx = core.select(sc, w.k, L)
+    return lay, pack, idx, core.attention(q, pk, pv, ck, cv, idx, h2k)
+
+
+def test_c2_full_32_layer_stack():
+    """C2 as specified: the whole 32-layer decode step (layers 0-1 dense,
+    2-31 PopKV-Q: TG 128 / G 16, 32K context, budget 4096, bf16, seed
+    42 + layer) through SparseDecodeStack.  Every sparse layer's prepack is
+    bit-exact with the oracle's and its indices equal the oracle's; every
+    layer's output is within 2e-2 / 1e-2 of its own oracle, eagerly and in a
+    captured HIP graph replayed twice."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    n_layers, dense = 32, (0, 1)
+    with ThreadPoolExecutor(max_workers=8) as pool:  # the C oracle releases the GIL
+        cases = list(pool.map(lambda li: _c2_layer_case(li, dense), range(n_layers)))
+    w0 = workloads.c2_layer(0)
+    mapping = workloads.head_to_kv(w0, DEV)
+    ops, caches = [], {}
+    for li, (lay, pack, _, _) in enumerate(cases):
+        lay = lay.to(DEV)
+        ops.append((lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v()))
+        if li not in dense:
+            w = workloads.c2_layer(li)
+            caches[li] = popkv.build_popkv_cache(lay.prefix_k(), group_size=w.token_group,
+                                                 dim_group_size=w.dim_group, reserve_tokens=128)
+    stack = popkv.SparseDecodeStack(caches, mapping, budget=w0.budget, full_layers=dense)
+    outs = [torch.empty_like(o[0]) for o in ops]
+    stack.step(ops, outs)
+    torch.cuda.synchronize()
+    L = w0.prefix_tokens
+    for li, ((_, pack, idx, want), got) in enumerate(zip(cases, outs)):
+        _assert_attention(got, want)
+        if li in dense:
+            continue
+        for a, b in zip(_packed_np(caches[li]), pack):
+            assert np.array_equal(a[:, :L], b), li
+        o, sel = popkv.popkv_layer_step(*ops[li][:1], caches[li], *ops[li][1:], mapping, budget=w0.budget,
+                                        return_indices=True)
+        assert np.array_equal(sel.cpu().numpy(), idx), li
+        assert torch.equal(o, got), li
+    eager = [o.clone() for o in outs]
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        stack.step(ops, outs)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stack.step(ops, outs)
+    for rep in range(2):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, eager)):
+            assert torch.equal(a, b), (rep, i)
+
+
 # ------------------------------------------------------------------ C3
 
-@pytest.mark.parametrize("context", [4096, 8192, 16384])
+@pytest.mark.parametrize("context", [4096, 8192, 16384, 32768])
 def test_c3_context_points(context):
-    """C3's short contexts at full size (PopKV-S, budget 4096, seed 7): at
-    4096 the budget covers every cached token (k = L, select-all)."""
+    """C3's contexts up to 32K at full size (PopKV-S, budget 4096, seed 7):
+    at 4096 the budget covers every cached token (k = L, select-all); 32768
+    is C1's shape at C3's seed."""
     w = workloads.c3(context)
     assert w.seed == 7 and w.budget == 4096
     if context == 4096:

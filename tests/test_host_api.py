@@ -212,6 +212,22 @@ def test_layer_step_rejects_every_mismatched_operand_before_the_device():
         step()
 
 
+def test_layer_step_attention_rejects_mismatched_operands_before_the_device():
+    q, pk, k, _, h2k = _step_operands()
+    ws = torch.zeros(1 << 16, dtype=torch.uint8)
+    att = lambda **kw: popkv.popkv_layer_step_attention(  # noqa: E731
+        kw.get("q", q), kw.get("pk", pk), kw.get("pv", pk), kw.get("h2k", h2k), budget=kw.get("budget", 16),
+        workspace=kw.get("ws", ws))
+    for kw, msg in [(dict(q=q[:, :64]), "requires a contiguous q"), (dict(pv=pk[:1]), "prefix K/V must be"),
+                    (dict(q=q[:7]), "positive multiple"), (dict(h2k=h2k[:3]), "head_to_kv"),
+                    (dict(budget=1), "budget"), (dict(pk=pk[:, :0], pv=pk[:, :0]), "token count"),
+                    (dict(ws=popkv.LayerStepWorkspace()), "has not been used")]:
+        with pytest.raises(ValueError, match=msg):
+            att(**kw)
+    with pytest.raises(RuntimeError, match="same CUDA device"):
+        att()
+
+
 def test_dense_step_rejects_mismatched_operands_before_the_device():
     q, pk, k, _, _ = _step_operands()
     dense = lambda **kw: popkv.dense_attention_step(  # noqa: E731
@@ -397,6 +413,46 @@ def test_batched_api_validation_before_the_device():
         step(q, cache, lengths, nk, nk, h2k, budget=4, max_tokens=5)
     with pytest.raises(RuntimeError, match="invalid score token count"):
         step(q, cache, lengths, nk, nk, h2k, budget=4, max_tokens=9)
+    # every plane's shape and dtype against (B, KVH, capacity, 4 or 128/G),
+    # before any device check
+    def with_plane(i, t):
+        p = list(planes)
+        p[i] = t
+        return pb.BatchedPopKVCache(8, 32, tuple(p), kc, kc.clone())
+
+    bad_planes = [
+        (with_plane(0, planes[0][:1]), "packed k_sign must be \\[2, 2, capacity, 4\\]"),
+        (with_plane(1, planes[1][:, :, :4]), "packed k_mag must be"),
+        (with_plane(2, planes[2][..., :2]), "packed k_low must be"),
+        (with_plane(3, torch.zeros(2, 2, 8, 4, dtype=torch.float32)), "packed k_delta must be a contiguous"),
+        (with_plane(2, torch.zeros(2, 2, 4, 8, dtype=torch.float16).transpose(2, 3)), "contiguous"),
+        (pb.BatchedPopKVCache(8, 32, planes[:3], kc, kc.clone()), "packed must contain"),
+        (pb.BatchedPopKVCache(8, 16, planes, kc, kc.clone()), "packed k_low must be"),
+        (pb.BatchedPopKVCache(8, 32, planes, kc, kc[..., :64]), "static K/V caches must be"),
+    ]
+    for bad, msg in bad_planes:
+        with pytest.raises(ValueError, match=msg):
+            step(q, bad, lengths, nk, nk, h2k, budget=4)
+        with pytest.raises(ValueError, match=msg):
+            pb.append_batched(bad, lengths, nk, nk)
+        with pytest.raises(ValueError, match=msg):
+            pb.prepack_batched(bad, lengths)
+    with pytest.raises(ValueError, match="status"):
+        step(q, cache, lengths, nk, nk, h2k, budget=4, status=torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(ValueError, match="status must be an int32"):
+        pb.append_batched(cache, lengths, nk, nk, status=torch.zeros(1, dtype=torch.int64))
+    odd = pb.SequenceLengths(torch.tensor([4, 6], dtype=torch.int32), [4, 6])
+    with pytest.raises(ValueError, match="contiguous int64"):
+        step(q, cache, odd, nk, nk, h2k, budget=4)
+    # shapes right, host tensors: refused before any pointer reaches the C ABI
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        step(q, cache, lengths, nk, nk, h2k, budget=4)
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        pb.append_batched(cache, lengths, nk, nk)
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        pb.prepack_batched(cache, lengths)
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        pb.build_batched_popkv_cache(kc, kc, lengths, group_size=8, dim_group_size=32)
 
 
 def _oracle_cache(tokens=150, tg=64, g=64, cap=256, seed=3, dtype=torch.bfloat16):
@@ -461,6 +517,31 @@ def test_packed_metadata_wire_round_trip_and_validation(tmp_path):
     neg = cache.packed[3].clone()
     neg[0, 5, 0] = -1.0
     with pytest.raises(ValueError, match="delta must be non-negative"):
-        wire.validate(popkv.PopKVCache(64, 64, 150, 128, cache.packed[:3] + (neg,), cache.active_keys))
+        wire.validate(popkv.PopKVCache(64, 64, 150, 128, cache.packed[:3] + (neg,), cache.active_keys),
+                      check_values=True)
+    # keys past fp16's range (bf16 / fp32 caches) and NaN keys: the reference
+    # packer stores fp16(low), fp16(high - low) unchecked (popkv_ext.cu:139-140),
+    # so such caches are valid and serialize bit for bit; the value checks are opt-in
+    hot = _oracle_cache(tokens=100, tg=64, g=64, cap=128, dtype=torch.float32)
+    keys = torch.randn(2, 100, 128, generator=torch.Generator().manual_seed(9))
+    keys[0, 3, 7] = 1e6
+    keys[1, 70, 0] = float("nan")
+    from oracle import core
+    import numpy as np
+    planes = []
+    for a, dt in zip(core.pack_keys(keys.numpy(), token_group_size=64, dim_group_size=64),
+                     (torch.int32, torch.int32, torch.float16, torch.float16)):
+        full = torch.zeros(2, 128, a.shape[2], dtype=dt)
+        full[:, :100] = torch.from_numpy(np.ascontiguousarray(a).view(np.int32 if dt == torch.int32 else np.int16)).view(dt)
+        planes.append(full)
+    hot = popkv.PopKVCache(64, 64, 100, 64, tuple(planes), keys[:, 64:].clone())
+    assert not bool(torch.isfinite(hot.packed[2][:, :100].float()).all() and
+                    torch.isfinite(hot.packed[3][:, :100].float()).all())
+    back = wire.from_bytes(wire.to_bytes(hot))
+    for a, b in zip(back.packed, hot.packed):
+        assert torch.equal(a.view(torch.int32 if a.dtype == torch.int32 else torch.int16),
+                           b.view(torch.int32 if b.dtype == torch.int32 else torch.int16))
+    with pytest.raises(ValueError, match="finite"):
+        wire.to_bytes(hot, check_values=True)
     with pytest.raises(ValueError, match="token_count"):
         wire.validate(popkv.PopKVCache(64, 64, 300, 256, cache.packed, torch.zeros(2, 44, 128)))

@@ -2,8 +2,9 @@
 ABI: on two calls in a row -- the second with fewer query/KV heads, a
 shorter context and a smaller budget -- its output and selection equal
 those of popkv_layer_step with a caller workspace, bit for bit (the same
-kernels), and the oracle's.  Also: a step too large for the library's
-scratch array is rejected before any launch."""
+kernels), and the oracle's.  The process's first call is made inside HIP
+graph capture and the graph replayed on new inputs.  Also: a step too large
+for the library's scratch array is rejected before any launch."""
 from __future__ import annotations
 
 import numpy as np
@@ -51,6 +52,45 @@ def _noalloc(w, layer, mapping, cache):
                      pv.stride(0), ck.data_ptr(), cv.data_ptr(), mapping.data_ptr(), w.q_heads, w.kv_heads, L,
                      w.budget, w.dim_group, out.data_ptr(), idx.data_ptr(), _native.stream_of(q.device))
     return out, idx
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """The process's first popkv_layer_step_noalloc call (which looks up the
+    scratch array's device address) made inside HIP graph capture; the
+    graph is then replayed with new queries and current K/V copied into its
+    input tensors in place, and each replay's output and selection equal
+    eager popkv_layer_step on the same inputs, bit for bit."""
+    w, layer, mapping, cache = _case(32, 8, 6000, 1024, 63)
+    L = layer.prefix_tokens
+    q = layer.queries.clone()
+    ck, cv = layer.current_k().clone(), layer.current_v().clone()
+    pk, pv = layer.prefix_k(), layer.prefix_v()
+    out = torch.full_like(q, float("nan"))
+    idx = torch.full((w.q_heads, w.k + 1), -1, device=DEV, dtype=torch.int64)
+    ks, km, kl, kd = cache.packed
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _native.call("popkv_layer_step_noalloc", q.data_ptr(), _native.dtype_code(q), ks.data_ptr(), km.data_ptr(),
+                     kl.data_ptr(), kd.data_ptr(), int(ks.shape[1]), pk.data_ptr(), pv.data_ptr(), pk.stride(0),
+                     pv.stride(0), ck.data_ptr(), cv.data_ptr(), mapping.data_ptr(), w.q_heads, w.kv_heads, L,
+                     w.budget, w.dim_group, out.data_ptr(), idx.data_ptr(), _native.stream_of(q.device))
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(64)
+    for rep in range(3):
+        q.copy_((layer.queries.float().cpu() + 0.5 * torch.randn(q.shape, generator=gen)).to(q.dtype))
+        ck.copy_(torch.randn(ck.shape, generator=gen).to(ck.dtype))
+        cv.copy_(torch.randn(cv.shape, generator=gen).to(cv.dtype))
+        out.fill_(float("nan"))
+        idx.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want_out, want_idx = popkv.popkv_layer_step(q, cache, pk, pv, ck, cv, mapping, budget=w.budget,
+                                                    return_indices=True)
+        torch.cuda.synchronize()
+        assert torch.equal(idx, want_idx), rep
+        assert torch.equal(out, want_out), rep
 
 
 def test_noalloc_layer_step_equals_workspace_entry_on_two_calls():
