@@ -413,7 +413,8 @@ def main() -> int:
     #      HIP events on the step's stream (host-side launch cost excluded)
     def attention_only(i: int) -> None:
         pk, pv, _ = sets[i % N_BUFFERS]
-        popkv.popkv_layer_step_attention(q, pk, pv, mapping, budget=w.budget, workspace=ws)
+        popkv.popkv_layer_step_attention(q, pk, pv, mapping, budget=w.budget, dim_group_size=w.dim_group,
+                                         workspace=ws)
 
     aux_reps = max(reps, 25)  # replays of N_BUFFERS launches for the per-kernel / per-stage figures
     for i in range(args.warmup):

@@ -298,16 +298,17 @@ int popkv_layer_step_noalloc(const void* queries, int32_t dtype,
                              void* output, int64_t* indices_out, void* stream);
 
 /* Re-runs only the fused select + sparse-attention kernel of the last
- * popkv_layer_step that used `workspace` (same shapes and budget): it reads
- * the order keys and threshold histograms the step left there and rewrites
- * the chunk partials (and re-zeroes the already zero key histograms), so it
- * can be repeated.  For timing the step's dominant kernel on its own; no
- * counterpart in the reference. */
+ * popkv_layer_step that used `workspace` (same shapes, budget and
+ * dim_group_size): it reads the order keys and threshold data the step left
+ * there (the kept key histograms and tile windows, or the chunk
+ * histograms) and rewrites the chunk partials, leaving the scorer's
+ * histogram region zero, so it can be repeated.  For timing the step's
+ * dominant kernel on its own; no counterpart in the reference. */
 int popkv_layer_step_attention(const void* queries, int32_t dtype,
                                const void* prefix_k, const void* prefix_v,
                                int64_t k_head_stride, int64_t v_head_stride,
                                const int64_t* head_to_kv, int64_t q_heads, int64_t kv_heads,
-                               int64_t tokens, int64_t budget,
+                               int64_t tokens, int64_t budget, int32_t dim_group_size,
                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Dense attention of one decode step over every prefix token plus the

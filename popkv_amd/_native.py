@@ -65,7 +65,7 @@ _SIGNATURES = {
     "popkv_layer_step_noalloc": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64,
                                                 _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _vp, _vp, _vp]),
     "popkv_layer_step_attention": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64,
-                                                  _c_i64, _vp, _c_size, _vp]),
+                                                  _c_i64, _c_i32, _vp, _c_size, _vp]),
     "popkv_dense_attention_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "popkv_dense_attention": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,
                                              _c_i64, _vp, _vp, _c_size, _vp]),

@@ -643,15 +643,17 @@ struct StepAppendArgs {
 // three waves per SIMD it keeps the residency of the plain step: 142 VGPRs
 // at bf16.  Measured at C4: 160.4 us per step with the append in this
 // launch, 167.9 with a separate append launch.)
-template <typename T, int KPT, int NB, bool SEQ>
+template <typename T, int KPT, int NB, bool SEQ, int WJ>
 __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
     const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
     uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
     float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq,
-    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out, StepAppendArgs<T> apx) {
+    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out, StepAppendArgs<T> apx,
+    WindowIn win) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
+    static_assert(WJ == 0 || kAttnWaves == 4, "the window path's tile layout: 4 waves x 2 halves");
     args_in_sgprs(q, kc, vc, k_hs, v_hs, keys, key_stride, ntok, k, rec, h2, gt1, nchunks, qpk,
                   static_cast<int>(kv_groups), head_to_kv, kv_heads);
     int block = static_cast<int>(blockIdx.x);
@@ -728,13 +730,29 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     // 2).  Measured at C1: a wait for every load before the pass -- what
     // loads on mode-dependent paths compile to -- sent it out about 3 us
     // later.
+    // The window path (WJ > 0: the scorer wrote tile windows, no chunk
+    // histograms) loads instead the row's high-byte histogram (every wave,
+    // lane l holding ranks 4l .. 4l + 3) and one tile record per lane: lane
+    // (hf, wp) of wave w holds tile w + 4 hf + 8 wp, the tiles its half
+    // sums (tile w + 4 hf + 8 j for j < WJ).
     constexpr int HB = 16;
-    const uint32_t b1 = rec[4 * h + z], above1 = rec[4 * h + 1 + z];
+    constexpr int NHV = WJ > 0 ? 1 : HB;
+    uint32_t b1 = 0u, above1 = 0u, gx = 0u;
     const uint16_t* hr = h2 + static_cast<int64_t>(h) * nchunks * 256 + tid;
-    uint32_t hv[HB];
+    uint32_t hv[NHV];
+    const int hf = lane >> 5, wp = lane & 31;
+    uint32_t gcnt[4] = {0u, 0u, 0u, 0u};
+    uint4 wr = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (WJ == 0) {
+        b1 = rec[4 * h + z];
+        above1 = rec[4 * h + 1 + z];
 #pragma unroll
-    for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(j, nchunks - 1)) * 256];
-    const uint32_t gx = gt1[static_cast<int64_t>(h) * nchunks + min(lane, nchunks - 1)];
+        for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(j, nchunks - 1)) * 256];
+        gx = gt1[static_cast<int64_t>(h) * nchunks + min(lane, nchunks - 1)];
+    } else {
+        load_rank4(win.hist + static_cast<int64_t>(h) * 256, gcnt);
+        wr = win.rec[static_cast<int64_t>(h) * win.tiles + min(wave + 4 * hf + 8 * wp, win.tiles - 1)];
+    }
     int nch = nchunks;  // this row's chunks
     if constexpr (SEQ) {
         // a count outside [0, launch bound] runs clamped and is flagged (by
@@ -749,6 +767,79 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     mask_chunk_keys<KPT>(n, kk);
     const int mode = k <= 0 ? 0 : (k >= ntok ? 1 : 2);  // none / every token / threshold
     __shared__ uint32_t s_g2[256], s_p2[256];
+    // window path: per-half partial sums of bin b1's low-byte histogram
+    // over all tiles / the tiles before this chunk (16-bit pairs: at most 8
+    // tiles x the tile's tokens per bin, below 2^16), and the waves' counts
+    // of keys above bin b1 in those earlier tiles.  Each half owns its slot:
+    // only its own wave writes it, so no barrier orders the writes.
+    __shared__ uint32_t s_gpart[WJ > 0 ? 2 * kAttnWaves : 1][128], s_ppart[WJ > 0 ? 2 * kAttnWaves : 1][128];
+    __shared__ uint32_t s_gtb[kAttnWaves];
+    // window path: b1 from the row's histogram, then the window rows at b1
+    // of this half's tiles, issued before the gather pass.  A tile whose
+    // window misses b1 (rare: the window spans the estimate -2 .. +1) is
+    // histogrammed from its keys here, also before the gather pass, whose
+    // loads would otherwise queue the scan's behind them.
+    int ntile_row = 0, c0t = 0, rrow = 0;
+    uint32_t gtb = 0u;  // keys above bin b1 in tiles before this chunk (this lane's share)
+    uint4 wv[WJ > 0 ? WJ : 1];
+    if constexpr (WJ > 0) {
+        const int ts = win.tile_tokens;
+        ntile_row = (ntok + ts - 1) / ts;
+        c0t = c * (CH / ts);
+        if (mode == 2) wave_find_bin(gcnt, static_cast<uint32_t>(k), &b1, &above1);
+        rrow = static_cast<int>(b1) - static_cast<int>(wr.x);
+        const uint4* wb = reinterpret_cast<const uint4*>(win.bins) + static_cast<int64_t>(h) * win.tiles * (kWinBins * 32) + wp;
+        bool miss = false;
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const int i = wave + 4 * hf + 8 * j;
+            const int rj = __shfl(rrow, hf * 32 + j);
+            const bool in_row = i < ntile_row;
+            const bool hit = in_row && static_cast<unsigned>(rj) < static_cast<unsigned>(kWinBins);
+            miss = miss || (in_row && !hit);
+            wv[j] = wb[hit ? (i * kWinBins + rj) * 32 : 0];
+        }
+        const int hs = wave * 2 + hf;
+        const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+        reinterpret_cast<uint4*>(&s_gpart[hs][0])[wp] = zero4;
+        reinterpret_cast<uint4*>(&s_ppart[hs][0])[wp] = zero4;
+        if (mode == 2 && __ballot(miss) != 0) {
+            const int per = ts / 32;
+            for (int j = 0; j < WJ; ++j) {
+                const int i = wave + 4 * hf + 8 * j;
+                const int rj = __shfl(rrow, hf * 32 + j);
+                if (i >= ntile_row || static_cast<unsigned>(rj) < static_cast<unsigned>(kWinBins)) continue;
+                // the lane's per = ts / 32 keys (at most 32), every load
+                // issued before any is used; keys are written up to ntok and
+                // the row holds them to ntok rounded up to 128, so a load
+                // past ntok re-reads the row's start and its keys are masked
+                const int t_first = i * ts + wp * per;
+                const uint16_t* krow = keys + static_cast<int64_t>(h) * key_stride;
+                constexpr int QMAX = 4;  // 8-key loads per lane: ts <= 1024
+                uint4 u[QMAX];
+#pragma unroll
+                for (int q = 0; q < QMAX; ++q)
+                    u[q] = *reinterpret_cast<const uint4*>(krow + (8 * q < per && t_first + 8 * q < ntok ? t_first + 8 * q : 0));
+#pragma unroll
+                for (int q = 0; q < QMAX; ++q) {
+                    const uint32_t wd[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int t = t_first + 8 * q + e;
+                        if (8 * q >= per || t >= ntok) continue;
+                        const uint32_t key = (wd[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+                        const uint32_t hb = key >> 8, inc = 1u << ((key & 1u) * 16);
+                        if (hb == b1) {
+                            atomicAdd(&s_gpart[hs][(key & 0xffu) >> 1], inc);
+                            if (i < c0t) atomicAdd(&s_ppart[hs][(key & 0xffu) >> 1], inc);
+                        } else if (hb > b1 && i < c0t) {
+                            ++gtb;
+                        }
+                    }
+                }
+            }
+        }
+    }
     __shared__ uint32_t s_scan1[kAttnWaves], s_scan2[kAttnWaves];
     __shared__ __align__(16) uint16_t s_list[CH];
     const bool fused = out != nullptr;  // the merge runs in the head's last block (see the end)
@@ -851,32 +942,76 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     // (and the sums stay behind the pass: the scheduler would otherwise
     // hoist some of them, with their waits, above its loads)
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < HB; ++j) {
-        const uint32_t x = j < nch ? hv[j] : 0u;
-        g2 += x;
-        p2 += j < c ? x : 0u;
-    }
-    for (int c0 = HB; c0 < nch; c0 += HB) {  // steps of more than HB chunks (large budgets)
-#pragma unroll
-        for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(c0 + j, nchunks - 1)) * 256];
+    uint32_t gt1_before = 0u;  // keys above bin b1 in earlier chunks
+    if constexpr (WJ == 0) {
 #pragma unroll
         for (int j = 0; j < HB; ++j) {
-            const uint32_t x = c0 + j < nch ? hv[j] : 0u;
+            const uint32_t x = j < nch ? hv[j] : 0u;
             g2 += x;
-            p2 += c0 + j < c ? x : 0u;
+            p2 += j < c ? x : 0u;
         }
+        for (int c0 = HB; c0 < nch; c0 += HB) {  // steps of more than HB chunks (large budgets)
+#pragma unroll
+            for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(c0 + j, nchunks - 1)) * 256];
+#pragma unroll
+            for (int j = 0; j < HB; ++j) {
+                const uint32_t x = c0 + j < nch ? hv[j] : 0u;
+                g2 += x;
+                p2 += c0 + j < c ? x : 0u;
+            }
+        }
+        gt1_before = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(lane < c ? gx : 0u, lane)), kWave - 1));
+        if (mode == 2) {
+            s_g2[tid] = g2;
+            s_p2[tid] = p2;
+        }
+        // (bin 0 -- which no real key reaches -- holds the fused merge's
+        // ticket; the window path re-zeroes the histogram in the merge, its
+        // last reader being this kernel)
+        if (c == 0 && (tid > 0 || !fused)) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
+    } else {
+        // the half's window rows added to its slot (which holds the missed
+        // tiles' counts), and the record lane's keys above bin b1 when its
+        // tile lies before this chunk
+        uint4 gs = make_uint4(0u, 0u, 0u, 0u), ps = gs;
+        if (mode == 2) {
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) {
+                const int i = wave + 4 * hf + 8 * j;
+                const int rj = __shfl(rrow, hf * 32 + j);
+                if (i < ntile_row && static_cast<unsigned>(rj) < static_cast<unsigned>(kWinBins)) {
+                    gs.x += wv[j].x; gs.y += wv[j].y; gs.z += wv[j].z; gs.w += wv[j].w;
+                    if (i < c0t) {
+                        ps.x += wv[j].x; ps.y += wv[j].y; ps.z += wv[j].z; ps.w += wv[j].w;
+                    }
+                }
+            }
+            const int ir = wave + 4 * hf + 8 * wp;
+            if (ir < ntile_row && ir < c0t && static_cast<unsigned>(rrow) < static_cast<unsigned>(kWinBins)) {
+                const uint32_t tot[kWinBins] = {wr.z & 0xffffu, wr.z >> 16, wr.w & 0xffffu, wr.w >> 16};
+                uint32_t above_b1 = wr.y;  // keys above the window
+#pragma unroll
+                for (int w = 0; w < kWinBins; ++w) above_b1 += w > rrow ? tot[w] : 0u;
+                gtb += above_b1;
+            }
+        }
+        // (this lane's four words of the slot: written before by this wave
+        // alone, whose LDS operations complete in order)
+        const int hs = wave * 2 + hf;
+        uint4* gw = reinterpret_cast<uint4*>(&s_gpart[hs][0]) + wp;
+        uint4* pw = reinterpret_cast<uint4*>(&s_ppart[hs][0]) + wp;
+        const uint4 g0 = *gw, p0 = *pw;
+        *gw = make_uint4(g0.x + gs.x, g0.y + gs.y, g0.z + gs.z, g0.w + gs.w);
+        *pw = make_uint4(p0.x + ps.x, p0.y + ps.y, p0.z + ps.z, p0.w + ps.w);
+        gtb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(gtb, lane)), kWave - 1));
+        if (lane == 0) s_gtb[wave] = gtb;
     }
-    // keys above bin b1 in earlier chunks
-    const uint32_t gt1_before = static_cast<uint32_t>(
-        __builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(lane < c ? gx : 0u, lane)), kWave - 1));
-    if (mode == 2) {
-        s_g2[tid] = g2;
-        s_p2[tid] = p2;
-    }
-    // (bin 0 -- which no real key reaches -- holds the fused merge's ticket)
-    if (c == 0 && (tid > 0 || !fused)) ghist[static_cast<int64_t>(h) * 256 + tid] = 0u;
     __syncthreads();
+    if constexpr (WJ > 0) {
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) gt1_before += s_gtb[w];
+    }
 
     // 3. T from the chunk histograms; the block's list: the tokens above bin
     //    b1 the waves' first passes left, bin b1's keys above T and the
@@ -884,19 +1019,44 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     uint32_t thr = 0, need_eq = 0, eq_before = 0;
     if (mode == 2) {
         uint32_t cnt[4];
+        if constexpr (WJ == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cnt[i] = s_g2[255 - (4 * lane + i)];
+            for (int i = 0; i < 4; ++i) cnt[i] = s_g2[255 - (4 * lane + i)];
+        } else {
+            // bins 255 - 4l .. 252 - 4l: the high and low halves of words
+            // 127 - 2l and 126 - 2l, summed over the eight half slots
+            cnt[0] = cnt[1] = cnt[2] = cnt[3] = 0u;
+#pragma unroll
+            for (int hs = 0; hs < 2 * kAttnWaves; ++hs) {
+                const uint2 v = *reinterpret_cast<const uint2*>(&s_gpart[hs][126 - 2 * lane]);
+                cnt[0] += v.y >> 16;
+                cnt[1] += v.y & 0xffffu;
+                cnt[2] += v.x >> 16;
+                cnt[3] += v.x & 0xffffu;
+            }
+        }
         const uint32_t need1 = static_cast<uint32_t>(k) - above1;
         uint32_t t2, above2;
         wave_find_bin(cnt, need1, &t2, &above2);
         thr = (b1 << 8) | t2;  // >= 0x03ff
         need_eq = need1 - above2;
-        eq_before = s_p2[t2];
+        // bin u of the chunks (tiles) before this one
+        auto p2_of = [&](int u) -> uint32_t {
+            if constexpr (WJ == 0) {
+                return s_p2[u];
+            } else {
+                uint32_t x = 0u;
+#pragma unroll
+                for (int hs = 0; hs < 2 * kAttnWaves; ++hs) x += (s_ppart[hs][u >> 1] >> ((u & 1) * 16)) & 0xffffu;
+                return x;
+            }
+        };
+        eq_before = p2_of(static_cast<int>(t2));
         if (idx_out != nullptr) {
             // keys of bin b1 with low byte > t2 in earlier chunks
             uint32_t x = 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x += 4 * lane + i > static_cast<int>(t2) ? s_p2[4 * lane + i] : 0u;
+            for (int i = 0; i < 4; ++i) x += 4 * lane + i > static_cast<int>(t2) ? p2_of(4 * lane + i) : 0u;
             const uint32_t gt2_before =
                 static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(x, lane)), kWave - 1));
             rank0 = gt1_before + gt2_before + min(eq_before, need_eq);
@@ -976,10 +1136,23 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     }
     __syncthreads();
     if (s_last == 0u || wave != 0) return;
-    if (lane == 0) {
-        __hip_atomic_store(&ghist[static_cast<int64_t>(h) * 256], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (idx_out != nullptr) idx_out[static_cast<int64_t>(h) * idx_stride + k] = ntok;
+    if constexpr (WJ == 0) {
+        if (lane == 0)
+            __hip_atomic_store(&ghist[static_cast<int64_t>(h) * 256], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        // every block of the head has read the histogram (before its
+        // ticket): keep a copy for re-runs of this kernel alone (win.keep),
+        // then zero it, ticket included, for the next step's scorer
+        uint4* gh = reinterpret_cast<uint4*>(ghist + static_cast<int64_t>(h) * 256);
+        if (win.keep != nullptr)
+            reinterpret_cast<uint4*>(win.keep + static_cast<int64_t>(h) * 256)[63 - lane] =
+                make_uint4(gcnt[3], gcnt[2], gcnt[1], gcnt[0]);
+        __hip_atomic_store(&gh[lane].x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gh[lane].y = 0u;
+        gh[lane].z = 0u;
+        gh[lane].w = 0u;
     }
+    if (lane == 0 && idx_out != nullptr) idx_out[static_cast<int64_t>(h) * idx_stride + k] = ntok;
     const int64_t crow = ((SEQ ? b * seq.kv_heads : 0) + kvh) * D;
     merge_head<T, true>(partials + static_cast<int64_t>(h) * nchunks * (D + 2), static_cast<int>(parts),
                         q + static_cast<int64_t>(h) * D, cur_k + crow, cur_v + crow, scale,
@@ -1529,7 +1702,7 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
                                   const uint32_t* rec, const uint16_t* h2, const uint32_t* gt1, uint32_t* ghist,
                                   const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
                                   int64_t idx_stride, const SeqTable& seq, const void* cur_k, const void* cur_v,
-                                  void* out, hipStream_t stream, const DecodeAppend* app) {
+                                  void* out, hipStream_t stream, const DecodeAppend* app, const WindowIn* win) {
     // 10 rows per slot and pass: 160 per pass, so a chunk holding up to 320
     // selected tokens (C1: 204-294 in chunks of 2048) is gathered in two
     // passes.  Measured at C1, select + attention: 8 rows 16.5 us (three
@@ -1570,22 +1743,42 @@ hipError_t launch_select_chunks_t(const void* q, const void* kc, const void* vc,
     const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
     const T *ck_ = static_cast<const T*>(cur_k), *cv_ = static_cast<const T*>(cur_v);
     T* o_ = static_cast<T*>(out);
-#define POPKV_SC(KPT)                                                                                            \
-    case KPT:                                                                                                    \
-        if (batched)                                                                                             \
-            hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, true>), grid, dim3(kAttnThreads), 0, stream, \
-                               q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
-                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_, apx); \
-        else                                                                                                     \
-            hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, false>), grid, dim3(kAttnThreads), 0, stream, \
-                               q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups,   \
-                               ghist, h2k, kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_, apx); \
+    const WindowIn wi = win != nullptr ? *win : WindowIn{};
+#define POPKV_SC_W(KPT, WJ)                                                                                       \
+    if (batched)                                                                                                 \
+        hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, true, WJ>), grid, dim3(kAttnThreads), 0, stream,   \
+                           q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups, ghist, h2k, \
+                           kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_, apx, wi);            \
+    else                                                                                                         \
+        hipLaunchKernelGGL((attn_select_chunk_kernel<T, KPT, NB, false, WJ>), grid, dim3(kAttnThreads), 0, stream,  \
+                           q_, k_, v_, k_hs, v_hs, keys, key_stride, nt, kk, rec, h2, gt1, nc, qpk, groups, ghist, h2k, \
+                           kv_clamp, scale, partials, idx_out, idx_stride, seq, ck_, cv_, o_, apx, wi)
+#define POPKV_SC(KPT)             \
+    case KPT:                     \
+        POPKV_SC_W(KPT, 0);       \
         break
-    switch (ch.kpt) {
-        POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
-        default: return hipErrorInvalidValue;
+#define POPKV_SC_WIN(KPT)                                 \
+    case KPT:                                             \
+        POPKV_SC_W(KPT, kWinMaxTiles / 8);                \
+        break
+    if (win != nullptr) {
+        // the tile windows (host-checked: window_kpt_ok, at most
+        // kWinMaxTiles tiles of whole chunks)
+        if (wi.tiles <= 0 || wi.tiles > kWinMaxTiles || wi.tile_tokens <= 0 || ch.tokens_per_chunk % wi.tile_tokens)
+            return hipErrorInvalidValue;
+        switch (ch.kpt) {
+            POPKV_SC_WIN(4); POPKV_SC_WIN(8); POPKV_SC_WIN(16);
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (ch.kpt) {
+            POPKV_SC(1); POPKV_SC(2); POPKV_SC(4); POPKV_SC(6); POPKV_SC(8); POPKV_SC(12); POPKV_SC(16); POPKV_SC(24); POPKV_SC(32);
+            default: return hipErrorInvalidValue;
+        }
     }
+#undef POPKV_SC_WIN
 #undef POPKV_SC
+#undef POPKV_SC_W
     return hipGetLastError();
 }
 
@@ -1616,24 +1809,24 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                           int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
                                           const void* current_k, const void* current_v, void* output,
-                                          hipStream_t stream, const DecodeAppend* append) {
+                                          hipStream_t stream, const DecodeAppend* append, const WindowIn* win) {
     if (tokens <= 0 || q_heads <= 0) return hipSuccess;
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_select_chunks_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
                                                  kv_heads, partials, idx_out, idx_stride, seq, current_k,
-                                                 current_v, output, stream, append);
+                                                 current_v, output, stream, append, win);
         case POPKV_DTYPE_F16:
             return launch_select_chunks_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                  key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
                                                  kv_heads, partials, idx_out, idx_stride, seq, current_k,
-                                                 current_v, output, stream, append);
+                                                 current_v, output, stream, append, win);
         default:
             return launch_select_chunks_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, keys,
                                                   key_stride, tokens, k, rec, h2, gt1, ghist, head_to_kv, q_heads,
                                                   kv_heads, partials, idx_out, idx_stride, seq, current_k,
-                                                 current_v, output, stream, append);
+                                                 current_v, output, stream, append, win);
     }
 }
 

@@ -48,20 +48,32 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Workspace layout of popkv_layer_step (batch 1, head_dim 128).
 struct StepLayout {
-    size_t hist, rec, h2, gt1, scores, partials, total;
-    int64_t score_stride, k, nchunks;
+    size_t hist, rec, h2, gt1, scores, partials, keep, wrec, wbins, total;
+    int64_t score_stride, k, nchunks, tiles, tile_tokens;
+    bool windows;  // the tile-window select applies to this shape (for GQA groups of 1, 2, 4 or 8)
 };
 
 // Layer-step workspace: [QH][256] u32 high-byte key histograms (zero between
 // calls) | [QH][4] u32 threshold records | [QH][chunks][256] u16 chunk
 // low-byte histograms | [QH][chunks] u32 chunk counts | [QH][score_stride]
-// u16 order keys | [QH][chunks][130] f32 chunk partials.
-StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
+// u16 order keys | [QH][chunks][130] f32 chunk partials, and for the
+// tile-window select: [QH][256] u32 kept histograms | [QH][tiles] uint4
+// window records | [QH][tiles][kWinBins][128] u32 window histograms.  The
+// window path applies to 64-dimension groups when 0 < k < tokens, the row
+// has at most kWinMaxTiles scorer tiles and a chunk is a whole number of
+// them.
+StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget, int32_t g) {
     StepLayout L{};
     L.k = budget - 1 < tokens ? budget - 1 : tokens;
     L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 128) * 128;
-    L.nchunks = popkv::step_chunks(tokens, L.k, qh).count;
+    const popkv::StepChunks ch = popkv::step_chunks(tokens, L.k, qh);
+    L.nchunks = ch.count;
+    L.tile_tokens = popkv::score_tile_tokens(g);
+    L.tiles = ceil_div(tokens > 0 ? tokens : 1, L.tile_tokens);
+    L.windows = g == 64 && L.k > 0 && L.k < tokens && L.tiles <= popkv::kWinMaxTiles &&
+                popkv::window_kpt_ok(ch.kpt) && ch.tokens_per_chunk % L.tile_tokens == 0;
     const size_t nc = static_cast<size_t>(L.nchunks > 0 ? L.nchunks : 1);
+    const size_t nt = L.windows ? static_cast<size_t>(L.tiles) : 0;
     size_t off = 0;
     L.hist = off; off = align_up(off + static_cast<size_t>(qh) * 256 * 4);
     L.rec = off; off = align_up(off + static_cast<size_t>(qh) * 4 * 4);
@@ -69,8 +81,16 @@ StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget) {
     L.gt1 = off; off = align_up(off + static_cast<size_t>(qh) * nc * 4);
     L.scores = off; off = align_up(off + static_cast<size_t>(qh * L.score_stride) * 2);
     L.partials = off; off = align_up(off + static_cast<size_t>(qh) * nc * (128 + 2) * 4);
+    L.keep = off; off = align_up(off + (L.windows ? static_cast<size_t>(qh) * 256 * 4 : 0));
+    L.wrec = off; off = align_up(off + static_cast<size_t>(qh) * nt * 16);
+    L.wbins = off; off = align_up(off + static_cast<size_t>(qh) * nt * popkv::kWinBins * 128 * 4);
     L.total = off;
     return L;
+}
+
+bool group_fits_windows(int64_t q_heads, int64_t kv_heads) {
+    const int64_t qpk = kv_heads > 0 ? q_heads / kv_heads : 0;
+    return qpk == 1 || qpk == 2 || qpk == 4 || qpk == 8;
 }
 
 // The allocation-free layer step's workspace: one array per GPU, held until
@@ -321,7 +341,7 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
 
 size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t budget, int32_t dim_group_size) {
     if (q_heads <= 0 || tokens < 0 || budget <= 1 || !valid_group(dim_group_size)) return 0;
-    return step_layout(q_heads, tokens, budget).total;
+    return step_layout(q_heads, tokens, budget, dim_group_size).total;
 }
 
 }  // extern "C"
@@ -343,7 +363,7 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     int st = check_score_common(head_to_kv, 1, q_heads, kv_heads, capacity, tokens, dim_group_size);
     if (st) return st;
     if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens");
-    const StepLayout L = step_layout(q_heads, tokens, budget);
+    const StepLayout L = step_layout(q_heads, tokens, budget, dim_group_size);
     if (!workspace || workspace_bytes < L.total)
         return fail(POPKV_ERR_WORKSPACE, "layer step needs %zu workspace bytes", L.total);
     if (!aligned16(workspace)) return fail(POPKV_ERR_INVALID, "workspace must be 16-byte aligned");
@@ -359,6 +379,21 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     uint32_t* gt1 = reinterpret_cast<uint32_t*>(ws + L.gt1);
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
+    const bool windows = L.windows && group_fits_windows(q_heads, kv_heads);
+    popkv::TileWindows tw;
+    popkv::WindowIn wi;
+    if (windows) {
+        tw.rec = reinterpret_cast<uint4*>(ws + L.wrec);
+        tw.bins = reinterpret_cast<uint32_t*>(ws + L.wbins);
+        tw.tiles = static_cast<int>(L.tiles);
+        tw.k = static_cast<int>(L.k);
+        wi.hist = hist;
+        wi.keep = reinterpret_cast<uint32_t*>(ws + L.keep);
+        wi.rec = tw.rec;
+        wi.bins = tw.bins;
+        wi.tiles = tw.tiles;
+        wi.tile_tokens = static_cast<int>(L.tile_tokens);
+    }
     hipStream_t s = as_stream(stream);
     if (clear_first) {
         st = launched(popkv::launch_fill_u32(hist, q_heads * 256, 0u, s), "popkv_layer_step(clear histograms)");
@@ -378,7 +413,7 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
                                                    static_cast<const uint16_t*>(k_delta), head_to_kv, 1,
                                                    static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
                                                    tokens, dim_group_size, keys, L.score_stride, hist,
-                                                   popkv::SeqTable{}, s),
+                                                   popkv::SeqTable{}, s, tw),
                       "popkv_layer_step(score)");
         if (st) return st;
     }
@@ -388,11 +423,14 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
         (void)popkv::launch_fill_u32(hist, q_heads * 256, 0u, s);
         return status;
     };
-    // 2. per-chunk low-byte histograms of the threshold's high-byte bin
-    st = launched(popkv::launch_chunk_hist(keys, L.score_stride, q_heads, tokens, L.k, hist, rec, h2, gt1,
-                                           popkv::SeqTable{}, s),
-                  "popkv_layer_step(chunk histograms)");
-    if (st) return clear_hist(st);
+    // 2. per-chunk low-byte histograms of the threshold's high-byte bin (the
+    //    tile-window path has them from the scorer's windows instead)
+    if (!windows) {
+        st = launched(popkv::launch_chunk_hist(keys, L.score_stride, q_heads, tokens, L.k, hist, rec, h2, gt1,
+                                               popkv::SeqTable{}, s),
+                      "popkv_layer_step(chunk histograms)");
+        if (st) return clear_hist(st);
+    }
     // 3. per (chunk, head): the chunk's selected tokens (also written as
     //    int64 at their rank when indices_out is given) and the sparse
     //    attention over them (re-zeroes the histograms); the head's last
@@ -403,7 +441,8 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
                                                         v_head_stride, keys, L.score_stride, tokens, L.k, rec, h2,
                                                         gt1, hist, head_to_kv, static_cast<int>(q_heads),
                                                         static_cast<int>(kv_heads), partials, indices_out, L.k + 1,
-                                                        popkv::SeqTable{}, current_k, current_v, output, s),
+                                                        popkv::SeqTable{}, current_k, current_v, output, s, nullptr,
+                                                        windows ? &wi : nullptr),
                   "popkv_layer_step(select + attention + merge)");
     if (st) return clear_hist(st);
     return POPKV_OK;
@@ -430,8 +469,8 @@ int popkv_layer_step_noalloc(const void* queries, int32_t dtype, const int32_t* 
                              const void* current_k, const void* current_v, const int64_t* head_to_kv,
                              int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget,
                              int32_t dim_group_size, void* output, int64_t* indices_out, void* stream) {
-    if (q_heads > 0 && tokens >= 0 && budget > 1) {
-        const size_t need = step_layout(q_heads, tokens, budget).total;
+    if (q_heads > 0 && tokens >= 0 && budget > 1 && valid_group(dim_group_size)) {
+        const size_t need = step_layout(q_heads, tokens, budget, dim_group_size).total;
         if (need > POPKV_LAYER_STEP_SCRATCH_BYTES)
             return fail(POPKV_ERR_WORKSPACE,
                         "popkv_layer_step_noalloc: this step needs %zu bytes of scratch, more than the "
@@ -450,7 +489,7 @@ int popkv_layer_step_noalloc(const void* queries, int32_t dtype, const int32_t* 
 size_t popkv_layer_step_batched_workspace_bytes(int64_t batch, int64_t q_heads, int64_t max_tokens, int64_t budget,
                                                 int32_t dim_group_size) {
     if (batch <= 0 || q_heads <= 0 || max_tokens < 0 || budget <= 1 || !valid_group(dim_group_size)) return 0;
-    return step_layout(batch * q_heads, max_tokens, budget).total;
+    return step_layout(batch * q_heads, max_tokens, budget, dim_group_size).total;
 }
 
 // The current token's append in a decode step (popkv_decode_layer_batched).
@@ -486,7 +525,7 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
     const int64_t kmax = budget - 1 < max_tokens ? budget - 1 : max_tokens;
     if (indices_out && index_row_stride < kmax + 1) return fail(POPKV_ERR_INVALID, "index row stride too small");
     const int64_t rows = batch * q_heads;
-    const StepLayout L = step_layout(rows, max_tokens, budget);
+    const StepLayout L = step_layout(rows, max_tokens, budget, dim_group_size);
     if (!workspace || workspace_bytes < L.total)
         return fail(POPKV_ERR_WORKSPACE, "batched layer step needs %zu workspace bytes", L.total);
     if (!aligned16(workspace)) return fail(POPKV_ERR_INVALID, "workspace must be 16-byte aligned");
@@ -529,6 +568,21 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
     uint32_t* gt1 = reinterpret_cast<uint32_t*>(ws + L.gt1);
     uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.scores);
     float* partials = reinterpret_cast<float*>(ws + L.partials);
+    const bool windows = L.windows && group_fits_windows(q_heads, kv_heads);
+    popkv::TileWindows tw;
+    popkv::WindowIn wi;
+    if (windows) {
+        tw.rec = reinterpret_cast<uint4*>(ws + L.wrec);
+        tw.bins = reinterpret_cast<uint32_t*>(ws + L.wbins);
+        tw.tiles = static_cast<int>(L.tiles);
+        tw.k = static_cast<int>(L.k);
+        wi.hist = hist;
+        wi.keep = reinterpret_cast<uint32_t*>(ws + L.keep);
+        wi.rec = tw.rec;
+        wi.bins = tw.bins;
+        wi.tiles = tw.tiles;
+        wi.tile_tokens = static_cast<int>(L.tile_tokens);
+    }
     hipStream_t s = as_stream(stream);
     // the same three kernels as popkv_layer_step, every row at its own
     // sequence's token count (see popkv::SeqTable).  With budget - 1 >=
@@ -541,7 +595,8 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
                                                    static_cast<const uint16_t*>(k_low),
                                                    static_cast<const uint16_t*>(k_delta), head_to_kv, batch,
                                                    static_cast<int>(q_heads), static_cast<int>(kv_heads), capacity,
-                                                   max_tokens, dim_group_size, keys, L.score_stride, hist, seq, s),
+                                                   max_tokens, dim_group_size, keys, L.score_stride, hist, seq, s,
+                                                   tw),
                       "popkv_layer_step_batched(score)");
         if (st) return st;
     }
@@ -549,15 +604,17 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
         (void)popkv::launch_fill_u32(hist, rows * 256, 0u, s);
         return status;
     };
-    st = launched(popkv::launch_chunk_hist(keys, L.score_stride, rows, max_tokens, L.k, hist, rec, h2, gt1, seq, s),
-                  "popkv_layer_step_batched(chunk histograms)");
-    if (st) return clear_hist(st);
+    if (!windows) {
+        st = launched(popkv::launch_chunk_hist(keys, L.score_stride, rows, max_tokens, L.k, hist, rec, h2, gt1, seq, s),
+                      "popkv_layer_step_batched(chunk histograms)");
+        if (st) return clear_hist(st);
+    }
     st = launched(popkv::launch_attention_select_chunks(queries, dtype, key_cache, value_cache, cache_rows * 128,
                                                         cache_rows * 128, keys, L.score_stride, max_tokens, L.k, rec,
                                                         h2, gt1, hist, head_to_kv, static_cast<int>(rows),
                                                         static_cast<int>(kv_heads), partials, indices_out,
                                                         index_row_stride, seq, current_k, current_v, output, s,
-                                                        app ? &dapp : nullptr),
+                                                        app ? &dapp : nullptr, windows ? &wi : nullptr),
                   app ? "popkv_decode_layer_batched(select + attention + merge + append)"
                       : "popkv_layer_step_batched(select + attention + merge)");
     if (st) return clear_hist(st);
@@ -619,20 +676,32 @@ int popkv_append(const void* new_k, const void* new_v, int32_t dtype, void* key_
 
 int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
                                int64_t k_head_stride, int64_t v_head_stride, const int64_t* head_to_kv,
-                               int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget,
+                               int32_t dim_group_size, void* workspace, size_t workspace_bytes, void* stream) {
     if (!queries || !prefix_k || !prefix_v || !head_to_kv || !workspace) return fail(POPKV_ERR_INVALID, "null pointer");
     if (!valid_dtype(dtype)) return fail(POPKV_ERR_INVALID, "tensors must be fp32/fp16/bf16");
     if (budget <= 1) return fail(POPKV_ERR_INVALID, "budget must reserve at least one retrieved and one current token");
     if (q_heads <= 0 || kv_heads <= 0 || q_heads > 65535) return fail(POPKV_ERR_INVALID, "empty or too many heads");
     if (tokens <= 0 || tokens > kMaxSelectTokens) return fail(POPKV_ERR_TOKENS, "invalid score token count");
-    const StepLayout L = step_layout(q_heads, tokens, budget);
+    if (!valid_group(dim_group_size)) return fail(POPKV_ERR_INVALID, "dim_group_size must be 16, 32, or 64");
+    const StepLayout L = step_layout(q_heads, tokens, budget, dim_group_size);
     if (workspace_bytes < L.total) return fail(POPKV_ERR_WORKSPACE, "layer step needs %zu workspace bytes", L.total);
     const size_t es = elem_size(dtype);
     if (!aligned16(workspace) || !aligned16(queries) || !aligned16(prefix_k) || !aligned16(prefix_v) ||
         (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
         return fail(POPKV_ERR_UNSUPPORTED, "layer step tensors need 16-byte alignment");
     char* ws = static_cast<char*>(workspace);
+    // the window path reads the histograms the last step kept (its merge
+    // zeroed the scorer's); this re-run keeps and zeroes nothing
+    const bool windows = L.windows && group_fits_windows(q_heads, kv_heads);
+    popkv::WindowIn wi;
+    if (windows) {
+        wi.hist = reinterpret_cast<const uint32_t*>(ws + L.keep);
+        wi.rec = reinterpret_cast<const uint4*>(ws + L.wrec);
+        wi.bins = reinterpret_cast<const uint32_t*>(ws + L.wbins);
+        wi.tiles = static_cast<int>(L.tiles);
+        wi.tile_tokens = static_cast<int>(L.tile_tokens);
+    }
     return launched(popkv::launch_attention_select_chunks(
                         queries, dtype, prefix_k, prefix_v, k_head_stride, v_head_stride,
                         reinterpret_cast<const uint16_t*>(ws + L.scores), L.score_stride, tokens, L.k,
@@ -640,7 +709,7 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* p
                         reinterpret_cast<const uint32_t*>(ws + L.gt1), reinterpret_cast<uint32_t*>(ws + L.hist),
                         head_to_kv, static_cast<int>(q_heads), static_cast<int>(kv_heads),
                         reinterpret_cast<float*>(ws + L.partials), nullptr, 0, popkv::SeqTable{}, nullptr, nullptr,
-                        nullptr, as_stream(stream)),
+                        nullptr, as_stream(stream), nullptr, windows ? &wi : nullptr),
                     "popkv_layer_step_attention");
 }
 

@@ -60,15 +60,45 @@ hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const 
                              int dim_group_size, uint16_t* scores, int64_t score_row_stride,
                              hipStream_t stream);
 
+// Tile windows of the layer step (the select's threshold without a
+// chunk-histogram pass).  The scorer's workgroup scores one tile of
+// score_tile_tokens(G) tokens of a GQA group's rows; for each (row, tile)
+// it estimates the high-byte bin of the row's k-th largest key from the
+// tile's own histogram (the bin where the tile's count from the top first
+// reaches its share ceil(k * tile tokens / row tokens)), takes the window
+// of kWinBins bins starting kWinBelow below that estimate and writes
+//   rec:  uint4 {window base bin, keys of the tile above the window,
+//                counts of window bins 0|1 and 2|3 as 16-bit pairs}
+//   bins: [kWinBins][128] uint32: the low-byte histograms of the window's
+//         bins, bins 2m and 2m+1 in the low and high halves of word m.
+// The select kernel then sums one window row per tile (the row's threshold
+// bin) instead of a histogram pass over the keys; a tile whose window misses
+// that bin is histogrammed from its keys there.
+constexpr int kWinBins = 4;
+constexpr int kWinBelow = 2;
+// per row: longer rows take launch_chunk_hist (measured: with 64-tile rows
+// -- C2's 512-token tiles, C4's 64K sequences -- the select blocks' window
+// reads, one 512-byte row per tile, cost more than the kernel they replace)
+constexpr int kWinMaxTiles = 32;
+inline int score_tile_tokens(int dim_group_size) { return dim_group_size == 64 ? 1024 : 512; }
+struct TileWindows {
+    uint4* rec = nullptr;    // [rows][tiles]
+    uint32_t* bins = nullptr;  // [rows][tiles][kWinBins][128]
+    int tiles = 0;           // tiles per row (the scorer's grid.x)
+    int k = 0;               // selected tokens of an unbatched step
+};
+
 // Layer-step scorer: encodes the raw query rows [batch*QH, 128] in-kernel
 // (fold order), writes the scores' radix order keys (uint16) instead of fp16
 // bits, and adds each row's 256-bin high-byte key histogram into
-// ghist[row][256] (which must hold zeros on entry).
+// ghist[row][256] (which must hold zeros on entry).  With win.rec non-null
+// (dim_group_size 64, GQA groups of 1, 2, 4 or 8 query heads) it also writes
+// the tile windows.
 hipError_t launch_score_d128_raw(const void* queries, int dtype, const int32_t* k_sign, const int32_t* k_mag,
                                  const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
                                  int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
                                  int dim_group_size, uint16_t* keys, int64_t key_row_stride, uint32_t* ghist,
-                                 const SeqTable& seq, hipStream_t stream);
+                                 const SeqTable& seq, hipStream_t stream, const TileWindows& win = TileWindows{});
 
 hipError_t launch_score_generic(const int32_t* q_sign, const int32_t* q_mag, const float* q_low,
                                 const float* q_delta, const int32_t* k_sign, const int32_t* k_mag,
@@ -140,6 +170,22 @@ struct DecodeAppend {
     int token_group_size;
     int dim_group_size;
 };
+// The select's inputs on the window path (no chunk histograms): the rows'
+// high-byte histograms (`hist`: the scorer's ghist in a layer step, the
+// kept copy when the kernel is re-run alone), the tile windows, and `keep`
+// (non-null: the fused merge copies each row's histogram there before
+// zeroing ghist).  Taken for chunks of a whole number of tiles
+// (window_kpt_ok), at most kWinMaxTiles tiles per row.
+struct WindowIn {
+    const uint32_t* hist = nullptr;
+    uint32_t* keep = nullptr;
+    const uint4* rec = nullptr;
+    const uint32_t* bins = nullptr;
+    int tiles = 0;
+    int tile_tokens = 0;
+};
+inline bool window_kpt_ok(int kpt) { return kpt == 4 || kpt == 8 || kpt == 16; }
+
 hipError_t launch_attention_select_chunks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                           int64_t k_head_stride, int64_t v_head_stride, const uint16_t* keys,
                                           int64_t key_stride, int64_t tokens, int64_t k, const uint32_t* rec,
@@ -147,7 +193,8 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
                                           int64_t* idx_out, int64_t idx_stride, const SeqTable& seq,
                                           const void* current_k, const void* current_v, void* output,
-                                          hipStream_t stream, const DecodeAppend* append = nullptr);
+                                          hipStream_t stream, const DecodeAppend* append = nullptr,
+                                          const WindowIn* win = nullptr);
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
 // Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one

@@ -342,10 +342,78 @@ __device__ void load_group_state(const int32_t* __restrict__ q_sign, const int32
     __syncthreads();
 }
 
+static_assert(kScoreThreads * score_tokens_per_thread<64>() == 1024 &&
+                  kScoreThreads * score_tokens_per_thread<16>() == 512 &&
+                  kScoreThreads * score_tokens_per_thread<32>() == 512,
+              "score_tile_tokens() states the scorer's tile");
+
+// The tile windows of one scorer workgroup (tile blockIdx.x of rows
+// qrow0 .. qrow0 + QPK - 1, the row's sequence holding ntok tokens of which
+// k are selected): wave h estimates row h's threshold bin from the tile's
+// histogram s_hist[h] and writes the window record, then every thread adds
+// its keys that fall in their row's window to the window histograms in LDS
+// (s_win, zero on entry; the caller writes them out).  A row that selects
+// none or every token gets base 256 (no window; its select never reads
+// it).  All threads of the block call it, after a barrier that completes
+// s_hist and s_keys.
+template <int QPK, int TILE>
+__device__ __forceinline__ void tile_windows(const uint32_t (*s_hist)[256], const uint16_t (*s_keys)[TILE],
+                                             uint32_t (*s_win)[kWinBins][128], uint32_t* s_base,
+                                             const TileWindows& win, int64_t qrow0, int64_t ntok, int64_t k) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t t_lo = static_cast<int64_t>(blockIdx.x) * TILE;
+    const int64_t n_i = min(max(ntok - t_lo, static_cast<int64_t>(0)), static_cast<int64_t>(TILE));
+    if (wave < QPK) {
+        uint32_t base = 256u, above = 0u, t01 = 0u, t23 = 0u;
+        if (n_i > 0 && k > 0 && k < ntok) {  // uniform
+            uint32_t cnt[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cnt[i] = s_hist[wave][255 - (4 * lane + i)];
+            // the tile's share of the selection, ceil(k * n_i / ntok), in [1, n_i]
+            const uint32_t need = static_cast<uint32_t>((k * n_i + ntok - 1) / ntok);
+            uint32_t est, est_above;
+            wave_find_bin(cnt, need, &est, &est_above);
+            base = min(max(est, static_cast<uint32_t>(kWinBelow + 1)) - kWinBelow, static_cast<uint32_t>(256 - kWinBins));
+            uint32_t part = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) part += 255u - static_cast<uint32_t>(4 * lane + i) >= base + kWinBins ? cnt[i] : 0u;
+            above = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(part, lane)), kWave - 1));
+            t01 = s_hist[wave][base] | (s_hist[wave][base + 1] << 16);
+            t23 = s_hist[wave][base + 2] | (s_hist[wave][base + 3] << 16);
+        }
+        if (lane == 0) {
+            s_base[wave] = base;
+            win.rec[(qrow0 + wave) * win.tiles + blockIdx.x] = make_uint4(base, above, t01, t23);
+        }
+    }
+    __syncthreads();
+    // every key of this thread first (the reads would otherwise wait for
+    // the atomics before them), then the atomics
+    constexpr int PER = TILE / kScoreThreads;
+    uint32_t kv[QPK][PER], bs[QPK];
+#pragma unroll
+    for (int h = 0; h < QPK; ++h) {
+        bs[h] = s_base[h];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) kv[h][e] = s_keys[h][e * kScoreThreads + threadIdx.x];
+    }
+#pragma unroll
+    for (int h = 0; h < QPK; ++h) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const uint32_t key = kv[h][e];
+            const uint32_t d = (key >> 8) - bs[h];  // wraps for keys below the window
+            if (d < static_cast<uint32_t>(kWinBins)) atomicAdd(&s_win[h][d][(key & 0xffu) >> 1], 1u << ((key & 1u) * 16));
+        }
+    }
+    __syncthreads();
+}
+
 // grid.x: token tiles of kScoreThreads * score_tokens_per_thread<G>(); grid.y: batch*kv_heads.
 // QT is the raw query type when the kernel encodes the query itself
 // (layer step), void when it reads a pre-encoded state.
-template <int G, int QPK, typename QT>
+template <int G, int QPK, typename QT, bool WIN>
 __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
     const float* __restrict__ q_low, const float* __restrict__ q_delta, const QT* __restrict__ q_raw,
@@ -353,7 +421,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const uint16_t* __restrict__ k_low, const uint16_t* __restrict__ k_delta,
     const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, int qpk_rt,
     int64_t cap, int64_t tokens, uint16_t* __restrict__ scores, int64_t out_stride,
-    uint32_t* __restrict__ ghist, SeqTable seq) {
+    uint32_t* __restrict__ ghist, SeqTable seq, TileWindows win) {
     constexpr int R = 128 / G;
     // Layer-step mode (the kernel encodes the raw query): the output holds the
     // scores' radix order keys instead of fp16 bits, and the per-head 256-bin
@@ -425,8 +493,25 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
 
     __shared__ GroupState<G> st;
     __shared__ uint32_t s_hist[STEP ? (QPK > 0 ? QPK : kMaxGroupHeads) : 1][256];
+    // tile windows (layer step, compile-time group size; a separate
+    // instantiation, so the plain scorer keeps its register count -- 79
+    // VGPRs at G64, three workgroups per CU at C4 instead of two): every key
+    // of the tile, and the windows' low-byte histograms (16-bit pairs)
+    constexpr bool WINK = WIN && STEP && QPK > 0;
+    constexpr int TILE = kScoreThreads * TPT;
+    __shared__ uint16_t s_keys[WINK ? QPK : 1][WINK ? TILE : 2];
+    __shared__ uint32_t s_win[WINK ? QPK : 1][kWinBins][128];
+    __shared__ uint32_t s_base[WINK ? QPK : 1];
+    const bool win_on = WINK && win.rec != nullptr;
     if constexpr (STEP) {
         for (int i = threadIdx.x; i < qpk * 256; i += kScoreThreads) (&s_hist[0][0])[i] = 0u;
+    }
+    if constexpr (WINK) {
+        if (win_on) {
+            for (int i = threadIdx.x; i < QPK * TILE / 2; i += kScoreThreads)
+                reinterpret_cast<uint32_t*>(&s_keys[0][0])[i] = 0u;
+            for (int i = threadIdx.x; i < QPK * kWinBins * 128; i += kScoreThreads) (&s_win[0][0][0])[i] = 0u;
+        }
     }
     if constexpr (std::is_void_v<QT>) {
         load_group_state<G>(q_sign, q_mag, q_low, q_delta, qrow0, qpk, st);
@@ -524,6 +609,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
                 // end-of-kernel write-back is shorter (C1 step 28.2 -> 27.7 us)
                 __hip_atomic_store(dst, static_cast<uint16_t>(key), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 atomicAdd(&s_hist[h][(key >> 8) & 0xffu], 1u);
+                if constexpr (WINK) {
+                    if (win_on) s_keys[h][it * kScoreThreads + threadIdx.x] = static_cast<uint16_t>(key);
+                }
             } else {
                 *dst = bits;
             }
@@ -531,9 +619,27 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     }
     if constexpr (STEP) {
         __syncthreads();
+        // the tile windows' LDS work first, then every global write of the
+        // epilogue together (the histogram atomics would otherwise hold the
+        // windows' LDS work back behind their issue)
+        if constexpr (WINK) {
+            if (win_on) tile_windows<QPK, TILE>(s_hist, s_keys, s_win, s_base, win, qrow0, ntok_b,
+                                                seq.tokens != nullptr
+                                                    ? min(static_cast<int64_t>(seq.budget) - 1, ntok_b)
+                                                    : static_cast<int64_t>(win.k));
+        }
         for (int i = threadIdx.x; i < qpk * 256; i += kScoreThreads) {
             const uint32_t c = (&s_hist[0][0])[i];
             if (c != 0u) atomicAdd(&ghist[(qrow0 + i / 256) * 256 + (i & 255)], c);
+        }
+        if constexpr (WINK) {
+            if (win_on) {
+                for (int i = threadIdx.x; i < QPK * kWinBins * 32; i += kScoreThreads) {
+                    const int h = i / (kWinBins * 32), r = i - h * (kWinBins * 32);
+                    const uint4 v = reinterpret_cast<const uint4*>(&s_win[h][0][0])[r];
+                    reinterpret_cast<uint4*>(win.bins + ((qrow0 + h) * win.tiles + blockIdx.x) * (kWinBins * 128))[r] = v;
+                }
+            }
         }
     }
 }
@@ -611,21 +717,33 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
                                const int32_t* ks, const int32_t* km, const uint16_t* kl, const uint16_t* kd,
                                const int64_t* h2k, int64_t batch, int qh, int kvh, int64_t cap, int64_t tokens,
                                uint16_t* out, int64_t out_stride, uint32_t* ghist, const SeqTable& seq,
-                               hipStream_t stream) {
+                               hipStream_t stream, const TileWindows& win) {
     const int qpk = qh / kvh;
     const int64_t per_block = static_cast<int64_t>(kScoreThreads) * score_tokens_per_thread<G>();
     dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block), static_cast<unsigned>(batch * kvh));
     const uint4* ks4 = reinterpret_cast<const uint4*>(ks);
     const uint4* km4 = reinterpret_cast<const uint4*>(km);
-#define POPKV_SCORE_LAUNCH(Q)                                                                                 \
-    hipLaunchKernelGGL((score_d128_kernel<G, Q, QT>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd, q_raw, \
-                       ks4, km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride, ghist, seq)
+#define POPKV_SCORE_LAUNCH(Q, W)                                                                              \
+    hipLaunchKernelGGL((score_d128_kernel<G, Q, QT, W>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd,    \
+                       q_raw, ks4, km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride, ghist, seq, win)
+    // the tile windows: the layer step's G64 scorer with a compile-time group
+    constexpr bool kWinG = G == 64 && !std::is_void_v<QT>;
+    if (kWinG && win.rec != nullptr) {
+        switch (qpk) {
+            case 1: POPKV_SCORE_LAUNCH(1, kWinG); break;
+            case 2: POPKV_SCORE_LAUNCH(2, kWinG); break;
+            case 4: POPKV_SCORE_LAUNCH(4, kWinG); break;
+            case 8: POPKV_SCORE_LAUNCH(8, kWinG); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (qpk) {
-        case 1: POPKV_SCORE_LAUNCH(1); break;
-        case 2: POPKV_SCORE_LAUNCH(2); break;
-        case 4: POPKV_SCORE_LAUNCH(4); break;
-        case 8: POPKV_SCORE_LAUNCH(8); break;
-        default: POPKV_SCORE_LAUNCH(0); break;
+        case 1: POPKV_SCORE_LAUNCH(1, false); break;
+        case 2: POPKV_SCORE_LAUNCH(2, false); break;
+        case 4: POPKV_SCORE_LAUNCH(4, false); break;
+        case 8: POPKV_SCORE_LAUNCH(8, false); break;
+        default: POPKV_SCORE_LAUNCH(0, false); break;
     }
 #undef POPKV_SCORE_LAUNCH
     return hipGetLastError();
@@ -636,20 +754,21 @@ hipError_t launch_score_d128_q(const int32_t* q_sign, const int32_t* q_mag, cons
                                const QT* q_raw, const int32_t* k_sign, const int32_t* k_mag, const uint16_t* k_low,
                                const uint16_t* k_delta, const int64_t* head_to_kv, int64_t batch, int q_heads,
                                int kv_heads, int64_t capacity, int64_t tokens, int dim_group_size, uint16_t* scores,
-                               int64_t score_row_stride, uint32_t* ghist, const SeqTable& seq, hipStream_t stream) {
+                               int64_t score_row_stride, uint32_t* ghist, const SeqTable& seq, hipStream_t stream,
+                               const TileWindows& win = TileWindows{}) {
     switch (dim_group_size) {
         case 16:
             return launch_score_d128_g<16, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
-                                               score_row_stride, ghist, seq, stream);
+                                               score_row_stride, ghist, seq, stream, win);
         case 32:
             return launch_score_d128_g<32, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
-                                               score_row_stride, ghist, seq, stream);
+                                               score_row_stride, ghist, seq, stream, win);
         default:
             return launch_score_d128_g<64, QT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, scores,
-                                               score_row_stride, ghist, seq, stream);
+                                               score_row_stride, ghist, seq, stream, win);
     }
 }
 
@@ -686,23 +805,23 @@ hipError_t launch_score_d128_raw(const void* queries, int dtype, const int32_t* 
                                  const uint16_t* k_low, const uint16_t* k_delta, const int64_t* head_to_kv,
                                  int64_t batch, int q_heads, int kv_heads, int64_t capacity, int64_t tokens,
                                  int dim_group_size, uint16_t* keys, int64_t key_row_stride, uint32_t* ghist,
-                                 const SeqTable& seq, hipStream_t stream) {
+                                 const SeqTable& seq, hipStream_t stream, const TileWindows& win) {
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_score_d128_q<float>(nullptr, nullptr, nullptr, nullptr, static_cast<const float*>(queries),
                                               k_sign, k_mag, k_low, k_delta, head_to_kv, batch, q_heads, kv_heads,
                                               capacity, tokens, dim_group_size, keys, key_row_stride, ghist, seq,
-                                              stream);
+                                              stream, win);
         case POPKV_DTYPE_F16:
             return launch_score_d128_q<f16_t>(nullptr, nullptr, nullptr, nullptr, static_cast<const f16_t*>(queries),
                                               k_sign, k_mag, k_low, k_delta, head_to_kv, batch, q_heads, kv_heads,
                                               capacity, tokens, dim_group_size, keys, key_row_stride, ghist, seq,
-                                              stream);
+                                              stream, win);
         default:
             return launch_score_d128_q<bf16_t>(nullptr, nullptr, nullptr, nullptr,
                                                static_cast<const bf16_t*>(queries), k_sign, k_mag, k_low, k_delta,
                                                head_to_kv, batch, q_heads, kv_heads, capacity, tokens, dim_group_size,
-                                               keys, key_row_stride, ghist, seq, stream);
+                                               keys, key_row_stride, ghist, seq, stream, win);
     }
 }
 

@@ -406,13 +406,13 @@ def popkv_layer_step(
 
 
 def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor,
-                               head_to_kv: torch.Tensor, *, budget: int,
+                               head_to_kv: torch.Tensor, *, budget: int, dim_group_size: int,
                                workspace: LayerStepWorkspace | torch.Tensor) -> None:
     """Re-run only the fused select + sparse-attention kernel of the last
-    ``popkv_layer_step`` that used ``workspace`` (same shapes and budget); it
-    reads the keys and threshold histograms the step left there and rewrites
-    the chunk partials inside the workspace.  A timing aid for the step's
-    dominant kernel."""
+    ``popkv_layer_step`` that used ``workspace`` (same shapes, budget and
+    dim_group_size); it reads the keys and threshold data the step left
+    there and rewrites the chunk partials inside the workspace.  A timing
+    aid for the step's dominant kernel."""
     if q.ndim != 2 or int(q.shape[1]) != 128 or not q.is_contiguous():
         raise ValueError("popkv_layer_step_attention requires a contiguous q [query heads, 128]")
     if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
@@ -426,6 +426,8 @@ def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v
         raise ValueError("invalid score token count")
     if budget <= 1:
         raise ValueError("budget must reserve at least one retrieved and one current token")
+    if dim_group_size not in (16, 32, 64):
+        raise ValueError("dim_group_size must be one of 16, 32, 64")
     _check_head_mapping(head_to_kv, q_heads)
     ws = workspace if isinstance(workspace, torch.Tensor) else workspace.buffer
     if ws is None:
@@ -438,7 +440,7 @@ def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v
     with torch.cuda.device(dev):
         nat.call("popkv_layer_step_attention", q.data_ptr(), nat.dtype_code(q), prefix_k.data_ptr(),
                  prefix_v.data_ptr(), prefix_k.stride(0), prefix_v.stride(0), mapping.data_ptr(), q_heads, kv_heads,
-                 tokens, int(budget), ws.data_ptr(), ws.numel(), nat.stream_of(dev))
+                 tokens, int(budget), int(dim_group_size), ws.data_ptr(), ws.numel(), nat.stream_of(dev))
 
 
 def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torch.Tensor, k: torch.Tensor,

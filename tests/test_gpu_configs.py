@@ -283,6 +283,28 @@ def test_layer_step_every_chunk_plan(context, budget, kpt):
     _check_full_layer(w, seed=300 + kpt, check_prepack=False, api_path=False)
 
 
+@pytest.mark.parametrize("context,ramp", [(32768, 4.0), (16384, 0.35), (16384, 8.0)])
+def test_layer_step_tile_windows_that_miss_the_threshold(context, ramp):
+    """Keys scaled by a ramp along the tokens (1 + ramp * t / L), so the
+    scorer's per-tile estimates of a row's threshold bin drift away from
+    the row's own: many tiles' windows miss it (ramp 4) or a few do (ramp
+    0.35), and the select histograms those tiles from their keys.
+    Indices exact and attention within tolerance against the oracle."""
+    w = workloads.scaled(workloads.C1, context=context, budget=min(4096, context // 2))
+    layer = workloads.make_layer(w, seed=900 + context)
+    scale = (1.0 + ramp * torch.arange(context, dtype=torch.float32) / context)[None, :, None]
+    layer = workloads.LayerInputs((layer.keys.float() * scale).to(w.dtype), layer.values, layer.queries)
+    layer = layer.to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    cache = popkv.build_popkv_cache(layer.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                    reserve_tokens=64)
+    sc, idx, out = _oracle(w, layer, mapping, cache)
+    o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(got.cpu().numpy(), idx)
+    _assert_attention(o, out)
+
+
 # ------------------------------------------------------------------ tie rule vs torch.topk
 
 def _tie_rows(kind: str, rows: int, tokens: int, seed: int) -> torch.Tensor:

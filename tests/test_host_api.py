@@ -217,10 +217,11 @@ def test_layer_step_attention_rejects_mismatched_operands_before_the_device():
     ws = torch.zeros(1 << 16, dtype=torch.uint8)
     att = lambda **kw: popkv.popkv_layer_step_attention(  # noqa: E731
         kw.get("q", q), kw.get("pk", pk), kw.get("pv", pk), kw.get("h2k", h2k), budget=kw.get("budget", 16),
-        workspace=kw.get("ws", ws))
+        dim_group_size=kw.get("g", 64), workspace=kw.get("ws", ws))
     for kw, msg in [(dict(q=q[:, :64]), "requires a contiguous q"), (dict(pv=pk[:1]), "prefix K/V must be"),
                     (dict(q=q[:7]), "positive multiple"), (dict(h2k=h2k[:3]), "head_to_kv"),
                     (dict(budget=1), "budget"), (dict(pk=pk[:, :0], pv=pk[:, :0]), "token count"),
+                    (dict(g=8), "dim_group_size"),
                     (dict(ws=popkv.LayerStepWorkspace()), "has not been used")]:
         with pytest.raises(ValueError, match=msg):
             att(**kw)
