@@ -107,7 +107,7 @@ int popkv_score(const void* queries, int32_t dtype, int64_t batch, int64_t q_hea
 /* Per-row top-k over fp16 scores: the k largest (PyTorch's fp16 radix order,
  * -0 < +0, NaN largest), ties at the k-th value taken in ascending token
  * order, written in ascending token order to indices[r, 0..k), and `current`
- * written to indices[r, k].  0 <= k <= tokens.  tokens <= 131072 per row.
+ * written to indices[r, k].  0 <= k <= tokens.  tokens <= 524288 per row.
  * Needs popkv_topk_select_workspace_bytes(rows, tokens) bytes of 256-byte
  * aligned workspace whose first rows * 1024 bytes (the per-row histograms)
  * are zero when the call begins; every call leaves them zero again, so the
@@ -198,7 +198,7 @@ int popkv_layer_step(const void* queries, int32_t dtype,
  *                          token_counts[b] cached tokens (rows 0 .. count-1
  *                          of its caches); the current token is index count.
  * max_tokens (host) bounds every count (1 <= max_tokens <= capacity,
- * cache_rows, 131072) and sizes the launch; a count above it is treated as
+ * cache_rows, 524288) and sizes the launch; a count above it is treated as
  * max_tokens.  Sequence b selects k_b = min(budget - 1, count_b) tokens;
  * indices_out (optional) [B, QH, index_row_stride] int64 receives them in
  * ascending order with the current token at slot k_b (entries past k_b are

@@ -40,7 +40,12 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-constexpr int64_t kMaxSelectTokens = 1024 * 128;
+// Longest row the selects take: 64 chunks of 32 keys per thread x 256
+// threads (a chunk's in-chunk offsets and low-byte histogram counts are
+// 16-bit, its chunk counts one per lane of a wave); step_chunks raises the
+// keys per thread until a row fits in 64 chunks.
+constexpr int64_t kMaxSelectTokens = int64_t{64} * popkv::kMaxChunkKeys * popkv::kChunkThreads;
+static_assert(kMaxSelectTokens == 524288, "64 chunks of 8192 tokens");
 constexpr int64_t kMaxGroupHeads = 64;
 constexpr size_t kAlign = 256;
 
@@ -273,7 +278,7 @@ int popkv_topk_select(const void* scores, int64_t rows, int64_t row_stride, int6
     if (index_row_stride < k + 1) return fail(POPKV_ERR_INVALID, "index row stride too small");
     if (index_dtype != POPKV_INDEX_I64 && index_dtype != POPKV_INDEX_I32)
         return fail(POPKV_ERR_INVALID, "index dtype must be int64 or int32");
-    if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens per row");
+    if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 524288 tokens per row");
     if (rows > 0x7fffffff / 32) return fail(POPKV_ERR_UNSUPPORTED, "too many rows");
     if (workspace_bytes < popkv::topk_select_workspace_bytes(rows, tokens))
         return fail(POPKV_ERR_WORKSPACE, "top-k select needs %zu workspace bytes",
@@ -362,7 +367,7 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     if (budget <= 1) return fail(POPKV_ERR_INVALID, "budget must reserve at least one retrieved and one current token");
     int st = check_score_common(head_to_kv, 1, q_heads, kv_heads, capacity, tokens, dim_group_size);
     if (st) return st;
-    if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens");
+    if (tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 524288 tokens");
     const StepLayout L = step_layout(q_heads, tokens, budget, dim_group_size);
     if (!workspace || workspace_bytes < L.total)
         return fail(POPKV_ERR_WORKSPACE, "layer step needs %zu workspace bytes", L.total);
@@ -520,7 +525,7 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
     if (batch <= 0) return fail(POPKV_ERR_INVALID, "empty batch");
     int st = check_score_common(head_to_kv, batch, q_heads, kv_heads, capacity, max_tokens, dim_group_size);
     if (st) return st;
-    if (max_tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 131072 tokens");
+    if (max_tokens > kMaxSelectTokens) return fail(POPKV_ERR_UNSUPPORTED, "select supports at most 524288 tokens");
     if (max_tokens > cache_rows) return fail(POPKV_ERR_CAPACITY, "max_tokens exceeds the static cache rows");
     const int64_t kmax = budget - 1 < max_tokens ? budget - 1 : max_tokens;
     if (indices_out && index_row_stride < kmax + 1) return fail(POPKV_ERR_INVALID, "index row stride too small");

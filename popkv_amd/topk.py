@@ -16,7 +16,7 @@ import torch
 
 from . import _native as nat
 
-MAX_SELECT_TOKENS = 131072
+MAX_SELECT_TOKENS = 524288  # 64 chunks of 8192 tokens (the C ABI checks the same bound)
 
 
 # Reusable workspaces, one per (device, stream): the native select keeps

@@ -281,11 +281,26 @@ def test_select_matches_oracle(kind, tokens):
         assert np.array_equal(got.cpu().numpy(), want), (kind, tokens, k)
 
 
-@pytest.mark.parametrize("tokens", [65535, 131071])
+@pytest.mark.parametrize("tokens", [65535, 131071, 200000, 524288])
 def test_select_long_rows(tokens):
     s = _scores("peaked", 3, tokens, seed=5)
     got = topk.select_with_current(s, 4095, tokens + 1)
     assert np.array_equal(got.cpu().numpy(), core.select(bits(s), 4095, tokens))
+
+
+def test_select_rows_past_131072_tokens_ties_and_torch_topk():
+    """32 rows of 200000 tie-heavy fp16 scores (values -3 .. 3): the select
+    equals the oracle's stable order and torch.topk's index sets at k = 4095
+    and 100000; a row of 524289 tokens is refused."""
+    s = _scores("ties", 32, 200000, seed=21)
+    for k in (4095, 100000):
+        got = topk.select_with_current(s, k, 200001).cpu().numpy()
+        assert np.array_equal(got, core.select(bits(s), k, 200000)), k
+        ref = torch.topk(s, k, dim=-1, sorted=False).indices.cpu().numpy()
+        for r in range(0, 32, 7):
+            assert set(got[r, :k].tolist()) == set(ref[r].tolist()), (k, r)
+    with pytest.raises(RuntimeError, match="524288"):
+        topk.select_with_current(torch.zeros(1, 524289, dtype=torch.float16, device=DEV), 10, 524290)
 
 
 @pytest.mark.parametrize("kind", ["ties", "two_values", "signed_zero", "random"])
@@ -472,6 +487,17 @@ def test_layer_step_long_context(context):
     """C3's long contexts: more than 32 key rounds per select thread (keys
     re-read per pass) and 4096-token attention chunks."""
     w = workloads.scaled(workloads.c3(context), context=context)
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
+@pytest.mark.parametrize("context,budget", [(200001, 4096), (262145, 65536)])
+def test_layer_step_rows_past_131072_tokens(context, budget):
+    """Rows beyond 131072 tokens (the selects take up to 64 chunks of 8192):
+    200000 cached tokens at budget 4096 (25 chunks) and 262144 at budget
+    65536 (32 chunks holding about 2048 selected tokens each).  Indices
+    exact, attention within tolerance, against the oracle."""
+    w = workloads.scaled(workloads.c3(131072), context=context, budget=budget)
     layer, mapping, cache = _layer_setup(w)
     _check_layer_step(w, layer, mapping, cache)
 

@@ -360,7 +360,7 @@ def test_library_host_only_entry_points():
     assert ws_bytes >= 4 * 256 * 4 + 4 * 128 * 2
     st = lib.popkv_topk_select(fake, 4, 10, 10, 11, 10, fake, 0, 12, fake, ws_bytes, None)
     assert st == -1
-    st = lib.popkv_topk_select(fake, 4, 200000, 200000, 11, 10, fake, 0, 12, fake, 1 << 30, None)
+    st = lib.popkv_topk_select(fake, 4, 524289, 524289, 11, 10, fake, 0, 12, fake, 1 << 30, None)
     assert st == -4
     st = lib.popkv_topk_select(fake, 4, 100, 100, 11, 10, fake, 0, 12, None, ws_bytes, None)
     assert st == -1 and "null" in lib.popkv_last_error().decode()
