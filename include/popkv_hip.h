@@ -318,7 +318,12 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype,
  * to output [QH, 128].  prefix K/V [KVH, tokens, 128], rows contiguous, any
  * head stride; tokens may be 0.  Needs
  * popkv_dense_attention_workspace_bytes() bytes of 16-byte aligned
- * workspace (no initialisation needed).  Replaces the full-layer branch of
+ * workspace whose first q_heads * 4 bytes, rounded up to 256 (the merge
+ * tickets), are zero when the call begins; every call leaves them zero
+ * (after a call with fewer query heads, clear the larger region first).
+ * fp16/bf16 groups of 4 query heads over at most 32768 tokens run in one
+ * launch (each KV group's last workgroup merges), others in two.
+ * Replaces the full-layer branch of
  * LlamaSparseDecoder.decode (reference popkv.py:1022-1038: torch.cat of the
  * prefix and current K/V, then scaled_dot_product_attention on the grouped
  * view q.view(KVH, QH/KVH, 1, D)). */

@@ -420,13 +420,13 @@ __device__ __forceinline__ int64_t merge_kv_row(const SeqTable& seq, const int64
 // No LDS or barrier: the split maxima and denominators are wave reductions
 // (lane s holds split s of each 64-split group), and the weights reach the
 // accumulation through readlane.  qh, ck, cv, the first group's maxima and
-// denominators and the first kMergeFirst splits' accumulators are loaded in
-// one burst, so a layer step's merge pays one memory latency for all of
-// them; further splits follow in batches of kMergeFirst.  Accumulation
+// denominators and the first NF splits' accumulators are loaded in one
+// burst, so a layer step's merge pays one memory latency for all of them;
+// further splits follow in batches of NF.  Accumulation
 // order: the current token, then the splits in ascending order.  COH: the
 // states are read with device-coherent loads (written by other workgroups
 // of the same kernel).
-template <typename T, bool COH>
+template <typename T, bool COH, int NF = kMergeFirst>
 __device__ __forceinline__ void merge_head(const float* __restrict__ ps, int nsplit, const T* __restrict__ qh,
                                            const T* __restrict__ ck, const T* __restrict__ cv, float scale,
                                            T* __restrict__ outh) {
@@ -442,10 +442,10 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ ps, int nsp
         m0 = ld_f32<COH>(ps + (static_cast<int64_t>(lane) * S));
         l0 = ld_f32<COH>(ps + (static_cast<int64_t>(lane) * S + 1));
     }
-    const int nf = min(nsplit, kMergeFirst);
-    float a0[kMergeFirst], a1[kMergeFirst];
+    const int nf = min(nsplit, NF);
+    float a0[NF], a1[NF];
 #pragma unroll
-    for (int j = 0; j < kMergeFirst; ++j) {
+    for (int j = 0; j < NF; ++j) {
         const int64_t so = static_cast<int64_t>(max(min(j, nf - 1), 0)) * S + 2;
         a0[j] = ld_f32<COH>(ps + (so + lane));
         a1[j] = ld_f32<COH>(ps + (so + lane + 64));
@@ -460,7 +460,7 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ ps, int nsp
     const float w0 = m0 == -INFINITY ? 0.0f : __expf(m0 - mx);
     float den = l0 * w0, num0 = wc * v0, num1 = wc * v1;
 #pragma unroll
-    for (int j = 0; j < kMergeFirst; ++j) {
+    for (int j = 0; j < NF; ++j) {
         if (j < nf) {
             const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w0), j));
             num0 = fmaf(ws, a0[j], num0);
@@ -479,16 +479,16 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ ps, int nsp
             den += l * w;
         }
         const int n = min(kWave, nsplit - s0);
-        for (int b = s0 == 0 ? nf : 0; b < n; b += kMergeFirst) {
-            float c0[kMergeFirst], c1[kMergeFirst];
+        for (int b = s0 == 0 ? nf : 0; b < n; b += NF) {
+            float c0[NF], c1[NF];
 #pragma unroll
-            for (int j = 0; j < kMergeFirst; ++j) {
+            for (int j = 0; j < NF; ++j) {
                 const int64_t so = static_cast<int64_t>(s0 + min(b + j, n - 1)) * S + 2;
                 c0[j] = ld_f32<COH>(ps + (so + lane));
                 c1[j] = ld_f32<COH>(ps + (so + lane + 64));
             }
 #pragma unroll
-            for (int j = 0; j < kMergeFirst; ++j) {
+            for (int j = 0; j < NF; ++j) {
                 if (b + j < n) {
                     const float ws =
                         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b + j));
@@ -1163,6 +1163,10 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
 // prefix token attends; the current token joins in the merge, as in the
 // layer step.  Splits of kDenseSplit tokens.
 constexpr int kDenseSplit = 512;
+// The MFMA kernel fuses the merge for up to this many splits (64 x 512 =
+// 32768 tokens: the merge loads every split's accumulators in one burst);
+// longer prefixes take the separate wide merge.
+constexpr int kDenseFusedMaxSplits = 64;
 
 // Dense attention, one GQA group per workgroup: the QPK query heads of KV
 // head g share every K/V row, so workgroup (s, g) reads each row of its
@@ -1241,7 +1245,8 @@ __device__ __forceinline__ mfma_f32x4 mfma_16x16x32(uint4 a, uint4 b, mfma_f32x4
 template <typename T>
 __global__ __launch_bounds__(kAttnThreads) void attn_dense_mfma_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
-    int64_t tokens, float scale, float* __restrict__ partials, int nsplit) {
+    int64_t tokens, float scale, float* __restrict__ partials, int nsplit, uint32_t* __restrict__ tickets,
+    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out) {
     constexpr int D = 128, QPK = 4, TILE = 16;
     constexpr int WTOK = kDenseSplit / kAttnWaves;  // tokens per wave
     constexpr int NT = WTOK / TILE;                  // tiles per wave
@@ -1349,6 +1354,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_mfma_kernel(
         if (it + AHEAD < NT) load_tile(it + AHEAD, kt[(it + AHEAD) % (AHEAD + 1)], vt[(it + AHEAD) % (AHEAD + 1)]);
         fold_tile(it, kt[it % (AHEAD + 1)], vt[it % (AHEAD + 1)]);
     }
+    const bool fused = tickets != nullptr;  // the merge runs in the group's last block (below)
 #pragma unroll
     for (int j = 0; j < QPK; ++j) {
         SoftmaxState st;
@@ -1357,9 +1363,31 @@ __global__ __launch_bounds__(kAttnThreads) void attn_dense_mfma_kernel(
 #pragma unroll
         for (int d = 0; d < 8; ++d) st.acc[d] = acc[j][d];
         store_partial<16>(st, lane, wave, 8 * col, D,
-                          partials + (static_cast<int64_t>(g * QPK + j) * nsplit + s) * (D + 2));
+                          partials + (static_cast<int64_t>(g * QPK + j) * nsplit + s) * (D + 2), fused);
         __syncthreads();  // store_partial's LDS is reused by the next head
     }
+    if (!fused) return;
+    // Fused merge, as in the layer step's select + attention kernel: the
+    // states went out with device-coherent stores; once this block's are
+    // acknowledged (the gfx942 / gfx950 rule stated at st_f32) it takes a
+    // ticket on tickets[g] (zero between calls), and the group's last block
+    // merges each of its heads' splits with the current token (wave j: head
+    // g * QPK + j, every split's accumulators loaded in one burst of up to
+    // 64) and resets the ticket.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&tickets[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old + 1u == static_cast<uint32_t>(nsplit) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last == 0u) return;
+    if (threadIdx.x == 0) __hip_atomic_store(&tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int h = g * QPK + wave;
+    merge_head<T, true, 64>(partials + static_cast<int64_t>(h) * nsplit * (D + 2), nsplit,
+                            q + static_cast<int64_t>(h) * D, cur_k + static_cast<int64_t>(g) * D,
+                            cur_v + static_cast<int64_t>(g) * D, scale, out + static_cast<int64_t>(h) * D);
 }
 
 
@@ -1854,7 +1882,8 @@ hipError_t launch_merge_current(const float* partials, int nsplit, const void* q
 namespace {
 template <typename T>
 hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t k_hs, int64_t v_hs, int64_t tokens,
-                          int nsplit, int q_heads, int kv_heads, float* partials, hipStream_t stream) {
+                          int nsplit, int q_heads, int kv_heads, float* partials, const DenseMerge* merge,
+                          hipStream_t stream) {
     const float scale = static_cast<float>(1.0 / sqrt(128.0));
     const dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(kv_heads));
     const T *q_ = static_cast<const T*>(q), *k_ = static_cast<const T*>(kc), *v_ = static_cast<const T*>(vc);
@@ -1863,8 +1892,12 @@ hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t
                        v_hs, tokens, scale, partials, nsplit)
     if constexpr (sizeof(T) == 2) {
         if (q_heads == 4 * kv_heads) {
+            const bool fuse = merge != nullptr && nsplit <= kDenseFusedMaxSplits;
             hipLaunchKernelGGL((attn_dense_mfma_kernel<T>), grid, dim3(kAttnThreads), 0, stream, q_, k_, v_, k_hs, v_hs,
-                               tokens, scale, partials, nsplit);
+                               tokens, scale, partials, nsplit, fuse ? merge->tickets : nullptr,
+                               fuse ? static_cast<const T*>(merge->current_k) : nullptr,
+                               fuse ? static_cast<const T*>(merge->current_v) : nullptr,
+                               fuse ? static_cast<T*>(merge->output) : nullptr);
             return hipGetLastError();
         }
     }
@@ -1881,20 +1914,25 @@ hipError_t launch_dense_t(const void* q, const void* kc, const void* vc, int64_t
 
 int dense_splits(int64_t tokens) { return static_cast<int>((tokens + kDenseSplit - 1) / kDenseSplit); }
 
+bool dense_merge_fuses(int dtype, int64_t tokens, int q_heads, int kv_heads) {
+    const int ns = dense_splits(tokens);
+    return dtype != POPKV_DTYPE_F32 && q_heads == 4 * kv_heads && ns > 0 && ns <= kDenseFusedMaxSplits;
+}
+
 hipError_t launch_attention_dense(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                   int64_t k_head_stride, int64_t v_head_stride, int64_t tokens, int q_heads,
-                                  int kv_heads, float* partials, hipStream_t stream) {
+                                  int kv_heads, float* partials, hipStream_t stream, const DenseMerge* merge) {
     const int ns = dense_splits(tokens);
     switch (dtype) {
         case POPKV_DTYPE_F32:
             return launch_dense_t<float>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
-                                         q_heads, kv_heads, partials, stream);
+                                         q_heads, kv_heads, partials, merge, stream);
         case POPKV_DTYPE_F16:
             return launch_dense_t<f16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
-                                         q_heads, kv_heads, partials, stream);
+                                         q_heads, kv_heads, partials, merge, stream);
         default:
             return launch_dense_t<bf16_t>(queries, prefix_k, prefix_v, k_head_stride, v_head_stride, tokens, ns,
-                                          q_heads, kv_heads, partials, stream);
+                                          q_heads, kv_heads, partials, merge, stream);
     }
 }
 }  // namespace popkv

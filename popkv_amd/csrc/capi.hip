@@ -718,10 +718,14 @@ int popkv_layer_step_attention(const void* queries, int32_t dtype, const void* p
                     "popkv_layer_step_attention");
 }
 
+// Dense-attention workspace: [align_up(QH * 4)] u32 merge tickets (zero
+// between calls; KVH <= QH of them used) | [QH][splits][130] f32 partials.
+size_t dense_tickets_bytes(int64_t q_heads) { return align_up(static_cast<size_t>(q_heads) * 4); }
+
 size_t popkv_dense_attention_workspace_bytes(int64_t q_heads, int64_t tokens) {
     if (q_heads <= 0 || tokens < 0) return 0;
     const int64_t ns = popkv::dense_splits(tokens);
-    return align_up(static_cast<size_t>(q_heads * (ns > 0 ? ns : 1) * (128 + 2)) * 4);
+    return dense_tickets_bytes(q_heads) + align_up(static_cast<size_t>(q_heads * (ns > 0 ? ns : 1) * (128 + 2)) * 4);
 }
 
 int popkv_dense_attention(const void* queries, int32_t dtype, const void* prefix_k, const void* prefix_v,
@@ -745,14 +749,20 @@ int popkv_dense_attention(const void* queries, int32_t dtype, const void* prefix
         (k_head_stride * es) % 16 || (v_head_stride * es) % 16)
         return fail(POPKV_ERR_UNSUPPORTED, "dense attention tensors need 16-byte alignment");
     hipStream_t s = as_stream(stream);
-    float* partials = static_cast<float*>(workspace);
+    uint32_t* tickets = static_cast<uint32_t*>(workspace);
+    float* partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + dense_tickets_bytes(q_heads));
     const int ns = popkv::dense_splits(tokens);
     if (ns > 0) {
+        // the merge inside the attention launch where it fuses (the group's
+        // last block merges), else the merge kernel below
+        const bool fused = popkv::dense_merge_fuses(dtype, tokens, static_cast<int>(q_heads), static_cast<int>(kv_heads));
+        const popkv::DenseMerge dm{tickets, current_k, current_v, output};
         const int st = launched(popkv::launch_attention_dense(queries, dtype, prefix_k, prefix_v, k_head_stride,
                                                               v_head_stride, tokens, static_cast<int>(q_heads),
-                                                              static_cast<int>(kv_heads), partials, s),
+                                                              static_cast<int>(kv_heads), partials, s,
+                                                              fused ? &dm : nullptr),
                                 "popkv_dense_attention(attention)");
-        if (st) return st;
+        if (st || fused) return st;
     }
     return launched(popkv::launch_merge_current(partials, ns, queries, dtype, current_k, current_v, nullptr,
                                                 static_cast<int>(q_heads), static_cast<int>(kv_heads), output,

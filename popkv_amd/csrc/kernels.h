@@ -200,9 +200,21 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
 // Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one
 // workgroup serves a whole group.
 int dense_splits(int64_t tokens);
+// The dense layer's merge fused into its attention launch: tickets[KVH]
+// (zero on entry, left zero), the current token and the output.  Taken when
+// dense_merge_fuses(): fp16 / bf16, GQA groups of 4 (the MFMA kernel), at
+// most 64 splits; otherwise launch_merge_current follows the launch.
+struct DenseMerge {
+    uint32_t* tickets;
+    const void* current_k;
+    const void* current_v;
+    void* output;
+};
+bool dense_merge_fuses(int dtype, int64_t tokens, int q_heads, int kv_heads);
 hipError_t launch_attention_dense(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                   int64_t k_head_stride, int64_t v_head_stride, int64_t tokens, int q_heads,
-                                  int kv_heads, float* partials, hipStream_t stream);
+                                  int kv_heads, float* partials, hipStream_t stream,
+                                  const DenseMerge* merge = nullptr);
 
 // Layer-step merge of the split partials plus the current token (head_dim
 // 128); with idx_out non-null, also writes `current` to idx_out[h][idx_slot].

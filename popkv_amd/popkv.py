@@ -450,8 +450,8 @@ def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torc
     current one (the reference's full layers, popkv.py:1022-1038), one C-ABI
     call: q [QH, 128], prefix K/V [KVH, L, 128] with contiguous rows, current
     k/v [KVH, 128] -> [QH, 128], query head h reading KV head h // (QH/KVH).
-    The workspace holds split partials; do not share it with
-    popkv_layer_step, whose histogram region must stay zero."""
+    The workspace holds merge tickets and split partials; do not share it
+    with popkv_layer_step, whose histogram region must stay zero."""
     q_heads, kv_heads = _check_step_operands("dense_attention_step", q, prefix_k, prefix_v, k, v, out)
     if q_heads // kv_heads not in (1, 2, 4, 8):
         raise ValueError("dense attention supports 1, 2, 4 or 8 query heads per KV head")
@@ -460,7 +460,9 @@ def dense_attention_step(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v: torc
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
     tokens = int(prefix_k.shape[1])
     nbytes = int(nat.lib().popkv_dense_attention_workspace_bytes(q_heads, tokens))
-    ws = (workspace or LayerStepWorkspace()).get(nbytes, dev)
+    # (its first bytes hold the merge tickets: zero on entry, left zero; a
+    # change of head count clears them, as for the layer step's histograms)
+    ws = (workspace or LayerStepWorkspace()).get(nbytes, dev, q_heads)
     output = torch.empty_like(qc) if out is None else out
     with torch.cuda.device(dev):
         nat.call("popkv_dense_attention", qc.data_ptr(), nat.dtype_code(qc), prefix_k.data_ptr(), prefix_v.data_ptr(),

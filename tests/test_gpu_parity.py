@@ -552,6 +552,32 @@ def test_dense_attention_matches_oracle(context, dtype):
     np.testing.assert_allclose(f32(out), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
 
 
+def test_dense_attention_fused_merge_tickets_and_split_limit():
+    """The MFMA dense kernel's fused merge (each KV group's last workgroup
+    merges; tickets zero between calls): one reused workspace, calls at 64
+    splits (32768 tokens: fused), 65 splits (the separate merge), 8 query
+    heads and again 32 (the ticket region cleared on the head-count change),
+    each against the oracle; and the same call twice gives equal bits."""
+    ws = popkv.LayerStepWorkspace()
+    for q_heads, kv_heads, context, seed in ((32, 8, 32769, 1), (32, 8, 33281, 2), (8, 2, 5000, 3),
+                                             (32, 8, 32769, 4)):
+        base = workloads.scaled(workloads.C1, context=context, budget=2)
+        w = workloads.Workload(base.name, base.method, q_heads, kv_heads, 128, context, 2, base.token_group,
+                               base.dim_group, torch.bfloat16, seed, True)
+        lay = workloads.make_layer(w).to(DEV)
+        mapping = workloads.head_to_kv(w, DEV)
+        L = lay.prefix_tokens
+        args = (lay.queries, lay.prefix_k(), lay.prefix_v(), lay.current_k(), lay.current_v())
+        out = popkv.dense_attention_step(*args, workspace=ws)
+        again = popkv.dense_attention_step(*args, workspace=ws)
+        assert torch.equal(out, again), (q_heads, context)
+        idx = np.tile(np.arange(L + 1, dtype=np.int64), (w.q_heads, 1))
+        want = core.attention(f32(lay.queries), f32(lay.prefix_k()), f32(lay.prefix_v()), f32(lay.current_k()),
+                              f32(lay.current_v()), idx, mapping.cpu().numpy())
+        np.testing.assert_allclose(f32(out), want, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+        assert not ws.buffer[: 256].any(), "merge tickets left non-zero"
+
+
 @pytest.mark.parametrize("q_heads,kv_heads,dtype", [(8, 8, torch.bfloat16), (8, 4, torch.float16),
                                                      (16, 2, torch.bfloat16), (8, 2, torch.float16),
                                                      (16, 4, torch.float32)])
