@@ -45,11 +45,11 @@ N_BUFFERS = 8
 # HBM bytes per launch of the layer step's select + attention kernel at C1,
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script (KiB per
 # dispatch), each scaled by the same counter on a plain 256 MiB copy
-# (bench.py --copy-calibration): FETCH_SIZE reads 131084.3 KiB for the copy's
+# (bench.py --copy-calibration): FETCH_SIZE reads 131084.5 KiB for the copy's
 # 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).
-# attn_select_chunk_kernel: FETCH_SIZE 28683.7 KiB, WRITE_SIZE 298.9 KiB
-# (profiles/layer_step_c1_hbm_traffic.md).
-ATTN_TRAFFIC_BYTES = round(28683.7 * 1024 * (262144 / 131084.3) + 298.9 * 1024)
+# attn_select_chunk_kernel (the tile-window select): FETCH_SIZE 28848.9 KiB,
+# WRITE_SIZE 275.4 KiB (profiles/layer_step_c1_hbm_traffic.md).
+ATTN_TRAFFIC_BYTES = round(28848.9 * 1024 * (262144 / 131084.5) + 275.4 * 1024)
 
 
 def parse_args():

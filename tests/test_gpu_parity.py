@@ -607,6 +607,12 @@ def test_retrieval_step_with_torch_topk_hook():
         layer.queries, layer.prefix_k(), layer.prefix_v(), layer.current_k(), layer.current_v(), cache, mapping,
         budget=w.budget, topk=lambda s, k: torch.topk(s, k=k, dim=-1, sorted=False).indices)
     np.testing.assert_allclose(f32(hooked), f32(ours), atol=ATTN_ATOL, rtol=ATTN_RTOL)
+    # the reference's experimental_topk hook set to this build's select: the
+    # loop reads hook(scores, k)[0] (popkv.py:1091-1093)
+    ours_hook = popkv.popkv_retrieval_step(
+        layer.queries, layer.prefix_k(), layer.prefix_v(), layer.current_k(), layer.current_v(), cache, mapping,
+        budget=w.budget, topk=topk.topk_indices)
+    assert torch.equal(ours_hook, ours)
 
 
 def test_c1_full_size_parity():
