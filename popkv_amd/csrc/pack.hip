@@ -192,8 +192,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
 // head y, rows [x*tg, min(x*tg + tg, tokens)) of `keys`, into packed rows
 // y*cap + offset + x*tg + t.  Fused append (APPEND true): block i appends
 // the new token of (sequence, KV head) i (pack128_append).  STAGE (16-bit
-// rows, G 64, tg <= 64): the group's rows are read from memory once, into
-// LDS, and the encode pass reads them there.
+// rows; tg <= 64 at G 64, tg <= 128 at G 32 / G 16): the group's rows are
+// read from memory once, into LDS, and the encode pass reads them there.
 template <typename T, int G, bool APPEND, bool STAGE = false>
 __global__ __launch_bounds__(kWave * pack128_waves<G>()) void pack128_kernel(
     const T* __restrict__ keys, int64_t head_stride, int64_t tokens, int tg,
@@ -230,8 +230,8 @@ hipError_t launch_pack_t(const T* keys, int64_t kvh, int64_t tokens, int d, int6
                       ((head_stride * static_cast<int64_t>(sizeof(T))) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(ks) % 16 == 0) && (reinterpret_cast<uintptr_t>(km) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(kl) % 16 == 0) && (reinterpret_cast<uintptr_t>(kd) % 16 == 0);
-    constexpr bool kStageable = G == 64 && sizeof(T) == 2;
-    if (fast && kStageable && tg <= 64)
+    constexpr bool kStageable = sizeof(T) == 2;
+    if (fast && kStageable && tg <= (G == 64 ? 64 : 128))
         hipLaunchKernelGGL((pack128_kernel<T, G, false, kStageable>), grid, dim3(kWave * pack128_waves<G>()), 0,
                            stream, keys, head_stride, tokens, tg, ks, km, kl, kd, cap, off, AppendArgs<T>{});
     else if (fast)

@@ -99,16 +99,18 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
                                               int32_t* __restrict__ k_sign, int32_t* __restrict__ k_mag,
                                               uint16_t* __restrict__ k_low, uint16_t* __restrict__ k_delta) {
     constexpr int D = 128, R = D / G, CH = G > 32 ? G : 32, NW = D / CH, PH1 = 16;
-    static_assert(!STAGE || (!WIDE && sizeof(T) == 2 && G == 64), "the staged form: 16-bit rows, G64");
-    // STAGE (n <= 64): phase 1 also keeps the group's rows in LDS, at SROW
-    // bytes per row (16 more than a row, so that phase 2's lanes, a row each,
-    // reading 16 bytes at one offset spread over all banks), and phase 2
-    // reads them there instead of from memory.
+    static_assert(!STAGE || (!WIDE && sizeof(T) == 2), "the staged form: 16-bit rows");
+    // STAGE (n <= SCAP: 64 rows at G64, 128 at G32 / G16): phase 1 also
+    // keeps the group's rows in LDS, at SROW bytes per row (16 more than a
+    // row, so that phase 2's lanes, a row each, reading 16 bytes at one
+    // offset spread over all banks), and phase 2 reads them there instead
+    // of from memory.
     constexpr int SROW = D * static_cast<int>(sizeof(T)) + 16;
+    constexpr int SCAP = G == 64 ? 64 : 128;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     __shared__ __align__(16) float s_hi[D], s_lo[D];  // 0.5*max and 0.5*min, read in vectors
-    __shared__ __align__(16) uint8_t s_rows[STAGE ? 64 * SROW : 16];
+    __shared__ __align__(16) uint8_t s_rows[STAGE ? SCAP * SROW : 16];
     if constexpr (!WIDE) {
         // Phase 1: lane l reads dims d8 .. d8+7 (16 bytes) of row slot
         // l / 16, so one load covers four rows; in each pass of 64 rows wave
@@ -129,10 +131,12 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
 #pragma unroll
                 for (int k = 0; k < QW; ++k) raw[k].load(row_of(min(r0 + 4 * (wave + NW * k) + sub, n - 1)) + d8);
             }
-            if constexpr (STAGE) {  // one pass (n <= 64): row slot 4*(wave + NW*k) + sub
+            if constexpr (STAGE) {  // row slot r0 + 4*(wave + NW*k) + sub (n <= SCAP)
+                if (r0 < SCAP) {
 #pragma unroll
-                for (int k = 0; k < QW; ++k)
-                    *reinterpret_cast<uint4*>(s_rows + (4 * (wave + NW * k) + sub) * SROW + d8 * 2) = raw[k].u;
+                    for (int k = 0; k < QW; ++k)
+                        *reinterpret_cast<uint4*>(s_rows + (r0 + 4 * (wave + NW * k) + sub) * SROW + d8 * 2) = raw[k].u;
+                }
             }
 #pragma unroll
             for (int k = 0; k < QW; ++k) {
@@ -285,7 +289,9 @@ __device__ __forceinline__ void pack128_group(const RowOf& row_of, int n, int64_
         return;
     }
     for (int t = lane; t < n; t += kWave) {
-        const T* row = row_of(t) + c0;
+        const T* row;
+        if constexpr (STAGE) row = reinterpret_cast<const T*>(s_rows + t * SROW) + c0;
+        else row = row_of(t) + c0;
         const int64_t orow = orow0 + t;
         constexpr int NWD = CH / 32, NR = CH / G;
         uint32_t sw[NWD], mw[NWD];

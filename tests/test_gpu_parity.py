@@ -149,25 +149,28 @@ def test_pack_edge_values_bit_exact(tg, g, dtype):
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
-@pytest.mark.parametrize("tg", (8, 16, 32, 64))
-def test_pack_staged_groups_bit_exact(tg, dtype):
-    """The G64 encode that keeps each group's rows in LDS (16-bit keys,
-    token groups of at most 64), through the C-ABI: every fill level of the
-    last group, keys at a head stride wider than their rows, packed rows
-    written at an offset; rows outside the written range keep their fill."""
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("tg", (8, 16, 32, 64, 128))
+def test_pack_staged_groups_bit_exact(tg, g, dtype):
+    """The encode that keeps each group's rows in LDS (16-bit keys, token
+    groups of at most 64 at G64 and 128 at G32 / G16; G64 at TG 128 takes
+    the unstaged form), through the C-ABI: every fill level of the last
+    group, keys at a head stride wider than their rows, packed rows written
+    at an offset; rows outside the written range keep their fill."""
+    r = 128 // g
     for n_last in (1, tg // 2 + 1, tg):
         tokens, offset = 2 * tg + n_last, 3
-        buf = _special_keys(dtype, 3, tokens + 5, seed=tg + n_last)
+        buf = _special_keys(dtype, 3, tokens + 5, seed=tg + n_last + g)
         keys = buf[:, :tokens]  # head stride (tokens + 5) rows
         cap = tokens + offset + 2
         planes = (torch.full((3, cap, 4), -7, dtype=torch.int32, device=DEV),
                   torch.full((3, cap, 4), -7, dtype=torch.int32, device=DEV),
-                  torch.full((3, cap, 2), 1.5, dtype=torch.float16, device=DEV),
-                  torch.full((3, cap, 2), 1.5, dtype=torch.float16, device=DEV))
+                  torch.full((3, cap, r), 1.5, dtype=torch.float16, device=DEV),
+                  torch.full((3, cap, r), 1.5, dtype=torch.float16, device=DEV))
         with torch.cuda.device(DEV):
             _native.call("popkv_pack", keys.data_ptr(), _native.dtype_code(keys), 3, tokens, 128, buf.stride(0),
-                         *(t.data_ptr() for t in planes), cap, offset, tg, 64, _native.stream_of(DEV))
-        want = core.pack_keys(f32(keys.contiguous()), token_group_size=tg, dim_group_size=64)
+                         *(t.data_ptr() for t in planes), cap, offset, tg, g, _native.stream_of(DEV))
+        want = core.pack_keys(f32(keys.contiguous()), token_group_size=tg, dim_group_size=g)
         for a, b, fill in zip(planes, want, (-7, -7, 1.5, 1.5)):
             got = bits(a)
             assert np.array_equal(got[:, :offset], bits(torch.full_like(a[:, :offset], fill)))
