@@ -268,6 +268,8 @@ def _scores(kind: str, rows: int, tokens: int, seed: int) -> torch.Tensor:
     elif kind == "nan":
         x = torch.randn(rows, tokens, generator=g)
         x[:, ::37] = float("nan")
+    elif kind == "drift":  # scores rising along the row: tile-local threshold estimates miss
+        x = torch.randn(rows, tokens, generator=g) * 0.5 + torch.linspace(-6.0, 6.0, tokens)
     else:  # peaked fp16 scores, as the scorer produces
         x = torch.randn(rows, tokens, generator=g) * 0.5
         x[:, ::97] += 4.0
@@ -282,6 +284,42 @@ def test_select_matches_oracle(kind, tokens):
         got = topk.select_with_current(s, k, tokens + 1)
         want = core.select(bits(s), k, tokens)
         assert np.array_equal(got.cpu().numpy(), want), (kind, tokens, k)
+
+
+@pytest.mark.parametrize("kind", ["random", "ties", "nan", "peaked", "drift"])
+@pytest.mark.parametrize("rows,tokens,k", [(32, 32767, 4095), (32, 32767, 2731), (32, 24576, 3000),
+                                           (24, 40000, 4500), (16, 65536, 8000), (16, 65536, 4000)])
+def test_select_tile_window_path(kind, rows, tokens, k):
+    """Shapes whose API-select chunks are whole 2048-token tiles (and at
+    most 512 tiles in all), so key_hist_kernel writes tile windows and the
+    select takes its threshold from them (no chunk-histogram launch):
+    chunks of 2048 and 4096 tokens, up to 32 tiles per row, a partial last
+    tile, tiles whose window misses the row's threshold bin (drift), ties,
+    NaN -- index-exact against the oracle."""
+    s = _scores(kind, rows, tokens, seed=tokens + k + len(kind))
+    got = topk.select_with_current(s, k, tokens + 1)
+    assert np.array_equal(got.cpu().numpy(), core.select(bits(s), k, tokens)), (kind, tokens, k)
+
+
+def test_select_tile_window_path_int32_unaligned_rows():
+    """The window path through the C-ABI with int32 indices and score rows
+    at an odd stride (not 16-byte aligned: key_hist's shifted loads), twice
+    on one workspace (its histograms left zero by the first call)."""
+    rows, tokens, k = 32, 32767, 4095
+    buf = _scores("peaked", rows, tokens + 1, seed=77)
+    s = buf[:, :tokens]  # row stride tokens + 1
+    nbytes = int(_native.lib().popkv_topk_select_workspace_bytes(rows, tokens))
+    ws = torch.zeros(nbytes, device=DEV, dtype=torch.uint8)
+    want = core.select(bits(s.contiguous()), k, tokens)
+    for rep in range(2):
+        out = torch.full((rows, k + 2), -7, device=DEV, dtype=torch.int32)
+        with torch.cuda.device(DEV):
+            _native.call("popkv_topk_select", s.data_ptr(), rows, s.stride(0), tokens, k, 999, out.data_ptr(),
+                         _native.INDEX_I32, out.stride(0), ws.data_ptr(), nbytes, _native.stream_of(s.device))
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:, :k], want[:, :k]), rep
+        assert (got[:, k] == 999).all() and (got[:, k + 1] == -7).all()
+    assert int(ws[: rows * 1024].count_nonzero()) == 0
 
 
 @pytest.mark.parametrize("tokens", [65535, 131071, 200000, 524288])
