@@ -496,6 +496,8 @@ def main() -> int:
     attn_gbps = fused_bytes / (attn_step_ms * 1e-3) / 1e9
     # the PMC traffic figure belongs to C1's shape (the workload it was measured on)
     traffic = ATTN_TRAFFIC_BYTES if w.name == workloads.C1.name else None
+    es = q.element_size()
+    distinct_bytes = unique_rows * w.head_dim * es * 2 + w.q_heads * L * 2 + w.q_heads * w.head_dim * es * 2
     result = {
         "metric": METRIC,
         "value": round(ms_per_step * 1e3, 3),
@@ -541,6 +543,10 @@ def main() -> int:
                      # the reference's convention counts every selected (query head, row) once; the heads
                      # of a GQA group share rows, so the kernel's DRAM traffic is lower
                      "algorithmic_convention": "per query head",
+                     # the distinct K/V rows the launch gathers (each once) plus its key rows, q and out,
+                     # over the same time: a bandwidth figure free of the per-head convention
+                     "distinct_bytes_per_launch": distinct_bytes,
+                     "distinct_GBps": round(distinct_bytes / (attn_step_ms * 1e-3) / 1e9, 1),
                      # DRAM bytes per launch (PMC, measured at C1 only) over the same time
                      "traffic_GBps": None if traffic is None else round(traffic / (attn_step_ms * 1e-3) / 1e9, 1),
                      "traffic_frac": None if traffic is None else
