@@ -9,14 +9,17 @@ Llama-3.1-8B shapes: 32 query heads / 8 KV heads, head_dim 128, 32K context,
 budget 4096, bf16 K/V): query encode + popcount score over 32767 cached
 tokens + per-head top-4095 + current token + sparse attention over 2048-token
 chunks with the log-sum-exp merge -- one ``popkv_layer_step`` C-ABI call
-(three kernels), replayed from a HIP graph.  Inputs are resident in HBM; eight
+(one kernel launch at C1: the scorer's workgroups hand their keys and
+histograms to the select + attention workgroups of the same grid),
+replayed from a HIP graph.  Inputs are resident in HBM; eight
 independent K/V + metadata sets (about 1.1 GB) rotate so the 256 MB MALL
 cannot hold the working set.
 
 Prints ONE JSON line: µs per layer step (lower is better), the achieved
-algorithmic HBM GB/s of the step, per-stage kernel times of the layer step
-(HIP events recorded between its kernels), the roofline of the dominant
-kernel (the layer step's select + sparse attention), the achievable
+algorithmic HBM GB/s of the step, the roofline of the dominant kernel (the
+layer step's single launch where the shape takes it, else its select +
+sparse attention kernel), the select + attention kernel timed alone, the
+achievable
 stream-copy bandwidth, and a CPU baseline (the torch-CPU counterpart of the
 reference's readable path on every host thread, a bounded sample of the same
 workload).  Beside them: the prepack of the prefix, the standalone append,
@@ -42,14 +45,16 @@ sys.path.insert(0, str(ROOT))
 METRIC = "µs/layer score+top-k+sparse-attn @32K ctx, B=4096; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 N_BUFFERS = 8
-# HBM bytes per launch of the layer step's select + attention kernel at C1,
-# from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script (KiB per
-# dispatch), each scaled by the same counter on a plain 256 MiB copy
-# (bench.py --copy-calibration): FETCH_SIZE reads 131084.5 KiB for the copy's
-# 262144 KiB (x 1.99981), WRITE_SIZE reads 262144.0 KiB (x 1.0).
-# attn_select_chunk_kernel (the tile-window select): FETCH_SIZE 28848.9 KiB,
-# WRITE_SIZE 275.4 KiB (profiles/layer_step_c1_hbm_traffic.md).
+# HBM bytes per launch at C1, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# runs of this script (KiB per dispatch), each scaled by the same counter on
+# a plain 256 MiB copy (bench.py --copy-calibration): FETCH_SIZE reads
+# 131084.5 KiB for the copy's 262144 KiB (x 1.99981), WRITE_SIZE reads
+# 262144.0 KiB (x 1.0) (profiles/layer_step_c1_hbm_traffic.md).
+# attn_select_chunk_kernel (the tile-window select, run alone by
+# popkv_layer_step_attention): FETCH_SIZE 28848.9 KiB, WRITE_SIZE 275.4 KiB.
 ATTN_TRAFFIC_BYTES = round(28848.9 * 1024 * (262144 / 131084.5) + 275.4 * 1024)
+# layer_step_fused_kernel (the whole C1 step in one launch): not yet measured
+STEP_TRAFFIC_BYTES = None
 
 
 def parse_args():
@@ -311,6 +316,7 @@ def main() -> int:
 
     import torch
 
+    from popkv_amd import _native as nat
     from popkv_amd import popkv, popkv_cuda, sparse_kernels, topk, workloads
 
     if not torch.cuda.is_available():
@@ -490,14 +496,29 @@ def main() -> int:
 
     copy_gbps = stream_copy_gbps(torch, dev, stream)
     step_gbps = alg["step"] / (ms_per_step * 1e-3) / 1e9
-    # the fused select + attention kernel: the attention's bytes plus the
-    # select's final pass over the key rows
-    fused_bytes = alg["attention"] + w.q_heads * L * 2
-    attn_gbps = fused_bytes / (attn_step_ms * 1e-3) / 1e9
-    # the PMC traffic figure belongs to C1's shape (the workload it was measured on)
-    traffic = ATTN_TRAFFIC_BYTES if w.name == workloads.C1.name else None
+    # the select + attention kernel: the attention's bytes plus the select's
+    # pass over the key rows
+    sel_bytes = alg["attention"] + w.q_heads * L * 2
+    sel_gbps = sel_bytes / (attn_step_ms * 1e-3) / 1e9
     es = q.element_size()
-    distinct_bytes = unique_rows * w.head_dim * es * 2 + w.q_heads * L * 2 + w.q_heads * w.head_dim * es * 2
+    sel_distinct = unique_rows * w.head_dim * es * 2 + w.q_heads * L * 2 + w.q_heads * w.head_dim * es * 2
+    # the layer step's launches at this shape: one kernel (scorer and select
+    # + attention workgroups in one grid) where 0 < k < L and the tile-window
+    # form applies; otherwise the select + attention kernel dominates
+    launches = int(nat.lib().popkv_layer_step_launches(w.q_heads, w.kv_heads, L, w.budget, w.dim_group))
+    single = launches == 1 and 0 < kk < L
+    c1 = w.name == workloads.C1.name  # the PMC traffic figures belong to C1's shape
+    if single:
+        # one launch per step: its duration is the graph-replayed step time
+        roof = {"kernel": "layer_step_fused_kernel (the whole layer step: score, select, sparse attention, merge)",
+                "bytes": alg["step"], "us": ms_per_step * 1e3, "traffic": STEP_TRAFFIC_BYTES if c1 else None,
+                "distinct": sel_distinct + alg["score"] + alg["encode"]}
+    else:
+        roof = {"kernel": "attn_select_chunk_kernel (the layer step's select + attention, timed alone)",
+                "bytes": sel_bytes, "us": attn_step_ms * 1e3, "traffic": ATTN_TRAFFIC_BYTES if c1 else None,
+                "distinct": sel_distinct}
+    roof_gbps = roof["bytes"] / (roof["us"] * 1e-6) / 1e9
+    traffic = roof["traffic"]
     result = {
         "metric": METRIC,
         "value": round(ms_per_step * 1e3, 3),
@@ -536,21 +557,28 @@ def main() -> int:
                    "algorithmic_bytes": append_bytes, "GBps": round(append_bytes / (append_ms * 1e-3) / 1e9, 1)},
         "decode_layer_with_append_us": round(decode_ms * 1e3, 3),
         "unique_kv_rows_per_step": unique_rows,
-        "roofline": {"bound": "hbm", "kernel": "attn_select_chunk_kernel (layer step select + attention)",
-                     "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(attn_step_ms * 1e3, 3),
+        "layer_step_launches": launches,
+        "roofline": {"bound": "hbm", "kernel": roof["kernel"],
+                     "achieved": round(roof_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(roof_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": roof["bytes"], "avg_launch_us": round(roof["us"], 3),
                      # the reference's convention counts every selected (query head, row) once; the heads
                      # of a GQA group share rows, so the kernel's DRAM traffic is lower
                      "algorithmic_convention": "per query head",
-                     # the distinct K/V rows the launch gathers (each once) plus its key rows, q and out,
-                     # over the same time: a bandwidth figure free of the per-head convention
-                     "distinct_bytes_per_launch": distinct_bytes,
-                     "distinct_GBps": round(distinct_bytes / (attn_step_ms * 1e-3) / 1e9, 1),
+                     # the distinct K/V rows the launch gathers (each once) plus its other operands, over
+                     # the same time: a bandwidth figure free of the per-head convention
+                     "distinct_bytes_per_launch": roof["distinct"],
+                     "distinct_GBps": round(roof["distinct"] / (roof["us"] * 1e-6) / 1e9, 1),
                      # DRAM bytes per launch (PMC, measured at C1 only) over the same time
-                     "traffic_GBps": None if traffic is None else round(traffic / (attn_step_ms * 1e-3) / 1e9, 1),
+                     "traffic_GBps": None if traffic is None else round(traffic / (roof["us"] * 1e-6) / 1e9, 1),
                      "traffic_frac": None if traffic is None else
-                     round(traffic / (attn_step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
+                     round(traffic / (roof["us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)},
+        # the select + attention kernel alone (popkv_layer_step_attention: re-run on the keys and
+        # thresholds the last step left), the dominant kernel of the multi-launch form
+        "select_attention_alone": {"us": round(attn_step_ms * 1e3, 3), "algorithmic_bytes": sel_bytes,
+                                   "GBps": round(sel_gbps, 1), "frac": round(sel_gbps / HBM_PEAK_GBPS, 4),
+                                   "distinct_GBps": round(sel_distinct / (attn_step_ms * 1e-3) / 1e9, 1),
+                                   "traffic": ATTN_TRAFFIC_BYTES if c1 else None},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -170,6 +170,15 @@ int popkv_sparse_attention_merge(const float* partials, int64_t q_heads, int64_t
  * _append_current, indexed_attention_split_partial and _merge. */
 size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t budget,
                                         int32_t dim_group_size);
+/* The kernel launches popkv_layer_step makes for a shape: 1 when the layer
+ * fits the tile-window form (64-dimension groups, at most 32 scorer tiles of
+ * 1024 tokens, GQA groups of 1, 2, 4 or 8: scorer, select, attention and
+ * merge in one launch) or the budget covers every cached token (select +
+ * attention only), 3 otherwise (scorer, chunk histograms, select +
+ * attention); 0 for an invalid shape.  No counterpart in the reference: a
+ * query for profilers and benchmarks. */
+int popkv_layer_step_launches(int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget,
+                              int32_t dim_group_size);
 int popkv_layer_step(const void* queries, int32_t dtype,
                      const int32_t* k_sign, const int32_t* k_mag,
                      const void* k_low, const void* k_delta, int64_t capacity,

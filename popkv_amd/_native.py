@@ -50,6 +50,7 @@ _SIGNATURES = {
                                                       _c_i64, _c_i32, _vp, _vp]),
     "popkv_sparse_attention_merge": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_i32, _vp]),
     "popkv_layer_step_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i32]),
+    "popkv_layer_step_launches": (_c_i32, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i32]),
     "popkv_layer_step": (ctypes.c_int, [_vp, _c_i32, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp, _vp,
                                         _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _vp, _vp, _vp, _c_size, _vp]),
     "popkv_layer_step_batched_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i32]),

@@ -30,6 +30,7 @@
 #include "device_common.h"
 #include "pack128.h"
 #include "kernels.h"
+#include "score128.h"
 #include "select_common.h"
 
 namespace popkv {
@@ -38,6 +39,10 @@ namespace {
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kAttnStage = 1024;  // indices of one split staged in LDS
+// Polls of the single-launch layer step's select blocks before they give up
+// waiting for the scorer (each poll is a device-coherent load round trip and
+// a short sleep: about 60 ms in all, against a scorer of a few microseconds).
+constexpr int kHandoffPolls = 1 << 16;
 
 template <typename T>
 __device__ __forceinline__ void load_row8(const T* p, int dim0, int d, float v[8]) {
@@ -643,20 +648,32 @@ struct StepAppendArgs {
 // three waves per SIMD it keeps the residency of the plain step: 142 VGPRs
 // at bf16.  Measured at C4: 160.4 us per step with the append in this
 // launch, 167.9 with a separate append launch.)
-template <typename T, int KPT, int NB, bool SEQ, int WJ>
-__global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_kernel(
+//
+// HANDOFF (the layer step's single-launch form, WJ > 0, not SEQ): the
+// scorer's workgroups run in the same launch.  The block first polls its
+// head's histogram row with device-coherent loads until the row sums to
+// ntok (every tile counted: the scorer adds its counts only after its keys,
+// window histograms and records were acknowledged at the coherence point),
+// then reads those with device-coherent loads.  The poll is bounded
+// (kHandoffPolls): the scorer's workgroups come first in the grid and the
+// dispatcher places workgroups in grid order, so they are resident before
+// any select block and never wait; the bound only guarantees that every
+// wave ends.
+template <typename T, int KPT, int NB, bool SEQ, int WJ, bool HANDOFF>
+__device__ __forceinline__ void attn_select_chunk_body(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
     const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
     const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
     uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
     float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq,
     const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out, StepAppendArgs<T> apx,
-    WindowIn win) {
+    WindowIn win, uint32_t block_id) {
     static_assert(kAttnThreads == kChunkThreads, "one key slice per thread");
+    static_assert(!HANDOFF || (WJ > 0 && !SEQ), "the hand-off: the unbatched window path");
     static_assert(WJ == 0 || kAttnWaves == 4, "the window path's tile layout: 4 waves x 2 halves");
     args_in_sgprs(q, kc, vc, k_hs, v_hs, keys, key_stride, ntok, k, rec, h2, gt1, nchunks, qpk,
                   static_cast<int>(kv_groups), head_to_kv, kv_heads);
-    int block = static_cast<int>(blockIdx.x);
+    int block = static_cast<int>(block_id);
     if constexpr (SEQ) {
         // The decode step's append: nothing below reads what it writes (the
         // static caches' rows at the counts -- the select reads the rows
@@ -709,7 +726,8 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     asm volatile("" : "+v"(z));
     const int begin = c * CH + tid * KPT;
     ChunkKeys<KPT> kk;
-    load_chunk_keys_raw<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, max(0, min(KPT, ntok - begin)), kk);
+    if constexpr (!HANDOFF)
+        load_chunk_keys_raw<KPT>(keys + static_cast<int64_t>(h) * key_stride, begin, max(0, min(KPT, ntok - begin)), kk);
     Raw8<T> qr;
     qr.load(q + static_cast<int64_t>(h) * D + dim0);
     const int64_t map = head_to_kv[hl + z];
@@ -749,9 +767,33 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
 #pragma unroll
         for (int j = 0; j < HB; ++j) hv[j] = hr[static_cast<int64_t>(min(j, nchunks - 1)) * 256];
         gx = gt1[static_cast<int64_t>(h) * nchunks + min(lane, nchunks - 1)];
-    } else {
+    } else if constexpr (!HANDOFF) {
         load_rank4(win.hist + static_cast<int64_t>(h) * 256, gcnt);
         wr = win.rec[static_cast<int64_t>(h) * win.tiles + min(wave + 4 * hf + 8 * wp, win.tiles - 1)];
+    } else {
+        // the scorer's hand-off: the row's histogram counts every token once
+        // all of its tiles are out (bins 0 .. 2, which no key reaches, are
+        // left out: bin 0 holds the merge ticket); the counts only grow, so
+        // a read that sums to ntok read every bin's final count.  Then the
+        // chunk's keys and the tile records, written before those counts.
+        if (k > 0 && k < ntok) {
+            const uint4* hrow = reinterpret_cast<const uint4*>(win.hist + static_cast<int64_t>(h) * 256) + (63 - lane);
+            for (int poll = 0;; ++poll) {
+                const uint4 u = ld_coh_u4(hrow);
+                gcnt[0] = u.w;
+                gcnt[1] = u.z;
+                gcnt[2] = u.y;
+                gcnt[3] = u.x;
+                const uint32_t part = lane == kWave - 1 ? u.w : u.x + u.y + u.z + u.w;
+                const uint32_t sum =
+                    static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(part, lane)), kWave - 1));
+                if (sum >= static_cast<uint32_t>(ntok) || poll >= kHandoffPolls) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        load_chunk_keys_raw<KPT, true>(keys + static_cast<int64_t>(h) * key_stride, begin,
+                                       max(0, min(KPT, ntok - begin)), kk);
+        wr = ld_coh_u4(&win.rec[static_cast<int64_t>(h) * win.tiles + min(wave + 4 * hf + 8 * wp, win.tiles - 1)]);
     }
     int nch = nchunks;  // this row's chunks
     if constexpr (SEQ) {
@@ -797,7 +839,7 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
             const bool in_row = i < ntile_row;
             const bool hit = in_row && static_cast<unsigned>(rj) < static_cast<unsigned>(kWinBins);
             miss = miss || (in_row && !hit);
-            wv[j] = wb[hit ? (i * kWinBins + rj) * 32 : 0];
+            wv[j] = ld_u4<HANDOFF>(wb + (hit ? (i * kWinBins + rj) * 32 : 0));
         }
         const int hs = wave * 2 + hf;
         const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
@@ -819,7 +861,8 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
                 uint4 u[QMAX];
 #pragma unroll
                 for (int q = 0; q < QMAX; ++q)
-                    u[q] = *reinterpret_cast<const uint4*>(krow + (8 * q < per && t_first + 8 * q < ntok ? t_first + 8 * q : 0));
+                    u[q] = ld_u4<HANDOFF>(reinterpret_cast<const uint4*>(
+                        krow + (8 * q < per && t_first + 8 * q < ntok ? t_first + 8 * q : 0)));
 #pragma unroll
                 for (int q = 0; q < QMAX; ++q) {
                     const uint32_t wd[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
@@ -1157,6 +1200,54 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
     merge_head<T, true>(partials + static_cast<int64_t>(h) * nchunks * (D + 2), static_cast<int>(parts),
                         q + static_cast<int64_t>(h) * D, cur_k + crow, cur_v + crow, scale,
                         out + static_cast<int64_t>(h) * D);
+}
+
+template <typename T, int KPT, int NB, bool SEQ, int WJ>
+__global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
+    const uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, const uint32_t* __restrict__ rec,
+    const uint16_t* __restrict__ h2, const uint32_t* __restrict__ gt1, int nchunks, int qpk, bool kv_groups,
+    uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int kv_heads, float scale,
+    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, SeqTable seq,
+    const T* __restrict__ cur_k, const T* __restrict__ cur_v, T* __restrict__ out, StepAppendArgs<T> apx,
+    WindowIn win) {
+    attn_select_chunk_body<T, KPT, NB, SEQ, WJ, false>(q, kc, vc, k_hs, v_hs, keys, key_stride, ntok, k, rec, h2, gt1,
+                                                       nchunks, qpk, kv_groups, ghist, head_to_kv, kv_heads, scale,
+                                                       partials, idx_out, idx_stride, seq, cur_k, cur_v, out, apx, win,
+                                                       blockIdx.x);
+}
+
+// The layer step in one launch (the tile-window form): workgroups
+// 0 .. nscore - 1 are the scorer's (tile id mod tiles of KV group
+// id / tiles, 512 threads), the rest the select + attention blocks (block
+// id - nscore, 256 threads: the upper four waves end at once).  The two
+// roles hand off through the scorer's histogram counts (score_d128_body,
+// attn_select_chunk_body with HANDOFF).
+template <typename T, int KPT, int NB, int QPK>
+__global__ __launch_bounds__(kScoreThreads) void layer_step_fused_kernel(
+    const uint4* __restrict__ k_sign, const uint4* __restrict__ k_mag, const uint16_t* __restrict__ k_low,
+    const uint16_t* __restrict__ k_delta, int64_t cap, int nscore, int tiles, TileWindows tw,
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t k_hs, int64_t v_hs,
+    uint16_t* __restrict__ keys, int64_t key_stride, int ntok, int k, int nchunks, int qpk, bool kv_groups,
+    uint32_t* __restrict__ ghist, const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, float scale,
+    float* __restrict__ partials, int64_t* __restrict__ idx_out, int64_t idx_stride, const T* __restrict__ cur_k,
+    const T* __restrict__ cur_v, T* __restrict__ out, WindowIn win) {
+    static_assert(kScoreThreads == 2 * kAttnThreads, "a select block is the lower half of a workgroup");
+    const uint32_t id = blockIdx.x;
+    if (id < static_cast<uint32_t>(nscore)) {
+        const uint32_t grow = id / static_cast<uint32_t>(tiles);
+        score_d128_body<64, QPK, T, true, true>(nullptr, nullptr, nullptr, nullptr, q, k_sign, k_mag, k_low, k_delta,
+                                                head_to_kv, q_heads, kv_heads, QPK, cap, ntok, keys, key_stride, ghist,
+                                                SeqTable{}, tw, id - grow * static_cast<uint32_t>(tiles), grow);
+        return;
+    }
+    // (a wave-uniform test, so the upper waves leave with a scalar branch;
+    // the block's barriers then wait for the lower four alone)
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x) >= static_cast<uint32_t>(kAttnThreads)) return;
+    attn_select_chunk_body<T, KPT, NB, false, kWinMaxTiles / 8, true>(
+        q, kc, vc, k_hs, v_hs, keys, key_stride, ntok, k, nullptr, nullptr, nullptr, nchunks, qpk, kv_groups, ghist,
+        head_to_kv, kv_heads, scale, partials, idx_out, idx_stride, SeqTable{}, cur_k, cur_v, out,
+        StepAppendArgs<T>{}, win, id - static_cast<uint32_t>(nscore));
 }
 
 // Dense attention (the reference's full layers, popkv.py:1022-1038): every
@@ -1828,7 +1919,90 @@ hipError_t launch_merge_current_t(const float* partials, int nsplit, const void*
                            idx_stride, idx_slot, current, seq);
     return hipGetLastError();
 }
+template <typename T>
+hipError_t launch_layer_step_fused_t(const void* queries, const int32_t* k_sign, const int32_t* k_mag,
+                                     const uint16_t* k_low, const uint16_t* k_delta, int64_t capacity,
+                                     const void* prefix_k, const void* prefix_v, int64_t k_hs, int64_t v_hs,
+                                     uint16_t* keys, int64_t key_stride, int64_t tokens, int64_t k,
+                                     const TileWindows& tw, const WindowIn& win, uint32_t* ghist,
+                                     const int64_t* h2k, int q_heads, int kv_heads, float* partials, int64_t* idx_out,
+                                     int64_t idx_stride, const void* cur_k, const void* cur_v, void* out,
+                                     hipStream_t stream) {
+    constexpr int NB = 10;  // as the two-launch form
+    const StepChunks ch = step_chunks(tokens, k, q_heads);
+    const float scale = static_cast<float>(1.0 / sqrt(128.0));
+    const int qpk_all = q_heads / kv_heads;
+    const bool groups = kv_heads % 8 == 0;
+    const int qpk = groups ? qpk_all : 1;
+    const int nscore = tw.tiles * kv_heads;
+    const dim3 grid(static_cast<unsigned>(nscore + ch.count * q_heads));
+    const uint4* ks4 = reinterpret_cast<const uint4*>(k_sign);
+    const uint4* km4 = reinterpret_cast<const uint4*>(k_mag);
+    const T *q_ = static_cast<const T*>(queries), *k_ = static_cast<const T*>(prefix_k),
+            *v_ = static_cast<const T*>(prefix_v);
+    const T *ck_ = static_cast<const T*>(cur_k), *cv_ = static_cast<const T*>(cur_v);
+    T* o_ = static_cast<T*>(out);
+    const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
+#define POPKV_FUSED(KPT, QPK)                                                                                      \
+    hipLaunchKernelGGL((layer_step_fused_kernel<T, KPT, NB, QPK>), grid, dim3(kScoreThreads), 0, stream, ks4, km4,  \
+                       k_low, k_delta, capacity, nscore, tw.tiles, tw, q_, k_, v_, k_hs, v_hs, keys, key_stride, nt,  \
+                       kk, nc, qpk, groups, ghist, h2k, q_heads, kv_heads, scale, partials, idx_out, idx_stride, ck_, \
+                       cv_, o_, win)
+#define POPKV_FUSED_Q(KPT)                              \
+    switch (qpk_all) {                                  \
+        case 1: POPKV_FUSED(KPT, 1); break;             \
+        case 2: POPKV_FUSED(KPT, 2); break;             \
+        case 4: POPKV_FUSED(KPT, 4); break;             \
+        case 8: POPKV_FUSED(KPT, 8); break;             \
+        default: return hipErrorInvalidValue;           \
+    }
+    switch (ch.kpt) {
+        case 4: POPKV_FUSED_Q(4); break;
+        case 8: POPKV_FUSED_Q(8); break;
+        case 16: POPKV_FUSED_Q(16); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef POPKV_FUSED_Q
+#undef POPKV_FUSED
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_layer_step_fused(const void* queries, int dtype, const int32_t* k_sign, const int32_t* k_mag,
+                                   const uint16_t* k_low, const uint16_t* k_delta, int64_t capacity,
+                                   const void* prefix_k, const void* prefix_v, int64_t k_head_stride,
+                                   int64_t v_head_stride, uint16_t* keys, int64_t key_stride, int64_t tokens,
+                                   int64_t k, const TileWindows& tw, const WindowIn& win, uint32_t* ghist,
+                                   const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                   int64_t* idx_out, int64_t idx_stride, const void* current_k,
+                                   const void* current_v, void* output, hipStream_t stream) {
+    // the shapes the window form takes (the caller checks them too)
+    if (tokens <= 0 || k <= 0 || k >= tokens || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads ||
+        tw.tiles <= 0 || tw.tiles > kWinMaxTiles || win.tiles != tw.tiles || win.tile_tokens != 1024 ||
+        (tokens + 1023) / 1024 != tw.tiles || output == nullptr)
+        return hipErrorInvalidValue;
+    const StepChunks ch = step_chunks(tokens, k, q_heads);
+    if (!window_kpt_ok(ch.kpt) || ch.tokens_per_chunk % win.tile_tokens) return hipErrorInvalidValue;
+    switch (dtype) {
+        case POPKV_DTYPE_F32:
+            return launch_layer_step_fused_t<float>(queries, k_sign, k_mag, k_low, k_delta, capacity, prefix_k,
+                                                    prefix_v, k_head_stride, v_head_stride, keys, key_stride, tokens,
+                                                    k, tw, win, ghist, head_to_kv, q_heads, kv_heads, partials,
+                                                    idx_out, idx_stride, current_k, current_v, output, stream);
+        case POPKV_DTYPE_F16:
+            return launch_layer_step_fused_t<f16_t>(queries, k_sign, k_mag, k_low, k_delta, capacity, prefix_k,
+                                                    prefix_v, k_head_stride, v_head_stride, keys, key_stride, tokens,
+                                                    k, tw, win, ghist, head_to_kv, q_heads, kv_heads, partials,
+                                                    idx_out, idx_stride, current_k, current_v, output, stream);
+        default:
+            return launch_layer_step_fused_t<bf16_t>(queries, k_sign, k_mag, k_low, k_delta, capacity, prefix_k,
+                                                     prefix_v, k_head_stride, v_head_stride, keys, key_stride,
+                                                     tokens, k, tw, win, ghist, head_to_kv, q_heads, kv_heads,
+                                                     partials, idx_out, idx_stride, current_k, current_v, output,
+                                                     stream);
+    }
+}
 
 hipError_t launch_attention_select_chunks(const void* queries, int dtype, const void* prefix_k, const void* prefix_v,
                                           int64_t k_head_stride, int64_t v_head_stride, const uint16_t* keys,

@@ -349,6 +349,16 @@ size_t popkv_layer_step_workspace_bytes(int64_t q_heads, int64_t tokens, int64_t
     return step_layout(q_heads, tokens, budget, dim_group_size).total;
 }
 
+int popkv_layer_step_launches(int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t budget,
+                              int32_t dim_group_size) {
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || tokens < 0 || tokens > kMaxSelectTokens ||
+        budget <= 1 || !valid_group(dim_group_size))
+        return 0;
+    const StepLayout L = step_layout(q_heads, tokens, budget, dim_group_size);
+    if (L.k <= 0 || L.k >= tokens) return 1;
+    return L.windows && group_fits_windows(q_heads, kv_heads) ? 1 : 3;
+}
+
 }  // extern "C"
 
 // The layer step on a given workspace.  clear_first: the histogram region is
@@ -403,6 +413,20 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
     if (clear_first) {
         st = launched(popkv::launch_fill_u32(hist, q_heads * 256, 0u, s), "popkv_layer_step(clear histograms)");
         if (st) return st;
+    }
+    // The tile-window form runs in one launch: the scorer's workgroups hand
+    // their keys, windows and histogram counts to the select + attention
+    // blocks of the same grid (launch_layer_step_fused), no kernel boundary
+    // between them.
+    if (windows) {
+        st = launched(popkv::launch_layer_step_fused(
+                          queries, dtype, k_sign, k_mag, static_cast<const uint16_t*>(k_low),
+                          static_cast<const uint16_t*>(k_delta), capacity, prefix_k, prefix_v, k_head_stride,
+                          v_head_stride, keys, L.score_stride, tokens, L.k, tw, wi, hist, head_to_kv,
+                          static_cast<int>(q_heads), static_cast<int>(kv_heads), partials, indices_out, L.k + 1,
+                          current_k, current_v, output, s),
+                      "popkv_layer_step(score + select + attention + merge)");
+        return st;  // (a launch that failed ran nothing: the histograms are still zero)
     }
 
     // 1. query encode + popcount score -> radix order keys of the fp16 scores

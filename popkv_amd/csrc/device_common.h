@@ -278,6 +278,31 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int /*lane*/) {
     return v;
 }
 
+// 16 bytes stored / loaded as two relaxed agent-scope 64-bit atomics: on
+// gfx942 / gfx950 global stores / loads with the sc1 bit, which write
+// through and read past the XCD's non-coherent L2, so data one workgroup
+// hands to another inside a kernel needs no L2 write-back or invalidate
+// (the hand-off's ordering rule is stated where it is used).
+__device__ __forceinline__ void st_coh_u4(uint4* p, uint4 v) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(q, static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint4 ld_coh_u4(const uint4* p) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<uint4*>(p));
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_uint4(static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b),
+                      static_cast<uint32_t>(b >> 32));
+}
+template <bool COH>
+__device__ __forceinline__ uint4 ld_u4(const uint4* p) {
+    if constexpr (COH) return ld_coh_u4(p);
+    else return *p;
+}
+
 // Exclusive prefix sum across a block of `waves` wave64s with a single
 // barrier: DPP scan inside each wave, wave totals through `sh` (`waves`
 // words).  For one use of `sh` per kernel (nothing may still be reading it).

@@ -195,6 +195,20 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const void* current_k, const void* current_v, void* output,
                                           hipStream_t stream, const DecodeAppend* append = nullptr,
                                           const WindowIn* win = nullptr);
+// The layer step's tile-window form in one launch (G64 scorer with the tile
+// windows, then the select + attention blocks with the fused merge; 0 < k <
+// tokens, at most kWinMaxTiles 1024-token tiles, window_kpt_ok chunks of
+// whole tiles, GQA groups of 1, 2, 4 or 8): the operands of
+// launch_score_d128_raw and launch_attention_select_chunks together.  ghist
+// must hold zeros on entry and does again on exit.
+hipError_t launch_layer_step_fused(const void* queries, int dtype, const int32_t* k_sign, const int32_t* k_mag,
+                                   const uint16_t* k_low, const uint16_t* k_delta, int64_t capacity,
+                                   const void* prefix_k, const void* prefix_v, int64_t k_head_stride,
+                                   int64_t v_head_stride, uint16_t* keys, int64_t key_stride, int64_t tokens,
+                                   int64_t k, const TileWindows& tw, const WindowIn& win, uint32_t* ghist,
+                                   const int64_t* head_to_kv, int q_heads, int kv_heads, float* partials,
+                                   int64_t* idx_out, int64_t idx_stride, const void* current_k,
+                                   const void* current_v, void* output, hipStream_t stream);
 // Dense attention over every prefix token (head_dim 128, contiguous rows):
 // partials[h][s][130] for dense_splits(tokens) splits of 512 tokens.
 // Query head h reads KV head h / (QH / KVH) (group sizes 1, 2, 4, 8); one

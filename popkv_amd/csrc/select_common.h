@@ -36,14 +36,17 @@ template <int KPT> struct ChunkKeys {
 // row's first keys and is zeroed.  load_chunk_keys_raw issues the loads for
 // the first n keys (the rest re-read the row's start, unmasked);
 // mask_chunk_keys then zeroes every key at or past n (which may be smaller
-// than the n the loads were issued for).
-template <int KPT>
+// than the n the loads were issued for).  COH: device-coherent loads (keys
+// written by other workgroups of the same launch; KPT a multiple of 4).
+template <int KPT, bool COH = false>
 __device__ __forceinline__ void load_chunk_keys_raw(const uint16_t* __restrict__ row, int begin, int n,
                                                     ChunkKeys<KPT>& k) {
+    static_assert(!COH || KPT % 4 == 0, "device-coherent key loads: 8-byte words");
     if constexpr (KPT % 8 == 0) {
         uint4 u[KPT / 8];
 #pragma unroll
-        for (int c = 0; c < KPT / 8; ++c) u[c] = *reinterpret_cast<const uint4*>(8 * c < n ? row + begin + 8 * c : row);
+        for (int c = 0; c < KPT / 8; ++c)
+            u[c] = ld_u4<COH>(reinterpret_cast<const uint4*>(8 * c < n ? row + begin + 8 * c : row));
 #pragma unroll
         for (int c = 0; c < KPT / 8; ++c) {
             k.w[4 * c] = u[c].x;
@@ -54,7 +57,16 @@ __device__ __forceinline__ void load_chunk_keys_raw(const uint16_t* __restrict__
     } else if constexpr (KPT % 4 == 0) {
         uint2 u[KPT / 4];
 #pragma unroll
-        for (int c = 0; c < KPT / 4; ++c) u[c] = *reinterpret_cast<const uint2*>(4 * c < n ? row + begin + 4 * c : row);
+        for (int c = 0; c < KPT / 4; ++c) {
+            const uint16_t* src = 4 * c < n ? row + begin + 4 * c : row;
+            if constexpr (COH) {
+                const uint64_t x = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<uint16_t*>(src)),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                u[c] = make_uint2(static_cast<uint32_t>(x), static_cast<uint32_t>(x >> 32));
+            } else {
+                u[c] = *reinterpret_cast<const uint2*>(src);
+            }
+        }
 #pragma unroll
         for (int c = 0; c < KPT / 4; ++c) {
             k.w[2 * c] = u[c].x;

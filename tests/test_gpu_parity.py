@@ -716,6 +716,27 @@ def test_layer_step_workspace_reused_across_head_counts():
         np.testing.assert_allclose(f32(o), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
 
 
+def test_layer_step_back_to_back_on_one_workspace():
+    """Steps of different layers queued back to back on one workspace, with
+    no host synchronization between them (the single-launch window form:
+    each step's select blocks read what its own scorer blocks wrote in the
+    same launch, never the previous step's keys, windows or histogram), the
+    last at another shape: each gives the oracle's indices and output."""
+    ws = popkv.LayerStepWorkspace()
+    cases = []
+    for context, budget, seed in ((32767, 4096, 31), (32767, 4096, 32), (8192, 1024, 33), (32767, 4096, 34)):
+        w = workloads.scaled(workloads.C1, context=context, budget=budget)
+        layer, mapping, cache = _layer_setup(w, seed=seed)
+        o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                        layer.current_v(), mapping, budget=w.budget, workspace=ws,
+                                        return_indices=True)
+        cases.append((w, layer, mapping, cache, o, got))
+    for w, layer, mapping, cache, o, got in cases:
+        sc, idx, out = _oracle_step(w, layer, mapping, cache)
+        assert np.array_equal(got.cpu().numpy(), idx), w.context
+        np.testing.assert_allclose(f32(o), out, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
 @pytest.mark.parametrize("tokens", [1000, 4095, 32767])
 def test_select_int32_output_through_the_c_abi(tokens):
     """popkv_topk_select with int32 indices (row stride k + 3): the same

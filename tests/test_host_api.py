@@ -349,6 +349,16 @@ def test_library_host_only_entry_points():
     assert lib.popkv_status_string(-2).decode() == "Pop-KV cache capacity exceeded"
     assert lib.popkv_layer_step_workspace_bytes(32, 32767, 4096, 64) > 32 * 32767 * 2
     assert lib.popkv_layer_step_workspace_bytes(32, 32767, 1, 64) == 0
+    # the layer step's launches: one at C1 and C3 up to 32K (the tile-window
+    # form), one when the budget covers the context (select + attention
+    # only), three past 32 tiles, for 16-dimension groups and GQA groups of 3
+    launches = lib.popkv_layer_step_launches
+    assert launches(32, 8, 32767, 4096, 64) == 1 and launches(32, 8, 16383, 4096, 64) == 1
+    assert launches(32, 8, 4095, 4096, 64) == 1 and launches(32, 8, 300, 512, 16) == 1
+    assert launches(32, 8, 65535, 4096, 64) == 3 and launches(32, 8, 32767, 4096, 16) == 3
+    assert launches(24, 8, 32767, 4096, 64) == 3
+    assert launches(32, 8, 32767, 1, 64) == 0 and launches(30, 8, 32767, 4096, 64) == 0
+    assert launches(32, 8, 524289, 4096, 64) == 0
     assert lib.popkv_score_workspace_bytes(1, 32, 128, 64) > 0
     # argument errors are reported before anything touches a device
     st = lib.popkv_pack(None, 2, 8, 10, 128, 1280, None, None, None, None, 10, 0, 64, 64, None)
