@@ -823,14 +823,20 @@ __device__ __forceinline__ void attn_select_chunk_body(
     // loads would otherwise queue the scan's behind them.
     int ntile_row = 0, c0t = 0, rrow = 0;
     uint32_t gtb = 0u;  // keys above bin b1 in tiles before this chunk (this lane's share)
-    uint4 wv[WJ > 0 ? WJ : 1];
+    uint2 wv[WJ > 0 ? WJ : 1];  // bins 8 wp .. 8 wp + 7 of a window row (byte counts)
     if constexpr (WJ > 0) {
         const int ts = win.tile_tokens;
         ntile_row = (ntok + ts - 1) / ts;
         c0t = c * (CH / ts);
         if (mode == 2) wave_find_bin(gcnt, static_cast<uint32_t>(k), &b1, &above1);
         rrow = static_cast<int>(b1) - static_cast<int>(wr.x);
-        const uint4* wb = reinterpret_cast<const uint4*>(win.bins) + static_cast<int64_t>(h) * win.tiles * (kWinBins * 32) + wp;
+        if (static_cast<unsigned>(rrow) < static_cast<unsigned>(kWinBins)) {
+            // a bin of more than 255 of the tile's keys may have overflowed
+            // its byte counts: taken from the keys, as a miss
+            const uint32_t tot = (rrow < 2 ? wr.z : wr.w) >> ((rrow & 1) * 16) & 0xffffu;
+            if (tot > 255u) rrow = -1;
+        }
+        const uint2* wb = reinterpret_cast<const uint2*>(win.bins) + static_cast<int64_t>(h) * win.tiles * (kWinBins * 32) + wp;
         bool miss = false;
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
@@ -839,7 +845,7 @@ __device__ __forceinline__ void attn_select_chunk_body(
             const bool in_row = i < ntile_row;
             const bool hit = in_row && static_cast<unsigned>(rj) < static_cast<unsigned>(kWinBins);
             miss = miss || (in_row && !hit);
-            wv[j] = ld_u4<HANDOFF>(wb + (hit ? (i * kWinBins + rj) * 32 : 0));
+            wv[j] = ld_u2<HANDOFF>(wb + (hit ? (i * kWinBins + rj) * 32 : 0));
         }
         const int hs = wave * 2 + hf;
         const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
@@ -1024,9 +1030,14 @@ __device__ __forceinline__ void attn_select_chunk_body(
                 const int i = wave + 4 * hf + 8 * j;
                 const int rj = __shfl(rrow, hf * 32 + j);
                 if (i < ntile_row && static_cast<unsigned>(rj) < static_cast<unsigned>(kWinBins)) {
-                    gs.x += wv[j].x; gs.y += wv[j].y; gs.z += wv[j].z; gs.w += wv[j].w;
+                    // byte counts of bins 8 wp .. 8 wp + 7 widened to the
+                    // slot's 16-bit pairs (bins 2m, 2m + 1 in word m)
+                    const uint32_t a = wv[j].x, b = wv[j].y;
+                    const uint4 v = make_uint4((a & 0xffu) | ((a << 8) & 0xff0000u), ((a >> 16) & 0xffu) | ((a >> 8) & 0xff0000u),
+                                               (b & 0xffu) | ((b << 8) & 0xff0000u), ((b >> 16) & 0xffu) | ((b >> 8) & 0xff0000u));
+                    gs.x += v.x; gs.y += v.y; gs.z += v.z; gs.w += v.w;
                     if (i < c0t) {
-                        ps.x += wv[j].x; ps.y += wv[j].y; ps.z += wv[j].z; ps.w += wv[j].w;
+                        ps.x += v.x; ps.y += v.y; ps.z += v.z; ps.w += v.w;
                     }
                 }
             }

@@ -63,7 +63,7 @@ struct StepLayout {
 // low-byte histograms | [QH][chunks] u32 chunk counts | [QH][score_stride]
 // u16 order keys | [QH][chunks][130] f32 chunk partials, and for the
 // tile-window select: [QH][256] u32 kept histograms | [QH][tiles] uint4
-// window records | [QH][tiles][kWinBins][128] u32 window histograms.  The
+// window records | [QH][tiles][kWinBins][64] u32 window byte histograms.  The
 // window path applies to 64-dimension groups when 0 < k < tokens, the row
 // has at most kWinMaxTiles scorer tiles and a chunk is a whole number of
 // them.
@@ -88,7 +88,7 @@ StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget, int32_t g) {
     L.partials = off; off = align_up(off + static_cast<size_t>(qh) * nc * (128 + 2) * 4);
     L.keep = off; off = align_up(off + (L.windows ? static_cast<size_t>(qh) * 256 * 4 : 0));
     L.wrec = off; off = align_up(off + static_cast<size_t>(qh) * nt * 16);
-    L.wbins = off; off = align_up(off + static_cast<size_t>(qh) * nt * popkv::kWinBins * 128 * 4);
+    L.wbins = off; off = align_up(off + static_cast<size_t>(qh) * nt * popkv::kWinBins * 64 * 4);
     L.total = off;
     return L;
 }

@@ -302,6 +302,16 @@ __device__ __forceinline__ uint4 ld_u4(const uint4* p) {
     if constexpr (COH) return ld_coh_u4(p);
     else return *p;
 }
+template <bool COH>
+__device__ __forceinline__ uint2 ld_u2(const uint2* p) {
+    if constexpr (COH) {
+        const uint64_t a = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<uint2*>(p)), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        return make_uint2(static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32));
+    } else {
+        return *p;
+    }
+}
 
 // Exclusive prefix sum across a block of `waves` wave64s with a single
 // barrier: DPP scan inside each wave, wave totals through `sh` (`waves`

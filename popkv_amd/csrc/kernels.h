@@ -69,8 +69,10 @@ hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const 
 // of kWinBins bins starting kWinBelow below that estimate and writes
 //   rec:  uint4 {window base bin, keys of the tile above the window,
 //                counts of window bins 0|1 and 2|3 as 16-bit pairs}
-//   bins: [kWinBins][128] uint32: the low-byte histograms of the window's
-//         bins, bins 2m and 2m+1 in the low and high halves of word m.
+//   bins: [kWinBins][64] uint32: the low-byte histograms of the window's
+//         bins as byte counts, bin 4m + e in byte e of word m (a bin whose
+//         tile count exceeds 255 may overflow its bytes: the select takes
+//         that bin from the keys instead).
 // The select kernel then sums one window row per tile (the row's threshold
 // bin) instead of a histogram pass over the keys; a tile whose window misses
 // that bin is histogrammed from its keys there.
@@ -78,12 +80,13 @@ constexpr int kWinBins = 4;
 constexpr int kWinBelow = 2;
 // per row: longer rows take launch_chunk_hist (measured: with 64-tile rows
 // -- C2's 512-token tiles, C4's 64K sequences -- the select blocks' window
-// reads, one 512-byte row per tile, cost more than the kernel they replace)
+// reads, then one 512-byte row per tile, cost more than the kernel they
+// replace)
 constexpr int kWinMaxTiles = 32;
 inline int score_tile_tokens(int dim_group_size) { return dim_group_size == 64 ? 1024 : 512; }
 struct TileWindows {
     uint4* rec = nullptr;    // [rows][tiles]
-    uint32_t* bins = nullptr;  // [rows][tiles][kWinBins][128]
+    uint32_t* bins = nullptr;  // [rows][tiles][kWinBins][64]
     int tiles = 0;           // tiles per row (the scorer's grid.x)
     int k = 0;               // selected tokens of an unbatched step
 };

@@ -224,13 +224,13 @@ static_assert(kScoreThreads * score_tokens_per_thread<64>() == 1024 &&
 // k are selected): wave h estimates row h's threshold bin from the tile's
 // histogram s_hist[h] and writes the window record (COH: as a
 // device-coherent store), then every thread adds its keys that fall in
-// their row's window to the window histograms in LDS (s_win, zero on entry;
-// the caller writes them out).  A row that selects none or every token gets
+// their row's window to the window histograms in LDS (s_win, byte counts,
+// zero on entry; the caller writes them out).  A row that selects none or every token gets
 // base 256 (no window; its select never reads it).  All threads of the
 // block call it, after a barrier that completes s_hist and s_keys.
 template <int QPK, int TILE, bool COH>
 __device__ __forceinline__ void tile_windows(const uint32_t (*s_hist)[256], const uint16_t (*s_keys)[TILE],
-                                             uint32_t (*s_win)[kWinBins][128], uint32_t* s_base,
+                                             uint32_t (*s_win)[kWinBins][64], uint32_t* s_base,
                                              const TileWindows& win, int64_t qrow0, int64_t ntok, int64_t k,
                                              uint32_t tile) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -279,7 +279,7 @@ __device__ __forceinline__ void tile_windows(const uint32_t (*s_hist)[256], cons
         for (int e = 0; e < PER; ++e) {
             const uint32_t key = kv[h][e];
             const uint32_t d = (key >> 8) - bs[h];  // wraps for keys below the window
-            if (d < static_cast<uint32_t>(kWinBins)) atomicAdd(&s_win[h][d][(key & 0xffu) >> 1], 1u << ((key & 1u) * 16));
+            if (d < static_cast<uint32_t>(kWinBins)) atomicAdd(&s_win[h][d][(key & 0xffu) >> 2], 1u << ((key & 3u) * 8));
         }
     }
     __syncthreads();
@@ -382,11 +382,11 @@ __device__ __forceinline__ void score_d128_body(
     // tile windows (layer step, compile-time group size; a separate
     // instantiation, so the plain scorer keeps its register count -- 79
     // VGPRs at G64, three workgroups per CU at C4 instead of two): every key
-    // of the tile, and the windows' low-byte histograms (16-bit pairs)
+    // of the tile, and the windows' low-byte histograms (byte counts)
     constexpr bool WINK = WIN && STEP && QPK > 0;
     constexpr int TILE = kScoreThreads * TPT;
     __shared__ uint16_t s_keys[WINK ? QPK : 1][WINK ? TILE : 2];
-    __shared__ uint32_t s_win[WINK ? QPK : 1][kWinBins][128];
+    __shared__ uint32_t s_win[WINK ? QPK : 1][kWinBins][64];
     __shared__ uint32_t s_base[WINK ? QPK : 1];
     const bool win_on = WINK && win.rec != nullptr;
     if constexpr (STEP) {
@@ -396,7 +396,7 @@ __device__ __forceinline__ void score_d128_body(
         if (win_on) {
             for (int i = threadIdx.x; i < QPK * TILE / 2; i += kScoreThreads)
                 reinterpret_cast<uint32_t*>(&s_keys[0][0])[i] = 0u;
-            for (int i = threadIdx.x; i < QPK * kWinBins * 128; i += kScoreThreads) (&s_win[0][0][0])[i] = 0u;
+            for (int i = threadIdx.x; i < QPK * kWinBins * 64; i += kScoreThreads) (&s_win[0][0][0])[i] = 0u;
         }
     }
     if constexpr (std::is_void_v<QT>) {
@@ -522,10 +522,10 @@ __device__ __forceinline__ void score_d128_body(
             }
         };
         auto store_windows = [&]() {
-            for (int i = threadIdx.x; i < QPK * kWinBins * 32; i += kScoreThreads) {
-                const int h = i / (kWinBins * 32), r = i - h * (kWinBins * 32);
+            for (int i = threadIdx.x; i < QPK * kWinBins * 16; i += kScoreThreads) {
+                const int h = i / (kWinBins * 16), r = i - h * (kWinBins * 16);
                 const uint4 v = reinterpret_cast<const uint4*>(&s_win[h][0][0])[r];
-                uint4* dst = reinterpret_cast<uint4*>(win.bins + ((qrow0 + h) * win.tiles + tile) * (kWinBins * 128)) + r;
+                uint4* dst = reinterpret_cast<uint4*>(win.bins + ((qrow0 + h) * win.tiles + tile) * (kWinBins * 64)) + r;
                 if constexpr (HANDOFF) st_coh_u4(dst, v);
                 else *dst = v;
             }

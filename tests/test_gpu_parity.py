@@ -507,6 +507,27 @@ def test_layer_step_heavy_ties(distinct):
     _check_layer_step(w, layer, mapping, cache)
 
 
+@pytest.mark.parametrize("distinct", [1, 3, 16])
+def test_layer_step_heavy_ties_single_launch(distinct):
+    """The same ties in the single-launch tile-window form (10000 tokens:
+    ten 1024-token tiles, the last one ragged, in chunks of whole tiles):
+    with 1 or 3 distinct rows a tile holds more than 255 keys of the
+    threshold bin, more than its window's byte counts can hold (the tile is
+    histogrammed from its keys), with 16 the byte counts hold them; windows
+    estimated from one tile's keys may miss the row's bin."""
+    w = workloads.scaled(workloads.C1, context=10000, budget=1200)
+    assert _native.lib().popkv_layer_step_launches(w.q_heads, w.kv_heads, w.context, w.budget, w.dim_group) == 1
+    layer = workloads.make_layer(w, seed=6)
+    g = torch.Generator().manual_seed(10 + distinct)
+    pick = torch.randint(0, distinct, (w.context,), generator=g)
+    layer.keys[:, :] = layer.keys[:, :distinct][:, pick]
+    layer = layer.to(DEV)
+    mapping = workloads.head_to_kv(w, DEV)
+    cache = popkv.build_popkv_cache(layer.prefix_k(), group_size=w.token_group, dim_group_size=w.dim_group,
+                                    reserve_tokens=64)
+    _check_layer_step(w, layer, mapping, cache)
+
+
 @pytest.mark.parametrize("context,budget", [(300, 512), (1025, 1025), (64, 2), (2, 2)])
 def test_layer_step_budget_covers_or_exceeds_context(context, budget):
     w = workloads.scaled(workloads.C1, context=context, budget=budget)
