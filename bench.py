@@ -46,15 +46,17 @@ METRIC = "µs/layer score+top-k+sparse-attn @32K ctx, B=4096; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 N_BUFFERS = 8
 # HBM bytes per launch at C1, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# runs of this script (KiB per dispatch), each scaled by the same counter on
-# a plain 256 MiB copy (bench.py --copy-calibration): FETCH_SIZE reads
-# 131084.5 KiB for the copy's 262144 KiB (x 1.99981), WRITE_SIZE reads
-# 262144.0 KiB (x 1.0) (profiles/layer_step_c1_hbm_traffic.md).
-# attn_select_chunk_kernel (the tile-window select, run alone by
-# popkv_layer_step_attention): FETCH_SIZE 28848.9 KiB, WRITE_SIZE 275.4 KiB.
-ATTN_TRAFFIC_BYTES = round(28848.9 * 1024 * (262144 / 131084.5) + 275.4 * 1024)
-# layer_step_fused_kernel (the whole C1 step in one launch): not yet measured
-STEP_TRAFFIC_BYTES = None
+# runs of this script (KiB per dispatch, median), each scaled by the same
+# counter on a plain 256 MiB copy (bench.py --copy-calibration): FETCH_SIZE
+# reads 131083.5 KiB for the copy's 262144 KiB (x 1.99985), WRITE_SIZE
+# reads 262144.0 KiB (x 1.0) (profiles/layer_step_c1_hbm_traffic.md).
+_FETCH_SCALE = 262144 / 131083.5
+# layer_step_fused_kernel (the whole C1 step in one launch): FETCH_SIZE
+# 34178.8 KiB, WRITE_SIZE 5007.0 KiB
+STEP_TRAFFIC_BYTES = round(34178.84 * 1024 * _FETCH_SCALE + 5007.03 * 1024)
+# attn_select_chunk_kernel (the tile-window select + attention, run alone
+# by popkv_layer_step_attention): FETCH_SIZE 28696.9 KiB, WRITE_SIZE 260.0 KiB
+ATTN_TRAFFIC_BYTES = round(28696.9 * 1024 * _FETCH_SCALE + 260.0 * 1024)
 
 
 def parse_args():

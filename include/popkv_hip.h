@@ -191,10 +191,12 @@ int popkv_layer_step(const void* queries, int32_t dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Batched decode step of one sparse layer over B independent sequences of
- * different lengths, head_dim 128, in one call (the same three kernels as
- * popkv_layer_step, every row at its own sequence's shape; with
- * budget - 1 >= max_tokens every sequence selects all its cached tokens and
- * only the select + attention kernel runs).  Layouts, all
+ * different lengths, head_dim 128, in one call (popkv_layer_step's scorer
+ * and select + attention as launches of their own -- with the chunk
+ * histograms between them where popkv_layer_step takes three launches --
+ * every row at its own sequence's shape; with budget - 1 >= max_tokens
+ * every sequence selects all its cached tokens and only the select +
+ * attention kernel runs).  Layouts, all
  * contiguous:
  *   queries, output        [B, QH, 128]       (dtype)
  *   k_sign/k_mag           [B, KVH, capacity, 4]    int32
@@ -312,7 +314,9 @@ int popkv_layer_step_noalloc(const void* queries, int32_t dtype,
  * there (the kept key histograms and tile windows, or the chunk
  * histograms) and rewrites the chunk partials, leaving the scorer's
  * histogram region zero, so it can be repeated.  For timing the step's
- * dominant kernel on its own; no counterpart in the reference. */
+ * select + attention half as a launch of its own (where the step is one
+ * launch, the same code without the hand-off); no counterpart in the
+ * reference. */
 int popkv_layer_step_attention(const void* queries, int32_t dtype,
                                const void* prefix_k, const void* prefix_v,
                                int64_t k_head_stride, int64_t v_head_stride,

@@ -613,8 +613,9 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
         wi.tile_tokens = static_cast<int>(L.tile_tokens);
     }
     hipStream_t s = as_stream(stream);
-    // the same three kernels as popkv_layer_step, every row at its own
-    // sequence's token count (see popkv::SeqTable).  With budget - 1 >=
+    // popkv_layer_step's kernels as launches of their own (scorer, chunk
+    // histograms unless the tile windows apply, select + attention), every
+    // row at its own sequence's token count (see popkv::SeqTable).  With budget - 1 >=
     // max_tokens every sequence selects all its cached tokens (its count is
     // at most the bound), so, as in popkv_layer_step, the scorer and the
     // chunk histograms are skipped and every select + attention workgroup

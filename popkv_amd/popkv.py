@@ -8,11 +8,14 @@ static K/V cache append (popkv.py:105-111, :964-972), ``_append_current`` /
 ``_sparse_layer_indices`` (popkv.py:283-291), and the PopKV branch of
 ``LlamaSparseDecoder.decode`` (popkv.py:1076-1115) as ``popkv_retrieval_step``.
 
-``popkv_layer_step`` is the same step as one C-ABI call (three kernels:
-encode + score with per-head key histograms, per-chunk histograms of the
-threshold bin, per-chunk select + sparse attention whose last workgroup per
-head does the log-sum-exp merge with the current token; with k >= tokens
-only the last).
+``popkv_layer_step`` is the same step as one C-ABI call: encode + score
+with per-head key histograms and tile windows, the per-chunk select +
+sparse attention, and the log-sum-exp merge with the current token in each
+head's last workgroup.  Where the tile-window form applies (64-dimension
+groups, at most 32 scorer tiles, GQA groups of 1, 2, 4 or 8) that is one
+kernel launch; otherwise three (the scorer, per-chunk histograms of the
+threshold bin, the select + attention); with k >= tokens only the select +
+attention.
 """
 from __future__ import annotations
 
@@ -412,7 +415,7 @@ def popkv_layer_step_attention(q: torch.Tensor, prefix_k: torch.Tensor, prefix_v
     ``popkv_layer_step`` that used ``workspace`` (same shapes, budget and
     dim_group_size); it reads the keys and threshold data the step left
     there and rewrites the chunk partials inside the workspace.  A timing
-    aid for the step's dominant kernel."""
+    aid for the step's select + attention half as a launch of its own."""
     if q.ndim != 2 or int(q.shape[1]) != 128 or not q.is_contiguous():
         raise ValueError("popkv_layer_step_attention requires a contiguous q [query heads, 128]")
     if prefix_k.ndim != 3 or prefix_v.shape != prefix_k.shape or int(prefix_k.shape[2]) != 128:
