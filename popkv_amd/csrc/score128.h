@@ -243,8 +243,13 @@ __device__ __forceinline__ void tile_windows(const uint32_t (*s_hist)[256], cons
             uint32_t cnt[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) cnt[i] = s_hist[wave][255 - (4 * lane + i)];
-            // the tile's share of the selection, ceil(k * n_i / ntok), in [1, n_i]
-            const uint32_t need = static_cast<uint32_t>((k * n_i + ntok - 1) / ntok);
+            // the tile's share of the selection, about k * n_i / ntok, in
+            // [1, n_i] (a single-precision estimate: the window only has to
+            // be centred near the threshold, any centre is correct)
+            const float share = static_cast<float>(k) * static_cast<float>(n_i) *
+                                __builtin_amdgcn_rcpf(static_cast<float>(ntok));
+            const uint32_t need = static_cast<uint32_t>(
+                min(max(__builtin_ceilf(share), 1.0f), static_cast<float>(n_i)));
             uint32_t est, est_above;
             wave_find_bin(cnt, need, &est, &est_above);
             base = min(max(est, static_cast<uint32_t>(kWinBelow + 1)) - kWinBelow, static_cast<uint32_t>(256 - kWinBins));

@@ -180,8 +180,13 @@ __global__ __launch_bounds__(kKeyHistThreads) void key_hist_kernel(const uint16_
                 uint32_t cnt[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) cnt[i] = s_hist[255 - (4 * lane + i)];
-                // the tile's share of the selection, ceil(k * n_i / tokens), in [1, n_i]
-                const uint32_t need = static_cast<uint32_t>((win.k * n_i + tokens - 1) / tokens);
+                // the tile's share of the selection, about k * n_i / tokens,
+                // in [1, n_i] (a single-precision estimate: the window only
+                // has to be centred near the threshold, any centre is correct)
+                const float share = static_cast<float>(win.k) * static_cast<float>(n_i) *
+                                    __builtin_amdgcn_rcpf(static_cast<float>(tokens));
+                const uint32_t need = static_cast<uint32_t>(
+                    min(max(__builtin_ceilf(share), 1.0f), static_cast<float>(n_i)));
                 uint32_t est, est_above;
                 wave_find_bin(cnt, need, &est, &est_above);
                 base = min(max(est, static_cast<uint32_t>(kWinBelow + 1)) - kWinBelow,
