@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import core
-from popkv_amd import popkv, popkv_cuda, topk, workloads
+from popkv_amd import _native, popkv, popkv_cuda, topk, workloads
 
 pytestmark = pytest.mark.gpu
 
@@ -388,6 +388,24 @@ def test_permuted_head_mapping(g):
     assert np.array_equal(got.cpu().numpy(), idx)
     _assert_attention(o, out)
 
+
+
+def test_single_launch_with_more_scorer_workgroups_than_cus():
+    """The single-launch layer step with 128 query heads over 32 KV heads at
+    16K: 512 scorer workgroups (two per CU of the MI355X's 256) ahead of
+    1024 select + attention workgroups in one grid.  The select workgroups
+    are dispatched only after every scorer workgroup, so the later ones
+    still run to their hand-off; indices exact and attention within
+    tolerance against the oracle."""
+    w = workloads.Workload("wide", "popkv-s", 128, 32, 128, 16384, 2048, 64, 64, torch.bfloat16, 4242, True)
+    assert int(_native.lib().popkv_layer_step_launches(w.q_heads, w.kv_heads, w.prefix_tokens, w.budget,
+                                                      w.dim_group)) == 1
+    layer, mapping, cache = _setup(w)
+    sc, idx, out = _oracle(w, layer, mapping, cache)
+    o, got = popkv.popkv_layer_step(layer.queries, cache, layer.prefix_k(), layer.prefix_v(), layer.current_k(),
+                                    layer.current_v(), mapping, budget=w.budget, return_indices=True)
+    assert np.array_equal(got.cpu().numpy(), idx)
+    _assert_attention(o, out)
 
 
 @pytest.mark.parametrize("q_heads,kv_heads,context,budget", [(12, 4, 6000, 700), (24, 8, 7000, 1100),
