@@ -544,6 +544,21 @@ def test_layer_step_dtypes(dtype):
     _check_layer_step(w, layer, mapping, cache)
 
 
+@pytest.mark.parametrize("q_heads,kv_heads,context,budget", [(32, 8, 16384, 4096), (32, 8, 32768, 4096),
+                                                             (64, 16, 32768, 2048)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_layer_step_single_launch_dtypes_and_chunk_plans(dtype, q_heads, kv_heads, context, budget):
+    """The single launch in bf16, fp16 and fp32, with chunks of 1024, 2048
+    and 4096 tokens (4, 8 and 16 keys per select thread), each shape taking
+    the one-launch form."""
+    w = workloads.Workload("single", "popkv-s", q_heads, kv_heads, 128, context, budget, 64, 64, dtype,
+                           11 + q_heads + budget, True)
+    assert int(_native.lib().popkv_layer_step_launches(w.q_heads, w.kv_heads, w.prefix_tokens, w.budget,
+                                                  w.dim_group)) == 1
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
 @pytest.mark.parametrize("context", [65536, 131072])
 def test_layer_step_long_context(context):
     """C3's long contexts: more than 32 key rounds per select thread (keys
