@@ -559,6 +559,19 @@ def test_layer_step_single_launch_dtypes_and_chunk_plans(dtype, q_heads, kv_head
     _check_layer_step(w, layer, mapping, cache)
 
 
+@pytest.mark.parametrize("q_heads,kv_heads", [(32, 32), (64, 32), (64, 8)])
+def test_layer_step_single_launch_gqa_group_sizes(q_heads, kv_heads):
+    """The single launch with GQA groups of 1, 2 and 8 query heads (the
+    scorer's and the select's group-size instantiations besides C1's 4) at
+    16K, budget 4096."""
+    w = workloads.Workload("gqa", "popkv-s", q_heads, kv_heads, 128, 16384, 4096, 64, 64, torch.bfloat16,
+                           q_heads + kv_heads, True)
+    assert int(_native.lib().popkv_layer_step_launches(w.q_heads, w.kv_heads, w.prefix_tokens, w.budget,
+                                                      w.dim_group)) == 1
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
 @pytest.mark.parametrize("context", [65536, 131072])
 def test_layer_step_long_context(context):
     """C3's long contexts: more than 32 key rounds per select thread (keys
