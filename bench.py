@@ -48,15 +48,15 @@ N_BUFFERS = 8
 # HBM bytes per launch at C1, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # runs of this script (KiB per dispatch, median), each scaled by the same
 # counter on a plain 256 MiB copy (bench.py --copy-calibration): FETCH_SIZE
-# reads 131083.5 KiB for the copy's 262144 KiB (x 1.99985), WRITE_SIZE
+# reads 131083.5 KiB for the copy's 262144 KiB (x 1.99982), WRITE_SIZE
 # reads 262144.0 KiB (x 1.0) (profiles/layer_step_c1_hbm_traffic.md).
 _FETCH_SCALE = 262144 / 131083.5
 # layer_step_fused_kernel (the whole C1 step in one launch): FETCH_SIZE
-# 34175.1 KiB, WRITE_SIZE 5007.0 KiB
-STEP_TRAFFIC_BYTES = round(34175.1 * 1024 * _FETCH_SCALE + 5007.0 * 1024)
+# 34179.1 KiB, WRITE_SIZE 5007.0 KiB
+STEP_TRAFFIC_BYTES = round(34179.1 * 1024 * _FETCH_SCALE + 5007.0 * 1024)
 # attn_select_chunk_kernel (the tile-window select + attention, run alone
-# by popkv_layer_step_attention): FETCH_SIZE 28695.8 KiB, WRITE_SIZE 260.0 KiB
-ATTN_TRAFFIC_BYTES = round(28695.8 * 1024 * _FETCH_SCALE + 260.0 * 1024)
+# by popkv_layer_step_attention): FETCH_SIZE 28707.7 KiB, WRITE_SIZE 260.0 KiB
+ATTN_TRAFFIC_BYTES = round(28707.7 * 1024 * _FETCH_SCALE + 260.0 * 1024)
 
 
 def parse_args():

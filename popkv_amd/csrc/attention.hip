@@ -1234,7 +1234,7 @@ __global__ __launch_bounds__(kAttnThreads, SEQ ? 3 : 1) void attn_select_chunk_k
 // id - nscore, 256 threads: the upper four waves end at once).  The two
 // roles hand off through the scorer's histogram counts (score_d128_body,
 // attn_select_chunk_body with HANDOFF).
-template <typename T, int KPT, int NB, int QPK>
+template <typename T, int KPT, int NB, int QPK, int TPT>
 __global__ __launch_bounds__(kScoreThreads) void layer_step_fused_kernel(
     const uint4* __restrict__ k_sign, const uint4* __restrict__ k_mag, const uint16_t* __restrict__ k_low,
     const uint16_t* __restrict__ k_delta, int64_t cap, int nscore, int tiles, TileWindows tw,
@@ -1247,7 +1247,7 @@ __global__ __launch_bounds__(kScoreThreads) void layer_step_fused_kernel(
     const uint32_t id = blockIdx.x;
     if (id < static_cast<uint32_t>(nscore)) {
         const uint32_t grow = id / static_cast<uint32_t>(tiles);
-        score_d128_body<64, QPK, T, true, true>(nullptr, nullptr, nullptr, nullptr, q, k_sign, k_mag, k_low, k_delta,
+        score_d128_body<64, QPK, T, true, true, TPT>(nullptr, nullptr, nullptr, nullptr, q, k_sign, k_mag, k_low, k_delta,
                                                 head_to_kv, q_heads, kv_heads, QPK, cap, ntok, keys, key_stride, ghist,
                                                 SeqTable{}, tw, id - grow * static_cast<uint32_t>(tiles), grow);
         return;
@@ -1954,11 +1954,18 @@ hipError_t launch_layer_step_fused_t(const void* queries, const int32_t* k_sign,
     const T *ck_ = static_cast<const T*>(cur_k), *cv_ = static_cast<const T*>(cur_v);
     T* o_ = static_cast<T*>(out);
     const int nt = static_cast<int>(tokens), kk = static_cast<int>(k), nc = static_cast<int>(ch.count);
-#define POPKV_FUSED(KPT, QPK)                                                                                      \
-    hipLaunchKernelGGL((layer_step_fused_kernel<T, KPT, NB, QPK>), grid, dim3(kScoreThreads), 0, stream, ks4, km4,  \
-                       k_low, k_delta, capacity, nscore, tw.tiles, tw, q_, k_, v_, k_hs, v_hs, keys, key_stride, nt,  \
-                       kk, nc, qpk, groups, ghist, h2k, q_heads, kv_heads, scale, partials, idx_out, idx_stride, ck_, \
-                       cv_, o_, win)
+#define POPKV_FUSED_T(KPT, QPK, TPT)                                                                                \
+    hipLaunchKernelGGL((layer_step_fused_kernel<T, KPT, NB, QPK, TPT>), grid, dim3(kScoreThreads), 0, stream, ks4, \
+                       km4, k_low, k_delta, capacity, nscore, tw.tiles, tw, q_, k_, v_, k_hs, v_hs, keys, key_stride, \
+                       nt, kk, nc, qpk, groups, ghist, h2k, q_heads, kv_heads, scale, partials, idx_out, idx_stride,  \
+                       ck_, cv_, o_, win)
+    // 1024-token tiles (two tokens per scorer thread) or 512 (one)
+    const bool one = win.tile_tokens == kScoreThreads;
+#define POPKV_FUSED(KPT, QPK)             \
+    if (one)                              \
+        POPKV_FUSED_T(KPT, QPK, 1);       \
+    else                                  \
+        POPKV_FUSED_T(KPT, QPK, 2)
 #define POPKV_FUSED_Q(KPT)                              \
     switch (qpk_all) {                                  \
         case 1: POPKV_FUSED(KPT, 1); break;             \
@@ -1975,6 +1982,7 @@ hipError_t launch_layer_step_fused_t(const void* queries, const int32_t* k_sign,
     }
 #undef POPKV_FUSED_Q
 #undef POPKV_FUSED
+#undef POPKV_FUSED_T
     return hipGetLastError();
 }
 
@@ -1990,8 +1998,9 @@ hipError_t launch_layer_step_fused(const void* queries, int dtype, const int32_t
                                    const void* current_v, void* output, hipStream_t stream) {
     // the shapes the window form takes (the caller checks them too)
     if (tokens <= 0 || k <= 0 || k >= tokens || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads ||
-        tw.tiles <= 0 || tw.tiles > kWinMaxTiles || win.tiles != tw.tiles || win.tile_tokens != 1024 ||
-        (tokens + 1023) / 1024 != tw.tiles || output == nullptr)
+        tw.tiles <= 0 || tw.tiles > kWinMaxTiles || win.tiles != tw.tiles ||
+        (win.tile_tokens != 1024 && win.tile_tokens != 512) || tw.tile_tokens != win.tile_tokens ||
+        (tokens + win.tile_tokens - 1) / win.tile_tokens != tw.tiles || output == nullptr)
         return hipErrorInvalidValue;
     const StepChunks ch = step_chunks(tokens, k, q_heads);
     if (!window_kpt_ok(ch.kpt) || ch.tokens_per_chunk % win.tile_tokens) return hipErrorInvalidValue;

@@ -73,7 +73,7 @@ StepLayout step_layout(int64_t qh, int64_t tokens, int64_t budget, int32_t g) {
     L.score_stride = ceil_div(tokens > 0 ? tokens : 1, 128) * 128;
     const popkv::StepChunks ch = popkv::step_chunks(tokens, L.k, qh);
     L.nchunks = ch.count;
-    L.tile_tokens = popkv::score_tile_tokens(g);
+    L.tile_tokens = popkv::step_tile_tokens(g, qh, tokens);
     L.tiles = ceil_div(tokens > 0 ? tokens : 1, L.tile_tokens);
     L.windows = g == 64 && L.k > 0 && L.k < tokens && L.tiles <= popkv::kWinMaxTiles &&
                 popkv::window_kpt_ok(ch.kpt) && ch.tokens_per_chunk % L.tile_tokens == 0;
@@ -402,6 +402,7 @@ static int layer_step_run(const void* queries, int32_t dtype, const int32_t* k_s
         tw.bins = reinterpret_cast<uint32_t*>(ws + L.wbins);
         tw.tiles = static_cast<int>(L.tiles);
         tw.k = static_cast<int>(L.k);
+        tw.tile_tokens = static_cast<int>(L.tile_tokens);
         wi.hist = hist;
         wi.keep = reinterpret_cast<uint32_t*>(ws + L.keep);
         wi.rec = tw.rec;
@@ -605,6 +606,7 @@ static int batched_step_run(const void* queries, int32_t dtype, const int32_t* k
         tw.bins = reinterpret_cast<uint32_t*>(ws + L.wbins);
         tw.tiles = static_cast<int>(L.tiles);
         tw.k = static_cast<int>(L.k);
+        tw.tile_tokens = static_cast<int>(L.tile_tokens);
         wi.hist = hist;
         wi.keep = reinterpret_cast<uint32_t*>(ws + L.keep);
         wi.rec = tw.rec;

@@ -62,7 +62,7 @@ hipError_t launch_score_d128(const int32_t* q_sign, const int32_t* q_mag, const 
 
 // Tile windows of the layer step (the select's threshold without a
 // chunk-histogram pass).  The scorer's workgroup scores one tile of
-// score_tile_tokens(G) tokens of a GQA group's rows; for each (row, tile)
+// step_tile_tokens() tokens of a GQA group's rows; for each (row, tile)
 // it estimates the high-byte bin of the row's k-th largest key from the
 // tile's own histogram (the bin where the tile's count from the top first
 // reaches its share ceil(k * tile tokens / row tokens)), takes the window
@@ -84,11 +84,21 @@ constexpr int kWinBelow = 2;
 // replace)
 constexpr int kWinMaxTiles = 32;
 inline int score_tile_tokens(int dim_group_size) { return dim_group_size == 64 ? 1024 : 512; }
+// The layer step's scorer tile: score_tile_tokens(G), except that rows of
+// 64-dimension groups short enough that their 1024-token tiles would give
+// at most 512 (tile, query row) pairs -- at GQA 4 fewer than half the
+// chip's 256 CUs in scorer workgroups -- take 512-token tiles (one token
+// per thread) and twice the workgroups.
+inline int step_tile_tokens(int dim_group_size, int64_t rows, int64_t tokens) {
+    if (dim_group_size == 64 && (tokens + 1023) / 1024 * rows <= 512) return 512;
+    return score_tile_tokens(dim_group_size);
+}
 struct TileWindows {
     uint4* rec = nullptr;    // [rows][tiles]
     uint32_t* bins = nullptr;  // [rows][tiles][kWinBins][64]
     int tiles = 0;           // tiles per row (the scorer's grid.x)
     int k = 0;               // selected tokens of an unbatched step
+    int tile_tokens = 0;     // tokens per tile: 1024 (two per thread) or 512 (one)
 };
 
 // Layer-step scorer: encodes the raw query rows [batch*QH, 128] in-kernel
@@ -200,7 +210,7 @@ hipError_t launch_attention_select_chunks(const void* queries, int dtype, const 
                                           const WindowIn* win = nullptr);
 // The layer step's tile-window form in one launch (G64 scorer with the tile
 // windows, then the select + attention blocks with the fused merge; 0 < k <
-// tokens, at most kWinMaxTiles 1024-token tiles, window_kpt_ok chunks of
+// tokens, at most kWinMaxTiles tiles of 1024 or 512 tokens (step_tile_tokens), window_kpt_ok chunks of
 // whole tiles, GQA groups of 1, 2, 4 or 8): the operands of
 // launch_score_d128_raw and launch_attention_select_chunks together.  ghist
 // must hold zeros on entry and does again on exit.

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kWave) void query_encode_kernel(
 // ---------------------------------------------------------------- score, D = 128
 
 // grid.x: token tiles of kScoreThreads * score_tokens_per_thread<G>(); grid.y: batch*kv_heads.
-template <int G, int QPK, typename QT, bool WIN>
+template <int G, int QPK, typename QT, bool WIN, int TPT>
 __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
     const float* __restrict__ q_low, const float* __restrict__ q_delta, const QT* __restrict__ q_raw,
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_d128_kernel(
     const int64_t* __restrict__ head_to_kv, int q_heads, int kv_heads, int qpk_rt,
     int64_t cap, int64_t tokens, uint16_t* __restrict__ scores, int64_t out_stride,
     uint32_t* __restrict__ ghist, SeqTable seq, TileWindows win) {
-    score_d128_body<G, QPK, QT, WIN, false>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
+    score_d128_body<G, QPK, QT, WIN, false, TPT>(q_sign, q_mag, q_low, q_delta, q_raw, k_sign, k_mag, k_low, k_delta,
                                             head_to_kv, q_heads, kv_heads, qpk_rt, cap, tokens, scores, out_stride,
                                             ghist, seq, win, blockIdx.x, blockIdx.y);
 }
@@ -232,16 +232,31 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
                                uint16_t* out, int64_t out_stride, uint32_t* ghist, const SeqTable& seq,
                                hipStream_t stream, const TileWindows& win) {
     const int qpk = qh / kvh;
-    const int64_t per_block = static_cast<int64_t>(kScoreThreads) * score_tokens_per_thread<G>();
+    constexpr int TPT = score_tokens_per_thread<G>();
+    const int64_t per_block = static_cast<int64_t>(kScoreThreads) * TPT;
     dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block), static_cast<unsigned>(batch * kvh));
     const uint4* ks4 = reinterpret_cast<const uint4*>(ks);
     const uint4* km4 = reinterpret_cast<const uint4*>(km);
-#define POPKV_SCORE_LAUNCH(Q, W)                                                                              \
-    hipLaunchKernelGGL((score_d128_kernel<G, Q, QT, W>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd,    \
+#define POPKV_SCORE_LAUNCH_T(Q, W, T)                                                                          \
+    hipLaunchKernelGGL((score_d128_kernel<G, Q, QT, W, T>), grid, dim3(kScoreThreads), 0, stream, qs, qm, ql, qd, \
                        q_raw, ks4, km4, kl, kd, h2k, qh, kvh, qpk, cap, tokens, out, out_stride, ghist, seq, win)
+#define POPKV_SCORE_LAUNCH(Q, W) POPKV_SCORE_LAUNCH_T(Q, W, TPT)
     // the tile windows: the layer step's G64 scorer with a compile-time group
     constexpr bool kWinG = G == 64 && !std::is_void_v<QT>;
     if (kWinG && win.rec != nullptr) {
+        // the tiles the layout chose (step_tile_tokens): 1024 or 512 tokens
+        if (win.tile_tokens == kScoreThreads) {
+            grid.x = static_cast<unsigned>((tokens + kScoreThreads - 1) / kScoreThreads);
+            switch (qpk) {
+                case 1: POPKV_SCORE_LAUNCH_T(1, kWinG, 1); break;
+                case 2: POPKV_SCORE_LAUNCH_T(2, kWinG, 1); break;
+                case 4: POPKV_SCORE_LAUNCH_T(4, kWinG, 1); break;
+                case 8: POPKV_SCORE_LAUNCH_T(8, kWinG, 1); break;
+                default: return hipErrorInvalidValue;
+            }
+            return hipGetLastError();
+        }
+        if (win.tile_tokens != per_block) return hipErrorInvalidValue;
         switch (qpk) {
             case 1: POPKV_SCORE_LAUNCH(1, kWinG); break;
             case 2: POPKV_SCORE_LAUNCH(2, kWinG); break;
@@ -251,6 +266,21 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
         }
         return hipGetLastError();
     }
+    if constexpr (TPT == 2) {
+        // fewer two-token workgroups than the chip's 256 CUs (short rows):
+        // one token per thread, twice the workgroups
+        if (static_cast<int64_t>(grid.x) * grid.y < 256) {
+            grid.x = static_cast<unsigned>((tokens + kScoreThreads - 1) / kScoreThreads);
+            switch (qpk) {
+                case 1: POPKV_SCORE_LAUNCH_T(1, false, 1); break;
+                case 2: POPKV_SCORE_LAUNCH_T(2, false, 1); break;
+                case 4: POPKV_SCORE_LAUNCH_T(4, false, 1); break;
+                case 8: POPKV_SCORE_LAUNCH_T(8, false, 1); break;
+                default: POPKV_SCORE_LAUNCH_T(0, false, 1); break;
+            }
+            return hipGetLastError();
+        }
+    }
     switch (qpk) {
         case 1: POPKV_SCORE_LAUNCH(1, false); break;
         case 2: POPKV_SCORE_LAUNCH(2, false); break;
@@ -259,6 +289,7 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
         default: POPKV_SCORE_LAUNCH(0, false); break;
     }
 #undef POPKV_SCORE_LAUNCH
+#undef POPKV_SCORE_LAUNCH_T
     return hipGetLastError();
 }
 

@@ -101,7 +101,10 @@ constexpr int kScoreThreads = 512;  // 8 waves: 1024 tokens x one GQA group per 
 // tokens), one for G32 / G16 (longer per-token work: more waves hide it
 // better).  Measured at 32K tokens: G64 7.4 vs 7.6 us, G32 8.4 vs 8.5 us,
 // G16 11.6 vs 12.4 us (again with the fma-finished count: the C2 layer step
-// 29.1 vs 30.2 us, two tokens taking 160 VGPRs).
+// 29.1 vs 30.2 us, two tokens taking 160 VGPRs).  Short G64 rows, whose
+// two-token tiles would leave CUs without a scorer workgroup, take one token
+// per thread (the launchers' choice): C3 8K step 21.4 vs 20.3 us, C3 16K
+// single launch 23.3 vs 21.3 us.
 template <int G> constexpr int score_tokens_per_thread() { return G == 64 ? 2 : 1; }
 constexpr int kMaxGroupHeads = 64;  // query heads per KV head the LDS stage holds
 
@@ -303,7 +306,7 @@ __device__ __forceinline__ void tile_windows(const uint32_t (*s_hist)[256], cons
 // ghist (device-scope atomics).  A row's histogram therefore sums to its
 // token count only once every tile's other outputs have reached the
 // coherence point; the select polls for that sum.
-template <int G, int QPK, typename QT, bool WIN, bool HANDOFF>
+template <int G, int QPK, typename QT, bool WIN, bool HANDOFF, int TPT = score_tokens_per_thread<G>()>
 __device__ __forceinline__ void score_d128_body(
     const int32_t* __restrict__ q_sign, const int32_t* __restrict__ q_mag,
     const float* __restrict__ q_low, const float* __restrict__ q_delta, const QT* __restrict__ q_raw,
@@ -359,7 +362,7 @@ __device__ __forceinline__ void score_d128_body(
     asm volatile("" : "+v"(z));
     const int64_t map_v = head_to_kv[qh0 + z];
     const int64_t ntok_v = seq.tokens != nullptr ? seq.tokens[b + z] : tokens;
-    constexpr int TPT = score_tokens_per_thread<G>();
+    static_assert(TPT == 1 || TPT == 2, "one or two tokens per thread");
     using RepWord = std::conditional_t<R == 2, uint32_t, std::conditional_t<R == 4, uint2, uint4>>;
     uint4 s4[TPT], m4[TPT];
     RepWord lw[TPT], dw[TPT];

@@ -572,6 +572,22 @@ def test_layer_step_single_launch_gqa_group_sizes(q_heads, kv_heads):
     _check_layer_step(w, layer, mapping, cache)
 
 
+@pytest.mark.parametrize("q_heads,kv_heads,context,budget", [(32, 8, 10001, 2048), (32, 4, 12001, 2048),
+                                                             (32, 8, 9001, 1024)])
+def test_layer_step_single_launch_512_token_tiles(q_heads, kv_heads, context, budget):
+    """Short rows in the single launch: at most 512 (1024-token tile, query
+    row) pairs, so the scorer takes 512-token tiles of one token per thread
+    (twice the workgroups) and the select reads their windows; ragged last
+    tiles, GQA groups of 4 and 8."""
+    w = workloads.Workload("short", "popkv-s", q_heads, kv_heads, 128, context, budget, 64, 64, torch.bfloat16,
+                           context % 97, True)
+    assert int(_native.lib().popkv_layer_step_launches(w.q_heads, w.kv_heads, w.prefix_tokens, w.budget,
+                                                      w.dim_group)) == 1
+    assert -(-w.prefix_tokens // 1024) * w.q_heads <= 512
+    layer, mapping, cache = _layer_setup(w)
+    _check_layer_step(w, layer, mapping, cache)
+
+
 @pytest.mark.parametrize("context", [65536, 131072])
 def test_layer_step_long_context(context):
     """C3's long contexts: more than 32 key rounds per select thread (keys
