@@ -247,6 +247,7 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
         // the tiles the layout chose (step_tile_tokens): 1024 or 512 tokens
         if (win.tile_tokens == kScoreThreads) {
             grid.x = static_cast<unsigned>((tokens + kScoreThreads - 1) / kScoreThreads);
+            if (static_cast<int>(grid.x) != win.tiles) return hipErrorInvalidValue;  // one record per tile
             switch (qpk) {
                 case 1: POPKV_SCORE_LAUNCH_T(1, kWinG, 1); break;
                 case 2: POPKV_SCORE_LAUNCH_T(2, kWinG, 1); break;
@@ -256,7 +257,7 @@ hipError_t launch_score_d128_g(const int32_t* qs, const int32_t* qm, const float
             }
             return hipGetLastError();
         }
-        if (win.tile_tokens != per_block) return hipErrorInvalidValue;
+        if (win.tile_tokens != per_block || static_cast<int>(grid.x) != win.tiles) return hipErrorInvalidValue;
         switch (qpk) {
             case 1: POPKV_SCORE_LAUNCH(1, kWinG); break;
             case 2: POPKV_SCORE_LAUNCH(2, kWinG); break;
